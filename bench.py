@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Benchmark of the MXFP4 MoE expert hot path on one MI355X.
+
+Workload (the metric's "GPT-OSS-120B MXFP4 MoE layer,
+batch 1"): 36 MoE layers x 128 GPT-OSS-120B experts (hidden 2880,
+intermediate 2880, gate/up interleaved, bf16 biases in the .gwt stride layout),
+all resident in HBM (61.2 GB), decode batch 1, top-4 routing from per-layer
+logits ~ N(0,1) that change every token.  One step = one token through the 36
+MoE blocks: route -> fused gate_up + SwiGLU -> fused down + weighted combine,
+each layer's bf16 output feeding the next layer (the trunk between MoE
+blocks is outside the timed path).  Weights are seeded synthetic MXFP4
+(nibbles U{0..15}, scales U{119..127}, biases N(0, 0.02)).
+
+Prints ONE JSON line (the driver's contract).  `value` is whole-job algorithmic
+HBM throughput in GB/s: every selected expert's packed nibbles, scales and bf16
+biases, plus the logits, activations and outputs, per token, divided by the
+wall time per token measured around the timed steps.  The `roofline` object
+covers the dominant kernel (fused gate_up) timed with hipEvents on the
+library's stream; `cpu_baseline` is the CPU oracle (a scalar port of the
+reference's CPU path) on a bounded sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, 8 TB/s
+
+H = F = 2880                # GPT-OSS hidden / intermediate
+E, K, L = 128, 4, 36        # experts, top-k, MoE layers (GPT-OSS-120B)
+METRIC = "HBM GB/s (% of peak) + µs/token, GPT-OSS-120B MXFP4 MoE layer, batch 1"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def expert_bytes(lay) -> int:
+    """Algorithmic bytes of one selected expert: both projections' packed
+    nibbles and scales, and the two bf16 bias vectors."""
+    return sum(lay.sizes[s] for s in lay.sizes)
+
+
+def gate_up_bytes(lay) -> int:
+    """Algorithmic bytes of one gate_up launch (one layer): k experts' gate_up
+    nibbles, scales and bias, the bf16 input read and the fp16 activations written."""
+    per = lay.sizes["gate_up_blocks"] + lay.sizes["gate_up_scales"] + lay.sizes["gate_up_bias"]
+    return K * per + H * 2 + K * F * 2
+
+
+def build_model(ctx, gw, lay, seed: int):
+    """36 layer files of 128 expert strides each, filled on the device."""
+    bufs = []
+    o, sz = lay.offsets, lay.sizes
+    for l in range(L):
+        buf = ctx.empty(lay.layer_file_size)
+        s = seed * 1000003 + l * 7919
+        ctx.fill_uniform_u8(buf, 0, 255, s)                       # every nibble U{0..15}
+        for e in range(E):
+            base = e * lay.stride
+            ctx.fill_uniform_u8(buf, 119, 127, s * 131 + 4 * e + 1,
+                                offset=base + o["gate_up_scales"], count=sz["gate_up_scales"])
+            ctx.fill_uniform_u8(buf, 119, 127, s * 131 + 4 * e + 2,
+                                offset=base + o["down_scales"], count=sz["down_scales"])
+            ctx.fill_normal(buf, gw.BF16, 2 * F, 0.0, 0.02, s * 131 + 4 * e + 3,
+                            offset=base + o["gate_up_bias"])
+            ctx.fill_normal(buf, gw.BF16, H, 0.0, 0.02, s * 131 + 4 * e + 4,
+                            offset=base + o["down_bias"])
+        bufs.append(buf)
+    ctx.synchronize()
+    return bufs
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The oracle (scalar C port of the reference CPU path: referenceMXFP4 + bias,
+    gptoss activation with fp16 rounding, Router.select, sequential combine) on
+    whole tokens of the same workload until `seconds` have elapsed.  Eight
+    distinct synthetic layer weight sets are cycled so no layer's 53 MB stays
+    in the host caches."""
+    import oracle
+    r = np.random.default_rng(77)
+    sets = []
+    for _ in range(8):
+        experts = []
+        for _ in range(K):
+            experts.append(oracle.Expert(
+                r.integers(0, 256, 2 * F * H // 2, dtype=np.uint8),
+                r.integers(119, 128, 2 * F * H // 32, dtype=np.uint8),
+                r.integers(0, 256, H * F // 2, dtype=np.uint8),
+                r.integers(119, 128, H * F // 32, dtype=np.uint8),
+                oracle.round_to_bf16((r.standard_normal(2 * F) * 0.02).astype(np.float32)),
+                oracle.round_to_bf16((r.standard_normal(H) * 0.02).astype(np.float32))))
+        sets.append(experts)
+    x = oracle.round_to_bf16(r.standard_normal(H).astype(np.float32))
+    tokens = 0
+    t0 = time.perf_counter()
+    while True:
+        for l in range(L):
+            logits = r.standard_normal((1, K)).astype(np.float32)   # top-4 of the 4 held
+            out, _, _ = oracle.moe_layer(sets[(tokens * L + l) % 8], K, logits, x, H, F)
+            x = oracle.round_to_bf16(out[0])
+        tokens += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            break
+    return {"tokens": tokens, "seconds": dt, "us_per_token": dt / tokens * 1e6}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="bounded CPU-baseline sample (0 disables it)")
+    ap.add_argument("--no-profile-pass", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this "
+              "build (the MoE decode path runs on a single MI355X; see the sharding note in "
+              "DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import godwit_amd as gw
+
+    ctx = gw.Context(0)
+    lay = gw.ExpertLayout(H, F, E)
+    runner = gw.ExpertRunner(ctx, H, F, "gptOssClampedGLU", 7.0, 1.702)
+    t0 = time.perf_counter()
+    layers = build_model(ctx, gw, lay, args.seed)
+    log(f"resident experts: {L} x {E} x {lay.stride} B = {L * lay.layer_file_size / 1e9:.2f} GB "
+        f"(filled in {time.perf_counter() - t0:.1f}s); {ctx.cu_count} CUs")
+
+    total_steps = args.warmup + args.steps
+    logits_all = ctx.empty(total_steps * L * E * 4)
+    ctx.fill_normal(logits_all, gw.F32, total_steps * L * E, 0.0, 1.0, args.seed * 31 + 7)
+    cur_logits = ctx.empty(L * E * 4)
+    xs = [ctx.empty(H * 2) for _ in range(L + 1)]
+    ctx.fill_normal(xs[0], gw.BF16, H, 0.0, 1.0, args.seed * 31 + 9)
+    outs = [ctx.empty(H * 4) for _ in range(L)]
+    ids = ctx.empty(L * K * 4)
+    ctx.synchronize()
+
+    def token():
+        for l in range(L):
+            runner.layer_forward(layers[l].ptr, lay.stride, E, K, xs[l].ptr, gw.BF16, 1,
+                                 outs[l].ptr, logits=cur_logits.address(l * E * 4),
+                                 out_bf16=xs[l + 1].ptr, routing_ids=ids.address(l * K * 4))
+
+    graph = gw.Graph.capture(ctx, token)
+    step_logits = L * E * 4
+
+    def step(i: int):
+        ctx.copy_async(cur_logits.ptr, logits_all.address(i * step_logits), step_logits)
+        graph.launch()
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i)
+    ctx.synchronize()
+    elapsed = time.perf_counter() - t0
+    s_per_token = elapsed / args.steps
+
+    # routing sanity: the last token's experts are distinct and in range
+    last = ids.download(np.int32, L * K).reshape(L, K)
+    assert np.all((last >= 0) & (last < E)) and all(len(set(r)) == K for r in last)
+
+    bytes_token = L * (K * expert_bytes(lay) + E * 4 + H * 2 + H * 4 + H * 2)
+    value = bytes_token / s_per_token / 1e9
+    log(f"{args.steps} tokens in {elapsed * 1e3:.2f} ms: {s_per_token * 1e6:.1f} us/token, "
+        f"{value:.0f} GB/s ({value / PEAK_HBM_GBS * 100:.1f}% of {PEAK_HBM_GBS:.0f})")
+
+    roofline = None
+    kernels = {}
+    if not args.no_profile_pass:
+        # Same steps again, eagerly, with every launch bracketed by hipEvents.
+        ctx.set_profiling(True)
+        ctx.profile_reset()
+        for i in range(args.steps):
+            ctx.copy_async(cur_logits.ptr, logits_all.address((args.warmup + i) * step_logits),
+                           step_logits)
+            token()
+        ctx.synchronize()
+        for name in ("route", "gate_up", "down"):
+            ms, n = ctx.profile(name)
+            kernels[name] = {"launches": n, "avg_us": ms / max(n, 1) * 1e3}
+        ctx.set_profiling(False)
+        gu_us = kernels["gate_up"]["avg_us"]
+        achieved = gate_up_bytes(lay) / (gu_us * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                    "kernel": "gate_up_kernel (fused MXFP4 gate_up GEMV + bias + SwiGLU)",
+                    "bytes_per_launch": gate_up_bytes(lay), "avg_launch_us": round(gu_us, 3)}
+        log("kernels: " + ", ".join(f"{k} {v['avg_us']:.2f} us x{v['launches']}"
+                                    for k, v in kernels.items()))
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        c = cpu_baseline(args.cpu_seconds)
+        cpu = {"value": round(bytes_token / (c["us_per_token"] * 1e-6) / 1e9, 4), "unit": "GB/s",
+               "us_per_token": round(c["us_per_token"], 1), "cores": 1, "kind": "port",
+               "sample": f"{c['tokens']} token(s) x {L} GPT-OSS-120B-shaped MoE layers (top-4, "
+                         f"2880x2880 experts, 8 distinct synthetic layer weight sets cycled), "
+                         f"scalar C oracle, 1 thread, {c['seconds']:.1f} s",
+               "cpu": platform.processor() or platform.machine()}
+        try:
+            with open("/proc/cpuinfo") as f:
+                for ln in f:
+                    if ln.startswith("model name"):
+                        cpu["cpu"] = ln.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+        log(f"cpu baseline: {c['us_per_token']:.0f} us/token ({cpu['value']:.3f} GB/s)")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(s_per_token * 1e3, 4),
+        "us_per_token": round(s_per_token * 1e6, 2),
+        "hbm_frac_of_peak": round(value / PEAK_HBM_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4",
+        "compute": "e2m1 weights x bf16/fp16 activations, fp32 accumulation",
+        "data": "synthetic (seeded MXFP4 nibbles U{0..15}, scales U{119..127}, "
+                "biases N(0,0.02) bf16, logits N(0,1) per token)",
+        "config": {"workload": "gptoss120b-moe-stack-decode", "model": "GPT-OSS-120B MoE blocks",
+                   "layers": L, "experts": E, "top_k": K, "hidden": H, "intermediate": F,
+                   "global_batch": 1, "seq_len": 1, "parallelism": "single-gpu",
+                   "bytes_per_token": bytes_token, "resident_bytes": L * lay.layer_file_size},
+        "kernels": kernels,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    graph.destroy()
+    runner.close()
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,990 @@
+// gw_api.hip — the C ABI of libgodwit_hip.so (declared in include/godwit_hip.h).
+//
+// Host-side mirror of the reference's engine API: MetalContext ->
+// gw_context, ExpertRunner -> gw_expert_runner, Router -> gw_router_*,
+// TransformerLayer's MoE block -> gw_moe_layer_forward.  Plans (the device
+// form of the demand map) are built here for the host-driven calls and by the
+// route kernel for the device-driven layer call.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/godwit_hip.h"
+#include "gw_launch.h"
+#include "gw_plan.h"
+
+using gw::Plan;
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+
+static thread_local std::string g_error;
+
+static int fail(int code, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+#define GW_HIP(call)                                                                     \
+    do {                                                                                 \
+        hipError_t e_ = (call);                                                          \
+        if (e_ != hipSuccess)                                                            \
+            return fail(e_ == hipErrorOutOfMemory ? GW_ERR_OOM : GW_ERR_HIP, "%s: %s (%s:%d)", \
+                        #call, hipGetErrorString(e_), __FILE__, __LINE__);               \
+    } while (0)
+
+#define GW_CHECK(cond, code, ...) \
+    do {                          \
+        if (!(cond)) return fail(code, __VA_ARGS__); \
+    } while (0)
+
+extern "C" const char *gw_last_error(void) { return g_error.c_str(); }
+extern "C" const char *gw_version(void) { return "godwit_hip 0.1 (gfx950)"; }
+
+static bool dtype_ok(int dt) { return dt == GW_F32 || dt == GW_F16 || dt == GW_BF16; }
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------
+
+struct ProfEvent {
+    const char *name;
+    hipEvent_t start, end;
+};
+
+struct gw_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int cus = 0;
+    int grid_a = 0, grid_b = 0;
+    bool capturing = false;
+    bool profiling = false;
+    std::vector<ProfEvent> events;       // recorded pairs, in order
+    std::vector<hipEvent_t> event_pool;  // reusable events
+    std::vector<std::pair<std::string, std::pair<double, int64_t>>> totals;
+};
+
+static gw::Launch launch_of(gw_context *ctx)
+{
+    gw::Launch L;
+    L.stream = ctx->stream;
+    L.cus = ctx->cus;
+    L.grid_a = ctx->grid_a;
+    L.grid_b = ctx->grid_b;
+    return L;
+}
+
+static hipEvent_t take_event(gw_context *ctx)
+{
+    if (!ctx->event_pool.empty()) {
+        hipEvent_t e = ctx->event_pool.back();
+        ctx->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Brackets one launch with events when profiling (never inside a capture).
+struct ProfScope {
+    gw_context *ctx;
+    const char *name;
+    hipEvent_t start = nullptr;
+    ProfScope(gw_context *c, const char *n) : ctx(c), name(n)
+    {
+        if (ctx->profiling && !ctx->capturing) {
+            start = take_event(ctx);
+            if (start) (void)hipEventRecord(start, ctx->stream);
+        }
+    }
+    ~ProfScope()
+    {
+        if (!start) return;
+        hipEvent_t end = take_event(ctx);
+        if (!end) return;
+        (void)hipEventRecord(end, ctx->stream);
+        ctx->events.push_back({name, start, end});
+    }
+};
+
+static int get_env_int(const char *name, int dflt)
+{
+    const char *v = getenv(name);
+    return v ? atoi(v) : dflt;
+}
+
+extern "C" int gw_device_count(int *count)
+{
+    GW_CHECK(count, GW_ERR_ARG, "count is null");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) n = 0;
+    *count = n;
+    return GW_OK;
+}
+
+extern "C" int gw_context_create(int device, gw_context **out)
+{
+    GW_CHECK(out, GW_ERR_ARG, "out is null");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        return fail(GW_ERR_NO_DEVICE, "no HIP device visible");
+    GW_CHECK(device >= 0 && device < n, GW_ERR_NO_DEVICE, "device %d out of range (%d)", device,
+             n);
+    GW_HIP(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    GW_HIP(hipGetDeviceProperties(&prop, device));
+    gw_context *ctx = new gw_context();
+    ctx->device = device;
+    ctx->cus = prop.multiProcessorCount;
+    ctx->grid_a = get_env_int("GODWIT_GRID_A", 0);
+    ctx->grid_b = get_env_int("GODWIT_GRID_B", 0);
+    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return fail(GW_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
+    }
+    *out = ctx;
+    return GW_OK;
+}
+
+static void release_events(gw_context *ctx)
+{
+    for (auto &p : ctx->events) {
+        ctx->event_pool.push_back(p.start);
+        ctx->event_pool.push_back(p.end);
+    }
+    ctx->events.clear();
+}
+
+extern "C" int gw_context_destroy(gw_context *ctx)
+{
+    if (!ctx) return GW_OK;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    release_events(ctx);
+    for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return GW_OK;
+}
+
+extern "C" int gw_context_synchronize(gw_context *ctx)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    GW_CHECK(!ctx->capturing, GW_ERR_ARG, "synchronize during graph capture");
+    GW_HIP(hipStreamSynchronize(ctx->stream));
+    return GW_OK;
+}
+
+extern "C" void *gw_context_stream(gw_context *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+extern "C" int gw_context_cu_count(gw_context *ctx, int *cus)
+{
+    GW_CHECK(ctx && cus, GW_ERR_ARG, "null argument");
+    *cus = ctx->cus;
+    return GW_OK;
+}
+
+extern "C" int gw_context_set_profiling(gw_context *ctx, int enabled)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    ctx->profiling = enabled != 0;
+    return GW_OK;
+}
+
+static int collect_events(gw_context *ctx)
+{
+    if (ctx->events.empty()) return GW_OK;
+    GW_HIP(hipStreamSynchronize(ctx->stream));
+    for (auto &p : ctx->events) {
+        float ms = 0.0f;
+        GW_HIP(hipEventElapsedTime(&ms, p.start, p.end));
+        bool found = false;
+        for (auto &t : ctx->totals) {
+            if (t.first == p.name) {
+                t.second.first += ms;
+                t.second.second += 1;
+                found = true;
+                break;
+            }
+        }
+        if (!found) ctx->totals.push_back({p.name, {(double)ms, 1}});
+    }
+    release_events(ctx);
+    return GW_OK;
+}
+
+extern "C" int gw_context_profile_read(gw_context *ctx, const char *name, double *total_ms,
+                                       int64_t *launches)
+{
+    GW_CHECK(ctx && name && total_ms && launches, GW_ERR_ARG, "null argument");
+    int rc = collect_events(ctx);
+    if (rc) return rc;
+    *total_ms = 0.0;
+    *launches = 0;
+    for (auto &t : ctx->totals)
+        if (t.first == name) {
+            *total_ms = t.second.first;
+            *launches = t.second.second;
+        }
+    return GW_OK;
+}
+
+extern "C" int gw_context_profile_reset(gw_context *ctx)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    int rc = collect_events(ctx);
+    ctx->totals.clear();
+    return rc;
+}
+
+// ---------------------------------------------------------------------------
+// memory
+// ---------------------------------------------------------------------------
+
+extern "C" int gw_malloc(gw_context *ctx, size_t bytes, void **out)
+{
+    GW_CHECK(ctx && out, GW_ERR_ARG, "null argument");
+    *out = nullptr;
+    if (bytes == 0) return GW_OK;
+    GW_HIP(hipSetDevice(ctx->device));
+    hipError_t e = hipMalloc(out, bytes);
+    if (e != hipSuccess) {
+        *out = nullptr;
+        return fail(e == hipErrorOutOfMemory ? GW_ERR_OOM : GW_ERR_HIP,
+                    "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    }
+    return GW_OK;
+}
+
+extern "C" int gw_free(gw_context *ctx, void *ptr)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    if (!ptr) return GW_OK;
+    GW_HIP(hipFree(ptr));
+    return GW_OK;
+}
+
+static int copy(gw_context *ctx, void *dst, const void *src, size_t n, hipMemcpyKind kind)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    if (n == 0) return GW_OK;
+    GW_CHECK(dst && src, GW_ERR_ARG, "null pointer");
+    GW_CHECK(!ctx->capturing, GW_ERR_ARG, "blocking copy during graph capture");
+    GW_HIP(hipMemcpyAsync(dst, src, n, kind, ctx->stream));
+    GW_HIP(hipStreamSynchronize(ctx->stream));
+    return GW_OK;
+}
+
+extern "C" int gw_memcpy_htod(gw_context *ctx, void *dst, const void *src, size_t bytes)
+{ return copy(ctx, dst, src, bytes, hipMemcpyHostToDevice); }
+extern "C" int gw_memcpy_dtoh(gw_context *ctx, void *dst, const void *src, size_t bytes)
+{ return copy(ctx, dst, src, bytes, hipMemcpyDeviceToHost); }
+extern "C" int gw_memcpy_dtod(gw_context *ctx, void *dst, const void *src, size_t bytes)
+{ return copy(ctx, dst, src, bytes, hipMemcpyDeviceToDevice); }
+
+extern "C" int gw_memcpy_dtod_async(gw_context *ctx, void *dst, const void *src, size_t bytes)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    if (bytes == 0) return GW_OK;
+    GW_CHECK(dst && src, GW_ERR_ARG, "null pointer");
+    GW_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return GW_OK;
+}
+
+extern "C" int gw_memset_zero(gw_context *ctx, void *dst, size_t bytes)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    if (bytes == 0) return GW_OK;
+    GW_CHECK(dst, GW_ERR_ARG, "null pointer");
+    GW_CHECK(!ctx->capturing, GW_ERR_ARG, "memset during graph capture");
+    GW_HIP(hipMemsetAsync(dst, 0, bytes, ctx->stream));
+    GW_HIP(hipStreamSynchronize(ctx->stream));
+    return GW_OK;
+}
+
+extern "C" int gw_fill_uniform_u8(gw_context *ctx, void *dst, size_t count, int lo, int hi,
+                                  uint64_t seed)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    GW_CHECK(count == 0 || dst, GW_ERR_ARG, "null pointer");
+    GW_CHECK(lo >= 0 && hi <= 255 && lo <= hi, GW_ERR_ARG, "bad range [%d, %d]", lo, hi);
+    ProfScope ps(ctx, "fill");
+    GW_HIP(gw::launch_fill_u8(launch_of(ctx), dst, count, lo, hi, seed));
+    return GW_OK;
+}
+
+extern "C" int gw_fill_normal(gw_context *ctx, void *dst, gw_dtype dtype, size_t count,
+                              float mean, float stddev, uint64_t seed)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    GW_CHECK(count == 0 || dst, GW_ERR_ARG, "null pointer");
+    GW_CHECK(dtype_ok(dtype), GW_ERR_ARG, "bad dtype %d", (int)dtype);
+    ProfScope ps(ctx, "fill");
+    GW_HIP(gw::launch_fill_normal(launch_of(ctx), dst, dtype, count, mean, stddev, seed));
+    return GW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// layout (ExpertLayout, InstallLayout.swift:50-92)
+// ---------------------------------------------------------------------------
+
+extern "C" int gw_expert_layout_init(int64_t hidden_size, int64_t intermediate_size,
+                                     int64_t expert_count, gw_expert_layout *out)
+{
+    GW_CHECK(out, GW_ERR_ARG, "out is null");
+    GW_CHECK(hidden_size > 0 && intermediate_size > 0 && expert_count > 0, GW_ERR_ARG,
+             "sizes must be positive");
+    GW_CHECK(hidden_size % 32 == 0 && intermediate_size % 32 == 0, GW_ERR_SHAPE,
+             "hidden (%lld) and intermediate (%lld) must be multiples of 32",
+             (long long)hidden_size, (long long)intermediate_size);
+    const int64_t page = 16384;
+    const int64_t gate_up_rows = 2 * intermediate_size;
+    const int64_t down_rows = hidden_size;
+    const int64_t bpr = hidden_size / 32;
+    int64_t sizes[GW_SECTION_COUNT];
+    sizes[GW_SECTION_GATE_UP_BLOCKS] = gate_up_rows * bpr * 16;
+    sizes[GW_SECTION_GATE_UP_SCALES] = gate_up_rows * bpr;
+    sizes[GW_SECTION_DOWN_BLOCKS] = down_rows * (intermediate_size / 32) * 16;
+    sizes[GW_SECTION_DOWN_SCALES] = down_rows * (intermediate_size / 32);
+    sizes[GW_SECTION_GATE_UP_BIAS] = gate_up_rows * 2;
+    sizes[GW_SECTION_DOWN_BIAS] = down_rows * 2;
+    int64_t cursor = 0;
+    for (int s = 0; s < GW_SECTION_COUNT; ++s) {
+        cursor = (cursor + page - 1) / page * page;
+        out->offsets[s] = cursor;
+        out->sizes[s] = sizes[s];
+        cursor += sizes[s];
+    }
+    out->stride = (cursor + page - 1) / page * page;
+    out->hidden_size = hidden_size;
+    out->intermediate_size = intermediate_size;
+    out->expert_count = expert_count;
+    out->page_size = page;
+    return GW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// kernel-level entry points
+// ---------------------------------------------------------------------------
+
+extern "C" int gw_mxfp4_dequant(gw_context *ctx, const uint8_t *packed, const uint8_t *scales,
+                                int64_t blocks, float *out)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    GW_CHECK(blocks >= 0, GW_ERR_ARG, "negative block count");
+    if (blocks == 0) return GW_OK;
+    GW_CHECK(packed && scales && out, GW_ERR_ARG, "null pointer");
+    GW_CHECK(aligned16(packed) && aligned16(out), GW_ERR_ARG,
+             "packed and out must be 16-byte aligned");
+    ProfScope ps(ctx, "dequant");
+    GW_HIP(gw::launch_dequant(launch_of(ctx), packed, scales, blocks, out));
+    return GW_OK;
+}
+
+static int check_gemv(const uint8_t *packed, const uint8_t *scales, const void *x, int x_dt,
+                      const float *y, int64_t rows, int64_t cols)
+{
+    GW_CHECK(rows >= 0 && cols >= 0, GW_ERR_ARG, "negative shape");
+    GW_CHECK(cols % 32 == 0, GW_ERR_SHAPE, "MXFP4 needs cols to be a multiple of 32 (got %lld)",
+             (long long)cols);
+    GW_CHECK(rows < (1ll << 31) && cols <= 32 * 4096, GW_ERR_SHAPE, "shape too large");
+    GW_CHECK(dtype_ok(x_dt), GW_ERR_ARG, "bad x dtype %d", x_dt);
+    if (rows == 0 || cols == 0) return GW_OK;
+    GW_CHECK(packed && scales && x && y, GW_ERR_ARG, "null pointer");
+    GW_CHECK(aligned16(packed), GW_ERR_ARG, "packed must be 16-byte aligned");
+    GW_CHECK((reinterpret_cast<uintptr_t>(x) & 3u) == 0, GW_ERR_ARG,
+             "x must be 4-byte aligned");
+    return GW_OK;
+}
+
+extern "C" int gw_mxfp4_gemv_bias(gw_context *ctx, const uint8_t *packed, const uint8_t *scales,
+                                  const void *bias, gw_dtype bias_dtype, const void *x,
+                                  gw_dtype x_dtype, float *y, int64_t rows, int64_t cols)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    int rc = check_gemv(packed, scales, x, x_dtype, y, rows, cols);
+    if (rc) return rc;
+    GW_CHECK(!bias || dtype_ok(bias_dtype), GW_ERR_ARG, "bad bias dtype %d", (int)bias_dtype);
+    if (rows == 0) return GW_OK;
+    if (cols == 0) {
+        GW_CHECK(!bias, GW_ERR_UNSUPPORTED, "cols == 0 with bias");
+        GW_HIP(hipMemsetAsync(y, 0, rows * 4, ctx->stream));
+        return GW_OK;
+    }
+    ProfScope ps(ctx, "gemv");
+    GW_HIP(gw::launch_gemv(launch_of(ctx), packed, scales, bias, bias ? (int)bias_dtype : -1, x,
+                           x_dtype, y, (int)rows, (int)cols));
+    return GW_OK;
+}
+
+extern "C" int gw_mxfp4_gemv(gw_context *ctx, const uint8_t *packed, const uint8_t *scales,
+                             const void *x, gw_dtype x_dtype, float *y, int64_t rows,
+                             int64_t cols)
+{
+    return gw_mxfp4_gemv_bias(ctx, packed, scales, nullptr, GW_F32, x, x_dtype, y, rows, cols);
+}
+
+extern "C" int gw_expert_activation(gw_context *ctx, gw_activation kind, const float *gate_up,
+                                    uint16_t *out_f16, int64_t width, float limit, float alpha)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    GW_CHECK(kind == GW_ACT_GPTOSS_CLAMPED_GLU || kind == GW_ACT_SILU, GW_ERR_ARG,
+             "bad activation %d", (int)kind);
+    GW_CHECK(width >= 0, GW_ERR_ARG, "negative width");
+    if (width == 0) return GW_OK;
+    GW_CHECK(gate_up && out_f16, GW_ERR_ARG, "null pointer");
+    ProfScope ps(ctx, "activation");
+    GW_HIP(gw::launch_activation(launch_of(ctx), (int)kind, gate_up, out_f16, width, limit,
+                                 alpha));
+    return GW_OK;
+}
+
+extern "C" int gw_expert_accumulate(gw_context *ctx, const float *expert_out, float *dst,
+                                    float weight, int64_t width)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    GW_CHECK(width >= 0, GW_ERR_ARG, "negative width");
+    if (width == 0) return GW_OK;
+    GW_CHECK(expert_out && dst, GW_ERR_ARG, "null pointer");
+    ProfScope ps(ctx, "accumulate");
+    GW_HIP(gw::launch_accumulate(launch_of(ctx), expert_out, dst, weight, width));
+    return GW_OK;
+}
+
+extern "C" int gw_router_logits(gw_context *ctx, const void *weight, gw_dtype weight_dtype,
+                                const void *bias, gw_dtype bias_dtype, const void *x,
+                                gw_dtype x_dtype, float *logits, int64_t experts,
+                                int64_t hidden, int32_t tokens)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    GW_CHECK(experts >= 0 && hidden >= 0 && tokens >= 0, GW_ERR_ARG, "negative shape");
+    GW_CHECK(dtype_ok(weight_dtype) && dtype_ok(x_dtype) && (!bias || dtype_ok(bias_dtype)),
+             GW_ERR_ARG, "bad dtype");
+    GW_CHECK(experts * tokens < (1ll << 31), GW_ERR_SHAPE, "shape too large");
+    if (experts == 0 || tokens == 0) return GW_OK;
+    GW_CHECK(weight && x && logits, GW_ERR_ARG, "null pointer");
+    ProfScope ps(ctx, "router");
+    GW_HIP(gw::launch_router(launch_of(ctx), weight, weight_dtype, bias,
+                             bias ? (int)bias_dtype : -1, x, x_dtype, logits, (int)experts,
+                             (int)hidden, tokens));
+    return GW_OK;
+}
+
+// Router.select (Router.swift:78-98), host side like the reference.
+extern "C" int gw_router_select(const float *logits, int64_t experts, int64_t top_k,
+                                int32_t *ids, float *weights)
+{
+    GW_CHECK(logits && ids && weights, GW_ERR_ARG, "null pointer");
+    GW_CHECK(top_k >= 1 && top_k <= experts, GW_ERR_SHAPE, "top_k %lld of %lld experts",
+             (long long)top_k, (long long)experts);
+    std::vector<int32_t> order((size_t)experts);
+    for (int64_t i = 0; i < experts; ++i) order[(size_t)i] = (int32_t)i;
+    for (int64_t position = 0; position < top_k; ++position) {
+        int64_t best = position;
+        for (int64_t c = position + 1; c < experts; ++c)
+            if (logits[order[(size_t)c]] > logits[order[(size_t)best]]) best = c;
+        std::swap(order[(size_t)position], order[(size_t)best]);
+    }
+    float peak = 0.0f;
+    for (int64_t i = 0; i < top_k; ++i) {
+        const float v = logits[order[(size_t)i]];
+        if (i == 0 || v > peak) peak = v;
+    }
+    std::vector<float> e((size_t)top_k);
+    float total = 0.0f;
+    for (int64_t i = 0; i < top_k; ++i) {
+        e[(size_t)i] = std::exp(logits[order[(size_t)i]] - peak);
+        total += e[(size_t)i];
+    }
+    for (int64_t i = 0; i < top_k; ++i) {
+        ids[i] = order[(size_t)i];
+        weights[i] = e[(size_t)i] / total;
+    }
+    return GW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// ExpertRunner
+// ---------------------------------------------------------------------------
+
+static constexpr int kPlanRing = 64;
+static constexpr int kMaxExperts = 1024;
+
+struct gw_expert_runner {
+    gw_context *ctx = nullptr;
+    int64_t hidden = 0, inter = 0;
+    int act = 0;
+    float limit = 7.0f, alpha = 1.702f;
+    int bias_dt = GW_BF16;
+    int64_t offsets[GW_SECTION_COUNT] = {};
+    // device scratch
+    Plan *plans = nullptr;           // [kPlanRing] host-built plans
+    Plan *route_plan = nullptr;      // device-built plan of gw_moe_layer_forward
+    uint16_t *act_buf = nullptr;     // [kMaxSlots, inter] fp16 activations
+    float *logits = nullptr;         // [kMaxTokens, kMaxExperts]
+    Plan *staging = nullptr;         // pinned host mirror of `plans`
+    int ring_next = 0;
+    int ring_used = 0;
+};
+
+extern "C" int gw_expert_runner_destroy(gw_expert_runner *r)
+{
+    if (!r) return GW_OK;
+    if (r->ctx) (void)hipStreamSynchronize(r->ctx->stream);
+    (void)hipFree(r->plans);
+    (void)hipFree(r->route_plan);
+    (void)hipFree(r->act_buf);
+    (void)hipFree(r->logits);
+    (void)hipHostFree(r->staging);
+    delete r;
+    return GW_OK;
+}
+
+extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
+                                       int64_t intermediate_size, gw_activation activation,
+                                       float swiglu_limit, float swiglu_alpha,
+                                       gw_expert_runner **out)
+{
+    GW_CHECK(ctx && out, GW_ERR_ARG, "null argument");
+    *out = nullptr;
+    GW_CHECK(activation == GW_ACT_GPTOSS_CLAMPED_GLU || activation == GW_ACT_SILU, GW_ERR_ARG,
+             "bad activation %d", (int)activation);
+    gw_expert_layout layout;
+    int rc = gw_expert_layout_init(hidden_size, intermediate_size, 1, &layout);
+    if (rc) return rc;
+    GW_CHECK(hidden_size <= 32 * 4096 && intermediate_size <= 32 * 4096, GW_ERR_SHAPE,
+             "shape too large");
+    GW_CHECK(gw::gate_up_lds_bytes((int)hidden_size, GW_F32, 1) <= gw::kLdsBudget, GW_ERR_SHAPE,
+             "hidden size %lld too large for the LDS-staged activation", (long long)hidden_size);
+    gw_expert_runner *r = new gw_expert_runner();
+    r->ctx = ctx;
+    r->hidden = hidden_size;
+    r->inter = intermediate_size;
+    r->act = activation;
+    r->limit = swiglu_limit;
+    r->alpha = swiglu_alpha;
+    for (int s = 0; s < GW_SECTION_COUNT; ++s) r->offsets[s] = layout.offsets[s];
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipMalloc((void **)&r->plans, sizeof(Plan) * kPlanRing);
+    if (e == hipSuccess) e = hipMalloc((void **)&r->route_plan, sizeof(Plan));
+    if (e == hipSuccess)
+        e = hipMalloc((void **)&r->act_buf, sizeof(uint16_t) * gw::kMaxSlots * intermediate_size);
+    if (e == hipSuccess)
+        e = hipMalloc((void **)&r->logits, sizeof(float) * gw::kMaxTokens * kMaxExperts);
+    if (e == hipSuccess) e = hipHostMalloc((void **)&r->staging, sizeof(Plan) * kPlanRing);
+    if (e != hipSuccess) {
+        gw_expert_runner_destroy(r);
+        return fail(e == hipErrorOutOfMemory ? GW_ERR_OOM : GW_ERR_HIP, "runner scratch: %s",
+                    hipGetErrorString(e));
+    }
+    *out = r;
+    return GW_OK;
+}
+
+extern "C" int gw_expert_runner_set_bias_dtype(gw_expert_runner *r, gw_dtype bias_dtype)
+{
+    GW_CHECK(r, GW_ERR_ARG, "runner is null");
+    GW_CHECK(bias_dtype == GW_BF16 || bias_dtype == GW_F32, GW_ERR_ARG, "bad bias dtype");
+    r->bias_dt = bias_dtype;
+    return GW_OK;
+}
+
+extern "C" int gw_expert_runner_section_offsets(gw_expert_runner *r,
+                                                int64_t offsets[GW_SECTION_COUNT])
+{
+    GW_CHECK(r && offsets, GW_ERR_ARG, "null argument");
+    for (int s = 0; s < GW_SECTION_COUNT; ++s) offsets[s] = r->offsets[s];
+    return GW_OK;
+}
+
+static gw::Sections sections_of(const int64_t off[GW_SECTION_COUNT])
+{
+    gw::Sections s;
+    s.gu_blocks = off[GW_SECTION_GATE_UP_BLOCKS];
+    s.gu_scales = off[GW_SECTION_GATE_UP_SCALES];
+    s.dn_blocks = off[GW_SECTION_DOWN_BLOCKS];
+    s.dn_scales = off[GW_SECTION_DOWN_SCALES];
+    s.gu_bias = off[GW_SECTION_GATE_UP_BIAS];
+    s.dn_bias = off[GW_SECTION_DOWN_BIAS];
+    return s;
+}
+
+// A host-built plan: expert-major groups over assignments, in order.
+struct HostPlan {
+    Plan p;
+    const gw_expert_weights *group_w[gw::kMaxSlots];
+    int max_group_tokens = 0;
+    void clear()
+    {
+        memset(&p, 0, sizeof(p));
+        max_group_tokens = 0;
+    }
+};
+
+static bool same_weights(const gw_expert_weights *a, const gw_expert_weights *b)
+{
+    if (a->buffer != b->buffer) return false;
+    for (int s = 0; s < GW_SECTION_COUNT; ++s)
+        if (a->offsets[s] != b->offsets[s]) return false;
+    return true;
+}
+
+// Runs one plan: upload, fused gate_up + activation, fused down + combine.
+// All groups of a plan share one set of section offsets (the runner launches
+// a separate plan per distinct offset set).
+static int run_plan(gw_expert_runner *r, HostPlan &hp, const int64_t offsets[GW_SECTION_COUNT],
+                    const void *inputs, int x_dt, float *outputs, int accumulate)
+{
+    gw_context *ctx = r->ctx;
+    // Regroup slots group-major (the kernels' convention): slots were appended
+    // in assignment order; renumber so each group's slots are contiguous.
+    Plan &p = hp.p;
+    Plan q = p;
+    int next = 0;
+    int remap[gw::kMaxSlots];
+    for (int g = 0; g < p.ngroups; ++g) {
+        q.group_slot0[g] = next;
+        int k = 0;
+        for (int s = 0; s < p.nslots; ++s) {
+            if (p.slot_group[s] != g) continue;
+            remap[s] = next;
+            q.slot_token[next] = p.slot_token[s];
+            q.slot_group[next] = g;
+            q.slot_weight[next] = p.slot_weight[s];
+            ++next;
+            ++k;
+        }
+        q.group_ntok[g] = k;
+    }
+    for (int t = 0; t < p.ntokens; ++t)
+        for (int k = 0; k < p.tok_nslots[t]; ++k) q.tok_slots[t][k] = remap[p.tok_slots[t][k]];
+    for (int g = 0; g < p.ngroups; ++g) q.group_base[g] = hp.group_w[g]->buffer;
+
+    if (r->ring_used == kPlanRing) {   // staging slots are reused only after their copies ran
+        GW_HIP(hipStreamSynchronize(ctx->stream));
+        r->ring_used = 0;
+    }
+    const int slot = r->ring_next;
+    r->ring_next = (r->ring_next + 1) % kPlanRing;
+    r->ring_used += 1;
+    r->staging[slot] = q;
+    GW_HIP(hipMemcpyAsync(r->plans + slot, r->staging + slot, sizeof(Plan),
+                          hipMemcpyHostToDevice, ctx->stream));
+    const gw::Sections sec = sections_of(offsets);
+    const gw::Launch L = launch_of(ctx);
+    // The staged inputs bound every group's width, so q.ntokens picks the
+    // kernel width (1, or the 8-wide variant) for both kernels.
+    GW_CHECK(gw::gate_up_lds_bytes((int)r->hidden, x_dt, q.ntokens) <= gw::kLdsBudget,
+             GW_ERR_SHAPE, "%d staged inputs of width %lld exceed the LDS budget", q.ntokens,
+             (long long)r->hidden);
+    {
+        ProfScope ps(ctx, "gate_up");
+        GW_HIP(gw::launch_gate_up(L, r->plans + slot, q.ntokens, inputs, x_dt, (int)r->hidden,
+                                  (int)r->inter, sec, r->bias_dt, r->act_buf, r->act, r->limit,
+                                  r->alpha));
+    }
+    {
+        ProfScope ps(ctx, "down");
+        GW_HIP(gw::launch_down(L, r->plans + slot, q.ntokens, q.nslots, r->act_buf,
+                               (int)r->hidden, (int)r->inter, sec, r->bias_dt, outputs, nullptr,
+                               accumulate));
+    }
+    return GW_OK;
+}
+
+// Adds (weights, token, w) to the plan being built; returns false if it does
+// not fit (the caller flushes and retries on an empty plan).
+static bool plan_add(HostPlan &hp, const gw_expert_weights *w, int32_t token, float weight,
+                     bool merge)
+{
+    Plan &p = hp.p;
+    if (p.nslots >= gw::kMaxSlots) return false;
+    int local = -1;
+    for (int t = 0; t < p.ntokens; ++t)
+        if (p.tok_global[t] == token) local = t;
+    if (local < 0) {
+        if (p.ntokens >= gw::kMaxTokens) return false;
+        local = p.ntokens;
+        p.tok_global[local] = token;
+        p.tok_nslots[local] = 0;
+        p.ntokens += 1;
+    }
+    if (p.tok_nslots[local] >= gw::kMaxTopK) return false;
+    int g = -1;
+    if (merge) {
+        for (int k = 0; k < p.ngroups; ++k) {
+            if (!same_weights(hp.group_w[k], w)) continue;
+            bool has = false;   // a group holds each token at most once
+            for (int s = 0; s < p.nslots; ++s)
+                if (p.slot_group[s] == k && p.slot_token[s] == local) has = true;
+            if (!has) { g = k; break; }
+        }
+    }
+    if (g < 0) {
+        g = p.ngroups++;
+        hp.group_w[g] = w;
+        p.group_ntok[g] = 0;
+    }
+    const int s = p.nslots++;
+    p.slot_token[s] = local;
+    p.slot_group[s] = g;
+    p.slot_weight[s] = weight;
+    p.group_ntok[g] += 1;
+    if (p.group_ntok[g] > hp.max_group_tokens) hp.max_group_tokens = p.group_ntok[g];
+    p.tok_slots[local][p.tok_nslots[local]++] = s;
+    return true;
+}
+
+static bool same_offsets(const gw_expert_weights *a, const gw_expert_weights *b)
+{
+    for (int s = 0; s < GW_SECTION_COUNT; ++s)
+        if (a->offsets[s] != b->offsets[s]) return false;
+    return true;
+}
+
+static int check_weights(gw_expert_runner *r, const gw_expert_weights *w)
+{
+    GW_CHECK(w && w->buffer, GW_ERR_ARG, "null expert weights");
+    GW_CHECK(aligned16(w->buffer), GW_ERR_ARG, "expert buffer must be 16-byte aligned");
+    for (int s = 0; s < 4; ++s)
+        GW_CHECK(w->offsets[s] >= 0 && (w->offsets[s] & 15) == 0, GW_ERR_ARG,
+                 "section %d offset %lld must be non-negative and 16-byte aligned", s,
+                 (long long)w->offsets[s]);
+    const int bias_align = r->bias_dt == GW_F32 ? 4 : 2;
+    for (int s = 4; s < 6; ++s)
+        GW_CHECK(w->offsets[s] >= 0 && (w->offsets[s] % bias_align) == 0, GW_ERR_ARG,
+                 "bias section %d offset misaligned", s);
+    return GW_OK;
+}
+
+// Shared driver of apply / applyBatch / applyAssignments.
+static int run_assignments(gw_expert_runner *r, const void *inputs, int x_dt,
+                           const gw_assignment *a, int32_t n, float *outputs, int accumulate,
+                           bool merge)
+{
+    GW_CHECK(dtype_ok(x_dt), GW_ERR_ARG, "bad x dtype %d", x_dt);
+    GW_CHECK(inputs && outputs, GW_ERR_ARG, "null pointer");
+    GW_CHECK((reinterpret_cast<uintptr_t>(inputs) & 3u) == 0, GW_ERR_ARG,
+             "inputs must be 4-byte aligned");
+    GW_CHECK(!r->ctx->capturing, GW_ERR_ARG, "host-planned calls cannot be captured");
+    for (int32_t i = 0; i < n; ++i) {
+        int rc = check_weights(r, &a[i].weights);
+        if (rc) return rc;
+        GW_CHECK(a[i].token >= 0, GW_ERR_ARG, "negative token index");
+    }
+    HostPlan hp;
+    hp.clear();
+    const gw_expert_weights *plan_offsets = nullptr;
+    int first_run = 1;
+    for (int32_t i = 0; i < n; ++i) {
+        const gw_expert_weights *w = &a[i].weights;
+        const bool fits_offsets = !plan_offsets || same_offsets(plan_offsets, w);
+        if (!fits_offsets || !plan_add(hp, w, a[i].token, a[i].routing_weight, merge)) {
+            int rc = run_plan(r, hp, plan_offsets->offsets, inputs, x_dt, outputs,
+                              accumulate || !first_run);
+            if (rc) return rc;
+            first_run = 0;
+            hp.clear();
+            plan_offsets = nullptr;
+            if (!plan_add(hp, w, a[i].token, a[i].routing_weight, merge))
+                return fail(GW_ERR_SHAPE, "assignment does not fit an empty plan");
+        }
+        if (!plan_offsets) plan_offsets = w;
+    }
+    if (hp.p.nslots > 0) {
+        int rc = run_plan(r, hp, plan_offsets->offsets, inputs, x_dt, outputs,
+                          accumulate || !first_run);
+        if (rc) return rc;
+    }
+    return GW_OK;
+}
+
+extern "C" int gw_expert_apply(gw_expert_runner *r, const void *x, gw_dtype x_dtype,
+                               const gw_expert_weights *weights, float *out)
+{
+    GW_CHECK(r, GW_ERR_ARG, "runner is null");
+    GW_CHECK(weights, GW_ERR_ARG, "weights is null");
+    gw_assignment a;
+    a.weights = *weights;
+    a.token = 0;
+    a.routing_weight = 1.0f;   // combine: 0 + out * 1 == out exactly
+    int rc = run_assignments(r, x, x_dtype, &a, 1, out, 0, false);
+    if (rc) return rc;
+    GW_HIP(hipStreamSynchronize(r->ctx->stream));
+    return GW_OK;
+}
+
+extern "C" int gw_expert_apply_batch(gw_expert_runner *r, const void *x, gw_dtype x_dtype,
+                                     const gw_expert_weights *experts,
+                                     const float *routing_weights, int32_t count, float *out)
+{
+    GW_CHECK(r, GW_ERR_ARG, "runner is null");
+    GW_CHECK(count >= 0, GW_ERR_ARG, "negative count");
+    GW_CHECK(count == 0 || (experts && routing_weights), GW_ERR_ARG, "null pointer");
+    GW_CHECK(out, GW_ERR_ARG, "out is null");
+    if (count == 0) {   // the reference returns zeros (ExpertRunner.swift:195)
+        GW_CHECK(!r->ctx->capturing, GW_ERR_ARG, "cannot capture");
+        GW_HIP(hipMemsetAsync(out, 0, sizeof(float) * r->hidden, r->ctx->stream));
+        GW_HIP(hipStreamSynchronize(r->ctx->stream));
+        return GW_OK;
+    }
+    std::vector<gw_assignment> a((size_t)count);
+    for (int32_t i = 0; i < count; ++i) {
+        a[(size_t)i].weights = experts[i];
+        a[(size_t)i].token = 0;
+        a[(size_t)i].routing_weight = routing_weights[i];
+    }
+    int rc = run_assignments(r, x, x_dtype, a.data(), count, out, 0, false);
+    if (rc) return rc;
+    GW_HIP(hipStreamSynchronize(r->ctx->stream));
+    return GW_OK;
+}
+
+extern "C" int gw_expert_apply_assignments_async(gw_expert_runner *r, const void *inputs,
+                                                 gw_dtype x_dtype,
+                                                 const gw_assignment *assignments,
+                                                 int32_t count, float *outputs)
+{
+    GW_CHECK(r, GW_ERR_ARG, "runner is null");
+    GW_CHECK(count >= 0, GW_ERR_ARG, "negative count");
+    if (count == 0) return GW_OK;   // ExpertRunner.swift:111
+    GW_CHECK(assignments, GW_ERR_ARG, "assignments is null");
+    return run_assignments(r, inputs, x_dtype, assignments, count, outputs, 1, true);
+}
+
+extern "C" int gw_expert_apply_assignments(gw_expert_runner *r, const void *inputs,
+                                           gw_dtype x_dtype, const gw_assignment *assignments,
+                                           int32_t count, float *outputs)
+{
+    int rc = gw_expert_apply_assignments_async(r, inputs, x_dtype, assignments, count, outputs);
+    if (rc) return rc;
+    GW_HIP(hipStreamSynchronize(r->ctx->stream));
+    return GW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// MoE layer (device-routed)
+// ---------------------------------------------------------------------------
+
+extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args *a)
+{
+    GW_CHECK(r && a, GW_ERR_ARG, "null argument");
+    GW_CHECK(a->tokens >= 1 && a->tokens <= gw::kMaxTokens, GW_ERR_SHAPE,
+             "decode layer takes 1..%d tokens (got %d)", gw::kMaxTokens, a->tokens);
+    GW_CHECK(a->expert_count >= 1 && a->expert_count <= kMaxExperts, GW_ERR_SHAPE,
+             "expert_count %lld out of range", (long long)a->expert_count);
+    GW_CHECK(a->top_k >= 1 && a->top_k <= gw::kMaxTopK && a->top_k <= a->expert_count,
+             GW_ERR_SHAPE, "top_k %lld out of range", (long long)a->top_k);
+    GW_CHECK(a->experts_base && a->x && a->out, GW_ERR_ARG, "null pointer");
+    GW_CHECK(aligned16(a->experts_base) && a->expert_stride > 0 && a->expert_stride % 16 == 0,
+             GW_ERR_ARG, "experts_base/stride must be 16-byte aligned");
+    GW_CHECK(dtype_ok(a->x_dtype), GW_ERR_ARG, "bad x dtype");
+    GW_CHECK((reinterpret_cast<uintptr_t>(a->x) & 3u) == 0, GW_ERR_ARG, "x must be 4-byte aligned");
+    GW_CHECK(a->logits || a->router_weight, GW_ERR_ARG, "need logits or router weights");
+    gw_context *ctx = r->ctx;
+    const gw::Launch L = launch_of(ctx);
+    const float *logits = a->logits;
+    if (!logits) {
+        GW_CHECK(dtype_ok(a->router_weight_dtype), GW_ERR_ARG, "bad router dtype");
+        ProfScope ps(ctx, "router");
+        GW_HIP(gw::launch_router(L, a->router_weight, a->router_weight_dtype, a->router_bias,
+                                 a->router_bias ? (int)a->router_bias_dtype : -1, a->x,
+                                 a->x_dtype, r->logits, (int)a->expert_count, (int)r->hidden,
+                                 a->tokens));
+        logits = r->logits;
+    }
+    {
+        ProfScope ps(ctx, "route");
+        GW_HIP(gw::launch_route(L, logits, (int)a->expert_count, (int)a->top_k, a->tokens,
+                                a->experts_base, a->expert_stride, r->route_plan,
+                                a->routing_ids, a->routing_weights));
+    }
+    GW_CHECK(gw::gate_up_lds_bytes((int)r->hidden, a->x_dtype, a->tokens) <= gw::kLdsBudget,
+             GW_ERR_SHAPE, "%d tokens of width %lld exceed the LDS budget", a->tokens,
+             (long long)r->hidden);
+    const gw::Sections sec = sections_of(r->offsets);
+    {
+        ProfScope ps(ctx, "gate_up");
+        GW_HIP(gw::launch_gate_up(L, r->route_plan, a->tokens, a->x, a->x_dtype, (int)r->hidden,
+                                  (int)r->inter, sec, r->bias_dt, r->act_buf, r->act, r->limit,
+                                  r->alpha));
+    }
+    {
+        ProfScope ps(ctx, "down");
+        GW_HIP(gw::launch_down(L, r->route_plan, a->tokens, (int)(a->tokens * a->top_k), r->act_buf,
+                               (int)r->hidden, (int)r->inter, sec, r->bias_dt, a->out,
+                               a->out_bf16, 0));
+    }
+    return GW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// graphs
+// ---------------------------------------------------------------------------
+
+struct gw_graph {
+    gw_context *ctx;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+extern "C" int gw_graph_begin_capture(gw_context *ctx)
+{
+    GW_CHECK(ctx, GW_ERR_ARG, "context is null");
+    GW_CHECK(!ctx->capturing, GW_ERR_ARG, "already capturing");
+    GW_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    return GW_OK;
+}
+
+extern "C" int gw_graph_end_capture(gw_context *ctx, gw_graph **out)
+{
+    GW_CHECK(ctx && out, GW_ERR_ARG, "null argument");
+    GW_CHECK(ctx->capturing, GW_ERR_ARG, "not capturing");
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    GW_HIP(hipStreamEndCapture(ctx->stream, &g));
+    hipGraphExec_t ex = nullptr;
+    hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return fail(GW_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    }
+    gw_graph *gr = new gw_graph{ctx, g, ex};
+    *out = gr;
+    return GW_OK;
+}
+
+extern "C" int gw_graph_launch(gw_graph *g)
+{
+    GW_CHECK(g, GW_ERR_ARG, "graph is null");
+    GW_HIP(hipGraphLaunch(g->exec, g->ctx->stream));
+    return GW_OK;
+}
+
+extern "C" int gw_graph_destroy(gw_graph *g)
+{
+    if (!g) return GW_OK;
+    (void)hipGraphExecDestroy(g->exec);
+    (void)hipGraphDestroy(g->graph);
+    delete g;
+    return GW_OK;
+}

@@ -1,0 +1,234 @@
+// gw_device.h — gfx950 device helpers for the MXFP4 decode kernels.
+//
+// MXFP4 (Sources/Godwit/Quant/MXFP4.swift:3-31): 32 e2m1 codes per block, two
+// per byte with the low nibble the even element, one e8m0 scale per block.
+// Codes are widened by CDNA4's v_cvt_scalef32_pk_{f32,f16,bf16}_fp4 (one
+// instruction per packed byte, scale operand 1.0 so the result is the exact
+// codebook value of MXFP4.swift:22-25), and dotted with the activation in
+// fp32 by v_dot2c_f32_{f16,bf16} (two products per lane-op) or v_fma_f32.
+// The block scale multiplies the block's fp32 partial afterwards, as in
+// referenceMXFP4 (Benchmark/DequantGEMVBenchmark.swift:106-116).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gw_plan.h"
+
+namespace gw {
+
+enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };   // == gw_dtype
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kNT = 256;   // threads per workgroup of the streaming kernels
+
+// e8m0 -> fp32, exactly 2^(b-127): b<<23 is the normal encoding, b == 0 is the
+// subnormal 2^-127, 0xFF is NaN (MXFP4.decodeScale, MXFP4.swift:37-40).
+__device__ __forceinline__ float decode_scale(uint32_t b)
+{
+    uint32_t bits = b << 23;
+    bits = (b == 0u) ? 0x00400000u : bits;
+    bits = (b == 255u) ? 0x7FC00000u : bits;
+    return __uint_as_float(bits);
+}
+
+// Activation vector layout in LDS: one block of 32 elements per row of
+// kBlockDw dwords; the 4-dword pad staggers consecutive blocks across banks
+// (lanes of a wave read consecutive blocks).
+template <int XK> struct XL { static constexpr int kBlockDw = 20; };   // 16-bit: 16 + 4
+template <> struct XL<DT_F32> { static constexpr int kBlockDw = 36; }; // f32: 32 + 4
+
+// --- one block: 16 packed bytes . 32 activations -> fp32 partial ----------
+
+#define GW_CVT_BF16(word, sel) __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4((word), 1.0f, (sel))
+#define GW_CVT_F16(word, sel) __builtin_amdgcn_cvt_scalef32_pk_f16_fp4((word), 1.0f, (sel))
+#define GW_CVT_F32(word, sel) __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((word), 1.0f, (sel))
+
+// Widened weights of one block, kept in registers so several token vectors can
+// reuse them.
+template <int XK> struct WBlock { uint32_t v[16]; };       // 16 packed 16-bit pairs
+template <> struct WBlock<DT_F32> { f32x2 v[16]; };
+
+template <int XK> __device__ __forceinline__ void widen(const uint4 &w, WBlock<XK> &o);
+
+template <> __device__ __forceinline__ void widen<DT_BF16>(const uint4 &w, WBlock<DT_BF16> &o)
+{
+#define GW_W(i, word, sel) o.v[i] = __builtin_bit_cast(uint32_t, GW_CVT_BF16(word, sel))
+    GW_W(0, w.x, 0); GW_W(1, w.x, 1); GW_W(2, w.x, 2); GW_W(3, w.x, 3);
+    GW_W(4, w.y, 0); GW_W(5, w.y, 1); GW_W(6, w.y, 2); GW_W(7, w.y, 3);
+    GW_W(8, w.z, 0); GW_W(9, w.z, 1); GW_W(10, w.z, 2); GW_W(11, w.z, 3);
+    GW_W(12, w.w, 0); GW_W(13, w.w, 1); GW_W(14, w.w, 2); GW_W(15, w.w, 3);
+#undef GW_W
+}
+
+template <> __device__ __forceinline__ void widen<DT_F16>(const uint4 &w, WBlock<DT_F16> &o)
+{
+#define GW_W(i, word, sel) o.v[i] = __builtin_bit_cast(uint32_t, GW_CVT_F16(word, sel))
+    GW_W(0, w.x, 0); GW_W(1, w.x, 1); GW_W(2, w.x, 2); GW_W(3, w.x, 3);
+    GW_W(4, w.y, 0); GW_W(5, w.y, 1); GW_W(6, w.y, 2); GW_W(7, w.y, 3);
+    GW_W(8, w.z, 0); GW_W(9, w.z, 1); GW_W(10, w.z, 2); GW_W(11, w.z, 3);
+    GW_W(12, w.w, 0); GW_W(13, w.w, 1); GW_W(14, w.w, 2); GW_W(15, w.w, 3);
+#undef GW_W
+}
+
+template <> __device__ __forceinline__ void widen<DT_F32>(const uint4 &w, WBlock<DT_F32> &o)
+{
+#define GW_W(i, word, sel) o.v[i] = GW_CVT_F32(word, sel)
+    GW_W(0, w.x, 0); GW_W(1, w.x, 1); GW_W(2, w.x, 2); GW_W(3, w.x, 3);
+    GW_W(4, w.y, 0); GW_W(5, w.y, 1); GW_W(6, w.y, 2); GW_W(7, w.y, 3);
+    GW_W(8, w.z, 0); GW_W(9, w.z, 1); GW_W(10, w.z, 2); GW_W(11, w.z, 3);
+    GW_W(12, w.w, 0); GW_W(13, w.w, 1); GW_W(14, w.w, 2); GW_W(15, w.w, 3);
+#undef GW_W
+}
+
+// Dot of a widened block with one activation block in LDS (layout XL<XK>).
+template <int XK> __device__ __forceinline__ float block_dot(const WBlock<XK> &w,
+                                                            const uint32_t *xb);
+
+template <> __device__ __forceinline__ float block_dot<DT_BF16>(const WBlock<DT_BF16> &w,
+                                                               const uint32_t *xb)
+{
+    const uint4 *xv = reinterpret_cast<const uint4 *>(xb);
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint4 x = xv[q];
+        a0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.v[4 * q + 0]),
+                                             __builtin_bit_cast(bf16x2, x.x), a0, false);
+        a1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.v[4 * q + 1]),
+                                             __builtin_bit_cast(bf16x2, x.y), a1, false);
+        a0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.v[4 * q + 2]),
+                                             __builtin_bit_cast(bf16x2, x.z), a0, false);
+        a1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.v[4 * q + 3]),
+                                             __builtin_bit_cast(bf16x2, x.w), a1, false);
+    }
+    return a0 + a1;
+}
+
+template <> __device__ __forceinline__ float block_dot<DT_F16>(const WBlock<DT_F16> &w,
+                                                              const uint32_t *xb)
+{
+    const uint4 *xv = reinterpret_cast<const uint4 *>(xb);
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint4 x = xv[q];
+        a0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w.v[4 * q + 0]),
+                                    __builtin_bit_cast(f16x2, x.x), a0, false);
+        a1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w.v[4 * q + 1]),
+                                    __builtin_bit_cast(f16x2, x.y), a1, false);
+        a0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w.v[4 * q + 2]),
+                                    __builtin_bit_cast(f16x2, x.z), a0, false);
+        a1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w.v[4 * q + 3]),
+                                    __builtin_bit_cast(f16x2, x.w), a1, false);
+    }
+    return a0 + a1;
+}
+
+template <> __device__ __forceinline__ float block_dot<DT_F32>(const WBlock<DT_F32> &w,
+                                                              const uint32_t *xb)
+{
+    const float4 *xv = reinterpret_cast<const float4 *>(xb);
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const float4 x = xv[q];
+        a0 = fmaf(w.v[2 * q].x, x.x, a0);
+        a1 = fmaf(w.v[2 * q].y, x.y, a1);
+        a0 = fmaf(w.v[2 * q + 1].x, x.z, a0);
+        a1 = fmaf(w.v[2 * q + 1].y, x.w, a1);
+    }
+    return a0 + a1;
+}
+
+// --- activation vector staging ---------------------------------------------
+
+// Copies one activation vector of `n` elements (n % 32 == 0) of dtype XK from
+// global memory into LDS layout XL<XK>.  All threads of the block participate.
+template <int XK>
+__device__ __forceinline__ void stage_vector(uint32_t *dst, const void *src, int n)
+{
+    constexpr int BD = XL<XK>::kBlockDw;
+    if constexpr (XK == DT_F32) {
+        const float *s = static_cast<const float *>(src);
+        for (int i = threadIdx.x; i < n; i += blockDim.x)
+            dst[(i >> 5) * BD + (i & 31)] = __float_as_uint(s[i]);
+    } else {
+        const uint32_t *s = static_cast<const uint32_t *>(src);   // element pairs
+        for (int i = threadIdx.x; i < n / 2; i += blockDim.x)
+            dst[(i >> 4) * BD + (i & 15)] = s[i];
+    }
+}
+
+// --- small numerics ----------------------------------------------------------
+
+// BFloat16.fromFloat (Install/Int8Affine.swift:86-93): RNE, NaN kept a NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float v)
+{
+    uint32_t bits = __float_as_uint(v);
+    if ((bits & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((bits >> 16) | 0x0040u);
+    uint32_t rounding = ((bits >> 16) & 1u) + 0x7FFFu;
+    return (uint16_t)((bits + rounding) >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b)
+{
+    return __uint_as_float((uint32_t)b << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v)
+{
+    return __builtin_bit_cast(uint16_t, (_Float16)v);   // v_cvt_f16_f32, RNE
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h)
+{
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ __forceinline__ float load_as_f32(const void *p, int dtype, int64_t i)
+{
+    if (dtype == DT_F32) return static_cast<const float *>(p)[i];
+    const uint16_t b = static_cast<const uint16_t *>(p)[i];
+    return dtype == DT_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+// Bias of row r: bf16 (the .gwt layout, InstallLayout.swift:76-77), f32, or none.
+__device__ __forceinline__ float load_bias(const void *bias, int dtype, int64_t r)
+{
+    return bias ? load_as_f32(bias, dtype, r) : 0.0f;
+}
+
+// dst + a * w with the product and the sum rounded separately (no FMA), the
+// arithmetic of expert_accumulate (expert.metal:115).
+__device__ __forceinline__ float add_scaled_rn(float dst, float a, float w)
+{
+#pragma clang fp contract(off)
+    return dst + a * w;
+}
+
+// GPT-OSS expert gate (expert.metal:93-101) and SiLU-GLU (expert.metal:388-392),
+// written in the kernels' operation order; fp16 rounding is the caller's.
+__device__ __forceinline__ float gptoss_glu(float gate, float up, float limit, float alpha)
+{
+    gate = fminf(gate, limit);
+    up = fminf(fmaxf(up, -limit), limit);
+    const float glu = gate * (1.0f / (1.0f + expf(-alpha * gate)));
+    return (up + 1.0f) * glu;
+}
+
+__device__ __forceinline__ float silu_glu(float gate, float up)
+{
+    const float silu = gate * (1.0f / (1.0f + expf(-gate)));
+    return silu * up;
+}
+
+__device__ __forceinline__ float apply_activation(int kind, float g, float u, float limit,
+                                                  float alpha)
+{
+    return kind == 0 ? gptoss_glu(g, u, limit, alpha) : silu_glu(g, u);
+}
+
+}  // namespace gw

@@ -1,0 +1,55 @@
+// gw_launch.h — host-side launchers of the gfx950 kernels (gw_kernels.hip).
+// Internal to libgodwit_hip.so; the public surface is include/godwit_hip.h.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gw_plan.h"
+
+namespace gw {
+
+struct Launch {
+    hipStream_t stream;
+    int cus;        // compute units of the device
+    int grid_a;     // workgroups of the gate_up kernel (0 = default)
+    int grid_b;     // workgroups of the down kernel (0 = default)
+};
+
+// Lanes per row and blocks per lane chosen for a row of `bpr` MXFP4 blocks.
+struct RowShape { int tpr; int m; int chunks; };
+RowShape row_shape(int bpr);
+
+hipError_t launch_dequant(const Launch &L, const uint8_t *packed, const uint8_t *scales,
+                          int64_t blocks, float *out);
+hipError_t launch_gemv(const Launch &L, const uint8_t *packed, const uint8_t *scales,
+                       const void *bias, int bias_dt, const void *x, int x_dt, float *y,
+                       int rows, int cols);
+hipError_t launch_activation(const Launch &L, int kind, const float *gate_up, uint16_t *out,
+                             int64_t width, float limit, float alpha);
+hipError_t launch_accumulate(const Launch &L, const float *src, float *dst, float w,
+                             int64_t width);
+hipError_t launch_router(const Launch &L, const void *W, int w_dt, const void *b, int b_dt,
+                         const void *x, int x_dt, float *logits, int experts, int hidden,
+                         int tokens);
+hipError_t launch_route(const Launch &L, const float *logits, int experts, int top_k,
+                        int tokens, const uint8_t *experts_base, int64_t stride, Plan *plan,
+                        int32_t *ids_out, float *w_out);
+hipError_t launch_gate_up(const Launch &L, const Plan *plan, int max_tokens, const void *x,
+                          int x_dt, int hidden, int inter, const Sections &sec, int bias_dt,
+                          uint16_t *act, int act_kind, float limit, float alpha);
+hipError_t launch_down(const Launch &L, const Plan *plan, int max_tokens, int max_slots,
+                       const uint16_t *act, int hidden, int inter, const Sections &sec,
+                       int bias_dt, float *out, uint16_t *out_bf16, int accumulate);
+hipError_t launch_fill_u8(const Launch &L, void *dst, size_t count, int lo, int hi,
+                          uint64_t seed);
+hipError_t launch_fill_normal(const Launch &L, void *dst, int dt, size_t count, float mean,
+                              float stddev, uint64_t seed);
+
+// LDS bytes the down kernel needs per slot of staged activations and the
+// fixed part; used by the host to bound slots per chunk.
+int down_lds_bytes(int hidden, int inter, int grid, int smax);
+int gate_up_lds_bytes(int hidden, int x_dt, int max_tokens);
+
+constexpr int kLdsBudget = 64 * 1024;
+
+}  // namespace gw

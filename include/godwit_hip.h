@@ -1,0 +1,287 @@
+/*
+ * godwit_hip.h — C ABI of the MI355X (gfx950) MoE expert hot-path library
+ * (libgodwit_hip.so).
+ *
+ * This is the drop-in boundary for rayl15/Godwit's MoE expert path.  Each
+ * entry point names the reference interface it replaces (paths relative to the
+ * reference repository root).  Plain pointers and sizes only: device buffers
+ * are `void*` device addresses from gw_malloc (or any hipMalloc'd memory of
+ * this process), host buffers are ordinary host memory.
+ *
+ * Conventions
+ *  - Every call returns an int status (gw_status); 0 is success.  On failure
+ *    gw_last_error() returns a thread-local message.  No C++ exception crosses
+ *    the ABI.  Shape violations return GW_ERR_SHAPE instead of trapping (the
+ *    reference traps with `precondition`).
+ *  - Calls on a context are stream-ordered on its stream.  Calls whose Swift
+ *    counterpart blocks (ExpertRunner.apply*, Router.logits, which run
+ *    MetalContext.run = commit + waitUntilCompleted) block here too;
+ *    gw_*_async variants and the layer/kernel calls only enqueue.
+ *  - A context and everything created from it is single-threaded; callers
+ *    serialise access.
+ *
+ * MXFP4 data (MXFP4.swift:3-31): a block is 32 e2m1 codes, two per byte, low
+ * nibble = even element, plus one e8m0 scale byte (2^(b-127), 0xFF = NaN).
+ * A matrix [rows, cols] is packed [rows, cols/32, 16] bytes + scales
+ * [rows, cols/32] bytes, row-major, cols % 32 == 0.
+ */
+#ifndef GODWIT_HIP_H
+#define GODWIT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__) || defined(__clang__)
+#pragma GCC visibility push(default)
+#endif
+
+/* ---- status, dtypes ---------------------------------------------------- */
+
+/* Replaces MetalError (Sources/Godwit/Infrastructure/Metal/MetalContext.swift:4-33)
+ * and the precondition traps of ExpertRunner.swift:194,276 / Router.swift:41,79. */
+typedef enum gw_status {
+    GW_OK = 0,
+    GW_ERR_ARG = 1,         /* null pointer, bad enum, negative size */
+    GW_ERR_SHAPE = 2,       /* cols % 32 != 0, size mismatch, limits exceeded */
+    GW_ERR_OOM = 3,         /* device allocation failed */
+    GW_ERR_HIP = 4,         /* HIP runtime error (message has hipGetErrorString) */
+    GW_ERR_NO_DEVICE = 5,   /* no HIP device / device index out of range */
+    GW_ERR_UNSUPPORTED = 6  /* valid request this build does not implement */
+} gw_status;
+
+typedef enum gw_dtype { GW_F32 = 0, GW_F16 = 1, GW_BF16 = 2 } gw_dtype;
+
+/* FeedForwardActivation (Sources/Godwit/Model/ArchitectureSpec.swift:14-38):
+ * .gptOssClampedGLU -> gptoss_expert_activation (expert.metal:82-102),
+ * .silu -> expert_activation_swiglu (expert.metal:380-393). */
+typedef enum gw_activation { GW_ACT_GPTOSS_CLAMPED_GLU = 0, GW_ACT_SILU = 1 } gw_activation;
+
+/* Thread-local message of the last failing call on this thread ("" if none). */
+const char *gw_last_error(void);
+/* Library version string. */
+const char *gw_version(void);
+
+/* ---- context (replaces MetalContext, MetalContext.swift:36-179) -------- */
+
+typedef struct gw_context gw_context;
+
+int gw_device_count(int *count);
+/* MetalContext.init: binds `device`, creates the context's stream. */
+int gw_context_create(int device, gw_context **out);
+int gw_context_destroy(gw_context *ctx);
+/* Blocks until all work enqueued on the context's stream is done. */
+int gw_context_synchronize(gw_context *ctx);
+/* The context's hipStream_t (as void*). */
+void *gw_context_stream(gw_context *ctx);
+/* Number of compute units of the context's device. */
+int gw_context_cu_count(gw_context *ctx, int *cus);
+
+/* Per-kernel timing (replaces Profiler, Infrastructure/Metal/Profiler.swift:11-98):
+ * while enabled, every launch is bracketed by hipEvents on the context stream.
+ * gw_context_profile_read synchronises and returns the summed GPU milliseconds
+ * and launch count of the kernel family `name` ("gate_up", "down", "route",
+ * "router", "gemv", "dequant", "activation", "accumulate"). */
+int gw_context_set_profiling(gw_context *ctx, int enabled);
+int gw_context_profile_read(gw_context *ctx, const char *name, double *total_ms,
+                            int64_t *launches);
+int gw_context_profile_reset(gw_context *ctx);
+
+/* ---- device memory (MetalContext.buffer / emptyBuffer, :161-178) ------- */
+
+int gw_malloc(gw_context *ctx, size_t bytes, void **out);
+int gw_free(gw_context *ctx, void *ptr);
+int gw_memcpy_htod(gw_context *ctx, void *dst, const void *src, size_t bytes);
+int gw_memcpy_dtoh(gw_context *ctx, void *dst, const void *src, size_t bytes);
+int gw_memcpy_dtod(gw_context *ctx, void *dst, const void *src, size_t bytes);
+int gw_memset_zero(gw_context *ctx, void *dst, size_t bytes);
+/* Enqueue-only device-to-device copy on the context stream (no wait). */
+int gw_memcpy_dtod_async(gw_context *ctx, void *dst, const void *src, size_t bytes);
+
+/* Seeded synthetic data on the device (counter-based: element i depends only
+ * on (seed, i)).  Replaces the xorshift inputs of
+ * DequantGEMVBenchmark.swift:35-54 for the large configurations.
+ *  - bytes uniform over [lo, hi] inclusive;
+ *  - normal(mean, std) written as f32, f16 or bf16 (RNE). */
+int gw_fill_uniform_u8(gw_context *ctx, void *dst, size_t count, int lo, int hi,
+                       uint64_t seed);
+int gw_fill_normal(gw_context *ctx, void *dst, gw_dtype dtype, size_t count, float mean,
+                   float std, uint64_t seed);
+
+/* ---- expert weight layout (ExpertLayout, Install/InstallLayout.swift:14-121) */
+
+/* Section order is ExpertLayout.Section (InstallLayout.swift:18-24). */
+enum {
+    GW_SECTION_GATE_UP_BLOCKS = 0,
+    GW_SECTION_GATE_UP_SCALES = 1,
+    GW_SECTION_DOWN_BLOCKS = 2,
+    GW_SECTION_DOWN_SCALES = 3,
+    GW_SECTION_GATE_UP_BIAS = 4,  /* bf16 [2F] */
+    GW_SECTION_DOWN_BIAS = 5,     /* bf16 [H] */
+    GW_SECTION_COUNT = 6
+};
+
+typedef struct gw_expert_layout {
+    int64_t hidden_size;
+    int64_t intermediate_size;
+    int64_t expert_count;
+    int64_t offsets[GW_SECTION_COUNT]; /* byte offset within one expert stride */
+    int64_t sizes[GW_SECTION_COUNT];
+    int64_t stride;                    /* page-aligned (16384) bytes per expert */
+    int64_t page_size;
+} gw_expert_layout;
+
+/* ExpertLayout.init(hiddenSize:intermediateSize:expertCount:) — InstallLayout.swift:50-92.
+ * Host-only; no device needed. */
+int gw_expert_layout_init(int64_t hidden_size, int64_t intermediate_size,
+                          int64_t expert_count, gw_expert_layout *out);
+
+/* ---- kernel-level entry points (the Metal argument tables) ------------- */
+
+/* mxfp4_dequant_reference / mxfp4_dequant_wide — Metal/Quant/mxfp4.metal:36-77.
+ * `blocks` blocks -> out[blocks*32] fp32, bit-exact with MXFP4.decode
+ * (MXFP4.swift:69-93): subnormal scales kept, 0xFF -> NaN, code 8 -> -0.0. */
+int gw_mxfp4_dequant(gw_context *ctx, const uint8_t *packed, const uint8_t *scales,
+                     int64_t blocks, float *out);
+
+/* mxfp4_gemv — Metal/Quant/dequant_gemv.metal:37-67 (no bias).
+ * y[r] = sum_b scale(r,b) * sum_i code(r,b,i) * x[32b+i], fp32 accumulation. */
+int gw_mxfp4_gemv(gw_context *ctx, const uint8_t *packed, const uint8_t *scales,
+                  const void *x, gw_dtype x_dtype, float *y, int64_t rows, int64_t cols);
+
+/* mxfp4_gemv_bias{,_persistent,_staged,_lut,_multirow} — Metal/MoE/expert.metal:46-77,
+ * 138-368: the GEMV plus bias[r] (bias_dtype GW_BF16 as in the .gwt layout, or
+ * GW_F32; bias may be NULL = no bias). */
+int gw_mxfp4_gemv_bias(gw_context *ctx, const uint8_t *packed, const uint8_t *scales,
+                       const void *bias, gw_dtype bias_dtype, const void *x,
+                       gw_dtype x_dtype, float *y, int64_t rows, int64_t cols);
+
+/* gptoss_expert_activation (expert.metal:82-102) / expert_activation_swiglu
+ * (expert.metal:380-393): interleaved fp32 gate_up[2*width] -> fp16 out[width]. */
+int gw_expert_activation(gw_context *ctx, gw_activation kind, const float *gate_up,
+                         uint16_t *out_f16, int64_t width, float limit, float alpha);
+
+/* expert_accumulate — expert.metal:107-116: dst[i] += expert_out[i] * weight. */
+int gw_expert_accumulate(gw_context *ctx, const float *expert_out, float *dst, float weight,
+                         int64_t width);
+
+/* bf16_gemv_bias — Metal/MoE/router.metal:18-34, as called by Router.logits
+ * (Runtime/Router.swift:38-66): logits[t, e] = W[e,:] . x[t,:] + bias[e] for
+ * `tokens` rows of x.  W is bf16 (reference) or f32; bias may be NULL. */
+int gw_router_logits(gw_context *ctx, const void *weight, gw_dtype weight_dtype,
+                     const void *bias, gw_dtype bias_dtype, const void *x, gw_dtype x_dtype,
+                     float *logits, int64_t experts, int64_t hidden, int32_t tokens);
+
+/* Router.select — Runtime/Router.swift:78-98, on the host: top_k by partial
+ * selection sort (strict >, swapAt), softmax over the k selected logits.
+ * ids highest-logit first. */
+int gw_router_select(const float *logits, int64_t experts, int64_t top_k, int32_t *ids,
+                     float *weights);
+
+/* ---- ExpertRunner (Runtime/ExpertRunner.swift:10-363) ------------------ */
+
+/* ExpertRunner.Weights (:54-64): one expert stride in device memory plus the
+ * byte offsets of its six sections (ExpertRunner.sectionOffsets, :67-75). */
+typedef struct gw_expert_weights {
+    const uint8_t *buffer;
+    int64_t offsets[GW_SECTION_COUNT];
+} gw_expert_weights;
+
+/* ExpertRunner.Assignment (:88-98). */
+typedef struct gw_assignment {
+    gw_expert_weights weights;
+    int32_t token;
+    float routing_weight;
+} gw_assignment;
+
+typedef struct gw_expert_runner gw_expert_runner;
+
+/* ExpertRunner.init(context:reader:swigluLimit:swigluAlpha:) (:37-47).
+ * limit/alpha are the model's activationLimit/activationAlpha (7.0 / 1.702 for
+ * GPT-OSS, ArchitectureSpec.swift:102-104).  Bias sections are bf16 as written
+ * by the installer; gw_expert_runner_set_bias_dtype switches to f32 sections. */
+int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size, int64_t intermediate_size,
+                            gw_activation activation, float swiglu_limit, float swiglu_alpha,
+                            gw_expert_runner **out);
+int gw_expert_runner_destroy(gw_expert_runner *runner);
+int gw_expert_runner_set_bias_dtype(gw_expert_runner *runner, gw_dtype bias_dtype);
+/* ExpertRunner.sectionOffsets (:67-75) for this runner's shape. */
+int gw_expert_runner_section_offsets(gw_expert_runner *runner,
+                                     int64_t offsets[GW_SECTION_COUNT]);
+
+/* ExpertRunner.apply(_:weights:) (:275-331): one expert, one token, no routing
+ * weight.  x [hidden] device, out [hidden] fp32 device (overwritten).  Blocks. */
+int gw_expert_apply(gw_expert_runner *runner, const void *x, gw_dtype x_dtype,
+                    const gw_expert_weights *weights, float *out);
+
+/* ExpertRunner.applyBatch(_:experts:) (:191-269): out = sum_i w_i * expert_i(x),
+ * accumulated in list order.  out [hidden] fp32 device (overwritten).  Blocks. */
+int gw_expert_apply_batch(gw_expert_runner *runner, const void *x, gw_dtype x_dtype,
+                          const gw_expert_weights *experts, const float *routing_weights,
+                          int32_t count, float *out);
+
+/* ExpertRunner.applyAssignments(inputs:assignments:outputs:) (:108-182):
+ * outputs[token] += routing_weight * expert(inputs[token]) for every
+ * assignment (in place; the caller zero-fills, TransformerLayer.swift:173).
+ * inputs [tokens, hidden], outputs [tokens, hidden] fp32, device.  Each
+ * distinct expert is read once per group of up to 8 tokens.  Blocks; the
+ * _async variant only enqueues. */
+int gw_expert_apply_assignments(gw_expert_runner *runner, const void *inputs,
+                                gw_dtype x_dtype, const gw_assignment *assignments,
+                                int32_t count, float *outputs);
+int gw_expert_apply_assignments_async(gw_expert_runner *runner, const void *inputs,
+                                      gw_dtype x_dtype, const gw_assignment *assignments,
+                                      int32_t count, float *outputs);
+
+/* ---- MoE block of TransformerLayer.forward (Runtime/TransformerLayer.swift:140-238) */
+
+/* One layer's MoE block for `tokens` (1..8) decode tokens, entirely on the
+ * device: router (bf16_gemv_bias, or given logits) -> top-k + softmax
+ * (Router.select) -> expert-major grouping (the demand map, :175-181) ->
+ * fused gate_up + activation -> fused down + weighted combine.
+ * Experts are HBM-resident at experts_base + e * expert_stride with the
+ * runner's section offsets (the .gwt layer file, ExpertLayout).
+ * out [tokens, hidden] fp32 is overwritten with the combined expert output
+ * (the residual add stays with the caller, :232-238).  Enqueue only. */
+typedef struct gw_moe_layer_args {
+    const uint8_t *experts_base;
+    int64_t expert_stride;
+    int64_t expert_count;
+    int64_t top_k;
+    const float *logits;              /* [tokens, expert_count] or NULL -> router runs */
+    const void *router_weight;        /* [expert_count, hidden] when logits == NULL */
+    gw_dtype router_weight_dtype;
+    const void *router_bias;          /* [expert_count] or NULL (Qwen3: no bias) */
+    gw_dtype router_bias_dtype;
+    const void *x;                    /* [tokens, hidden] */
+    gw_dtype x_dtype;
+    int32_t tokens;
+    float *out;                       /* [tokens, hidden] fp32 */
+    uint16_t *out_bf16;               /* optional bf16 copy of out (next layer's input) */
+    int32_t *routing_ids;             /* optional [tokens, top_k] */
+    float *routing_weights;           /* optional [tokens, top_k] */
+} gw_moe_layer_args;
+
+int gw_moe_layer_forward(gw_expert_runner *runner, const gw_moe_layer_args *args);
+
+/* ---- graphs (replace per-call command buffers with one replayable graph) */
+
+typedef struct gw_graph gw_graph;
+/* Starts stream capture on the context's stream; calls until end_capture are
+ * recorded, not run (only enqueue-only calls may be captured). */
+int gw_graph_begin_capture(gw_context *ctx);
+int gw_graph_end_capture(gw_context *ctx, gw_graph **out);
+int gw_graph_launch(gw_graph *graph);
+int gw_graph_destroy(gw_graph *graph);
+
+#if defined(__GNUC__) || defined(__clang__)
+#pragma GCC visibility pop
+#endif
+
+#ifdef __cplusplus
+}
+#endif
+#endif

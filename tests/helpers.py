@@ -1,0 +1,74 @@
+"""Seeded synthetic inputs and error metrics shared by the tests.
+
+Inputs follow the distributions of the benchmark configurations: e2m1 nibbles
+uniform over 0..15 (bytes uniform), e8m0 scales uniform over 119..127, fp32
+biases N(0, 0.02) rounded to bf16-representable values (the .gwt layout
+stores bf16 biases), activations N(0, 1).
+"""
+import numpy as np
+
+import oracle
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def mxfp4_matrix(r, rows, cols, scale_lo=119, scale_hi=127):
+    packed = r.integers(0, 256, size=rows * cols // 2, dtype=np.uint8)
+    scales = r.integers(scale_lo, scale_hi + 1, size=rows * cols // 32, dtype=np.uint8)
+    return packed, scales
+
+
+def bias_bf16(r, n, std=0.02):
+    """Returns (bf16 bits, the same values as fp32)."""
+    bits = oracle.f32_to_bf16_bits((r.standard_normal(n) * std).astype(np.float32))
+    return bits, oracle.bf16_bits_to_f32(bits)
+
+
+def normal_bf16(r, n):
+    bits = oracle.f32_to_bf16_bits(r.standard_normal(n).astype(np.float32))
+    return bits, oracle.bf16_bits_to_f32(bits)
+
+
+def gemv_metric(got, ref):
+    """DequantGEMVBenchmark.compareToReference (DequantGEMVBenchmark.swift:338-349):
+    max |got - ref| / max(|ref|, 1)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1.0)))
+
+
+def expert_metric(got, ref):
+    """runExpertCheck (GodwitCLI/main.swift:518-532): max |got - ref| / mean |ref|."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(got - ref)) / max(np.mean(np.abs(ref)), 1e-30))
+
+
+class ExpertData:
+    """One expert's sections as host arrays, plus its bytes in the .gwt stride layout."""
+
+    def __init__(self, r, hidden, inter, layout_offsets, stride, with_bias=True):
+        self.gu_packed, self.gu_scales = mxfp4_matrix(r, 2 * inter, hidden)
+        self.dn_packed, self.dn_scales = mxfp4_matrix(r, hidden, inter)
+        if with_bias:
+            self.gu_bias_bits, self.gu_bias = bias_bf16(r, 2 * inter)
+            self.dn_bias_bits, self.dn_bias = bias_bf16(r, hidden)
+        else:
+            self.gu_bias_bits = np.zeros(2 * inter, np.uint16)
+            self.dn_bias_bits = np.zeros(hidden, np.uint16)
+            self.gu_bias = np.zeros(2 * inter, np.float32)
+            self.dn_bias = np.zeros(hidden, np.float32)
+        blob = np.zeros(stride, np.uint8)
+        for name, arr in (("gate_up_blocks", self.gu_packed), ("gate_up_scales", self.gu_scales),
+                          ("down_blocks", self.dn_packed), ("down_scales", self.dn_scales),
+                          ("gate_up_bias", self.gu_bias_bits.view(np.uint8)),
+                          ("down_bias", self.dn_bias_bits.view(np.uint8))):
+            off = layout_offsets[name]
+            blob[off:off + arr.nbytes] = arr.view(np.uint8)
+        self.blob = blob
+
+    def oracle_expert(self):
+        return oracle.Expert(self.gu_packed, self.gu_scales, self.dn_packed, self.dn_scales,
+                             self.gu_bias, self.dn_bias)

@@ -1,0 +1,227 @@
+"""GPU parity of the kernel-level entry points against the CPU oracle.
+
+Mirrors Tests/GodwitTests/DequantGEMVTests.swift (GEMV vs referenceMXFP4 at
+64x256 and 32x2880, metric < 1e-3) and ActivationTests.swift (fixed vectors),
+and adds the bit-exact dequant table and the BASELINE config-0 shape.
+"""
+import numpy as np
+import pytest
+
+import godwit_amd as gw
+import oracle
+from helpers import bias_bf16, gemv_metric, mxfp4_matrix, normal_bf16, rng
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits_equal(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    nan_a, nan_b = np.isnan(a), np.isnan(b)
+    assert np.array_equal(nan_a, nan_b), "NaN positions differ"
+    return np.array_equal(a[~nan_a].view(np.uint32), b[~nan_b].view(np.uint32))
+
+
+def test_dequant_exhaustive_codes_and_scales(ctx):
+    """Every (byte, scale) pair: 256 packed bytes x 256 scale bytes, bit-exact with
+    MXFP4.decode (MXFP4.swift:69-93): subnormal scales, NaN for 0xFF, -0.0 for code 8."""
+    blocks = 256 * 16   # block b: scale b // 16, bytes cover all 256 values once per scale
+    packed = np.tile(np.arange(256, dtype=np.uint8), 256)
+    scales = np.repeat(np.arange(256, dtype=np.uint8), 16)
+    pb, sb, ob = ctx.buffer(packed), ctx.buffer(scales), ctx.empty(blocks * 32 * 4)
+    gw.mxfp4_dequant(ctx, pb, sb, blocks, ob)
+    got = ob.download(np.float32, blocks * 32)
+    want = oracle.decode(packed, scales, blocks)
+    assert _bits_equal(got, want)
+    # spot checks of the special values
+    assert got[0] == 0.0 and np.signbit(got[0]) is np.False_
+    neg0 = got[(0x08 & 0xF) * 2 + 0]   # byte 0x08: low nibble code 8 -> -0.0
+    assert neg0 == 0.0 and np.signbit(neg0)
+    for b in (pb, sb, ob):
+        b.free()
+
+
+def test_dequant_random_large(ctx):
+    r = rng(1)
+    blocks = 5760 * 90
+    packed, scales = mxfp4_matrix(r, 5760, 2880, 0, 255)
+    pb, sb, ob = ctx.buffer(packed), ctx.buffer(scales), ctx.empty(blocks * 32 * 4)
+    gw.mxfp4_dequant(ctx, pb, sb, blocks, ob)
+    assert _bits_equal(ob.download(np.float32, blocks * 32), oracle.decode(packed, scales, blocks))
+    for b in (pb, sb, ob):
+        b.free()
+
+
+def _run_gemv(ctx, packed, scales, x, x_dtype, rows, cols, bias=None, bias_dtype=gw.BF16):
+    pb, sb, xb, yb = ctx.buffer(packed), ctx.buffer(scales), ctx.buffer(x), ctx.empty(rows * 4)
+    bb = ctx.buffer(bias) if bias is not None else None
+    gw.mxfp4_gemv_bias(ctx, pb, sb, bb, bias_dtype, xb, x_dtype, yb, rows, cols)
+    y = yb.download(np.float32, rows)
+    for b in (pb, sb, xb, yb, bb):
+        if b is not None:
+            b.free()
+    return y
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 256), (32, 2880)])
+def test_gemv_matches_reference_xorshift(ctx, rows, cols):
+    """DequantGEMVTests.swift:20-42: the reference's own inputs (xorshift bytes seed
+    0xA5A5, scales 120 + i % 14, fp16 x seed 0x1234), metric < 1e-3."""
+    packed = oracle.xorshift_bytes(0xA5A5, rows * cols // 2)
+    scales = (120 + np.arange(rows * cols // 32) % 14).astype(np.uint8)
+    x16 = oracle.xorshift_activations_f16(0x1234, cols)
+    ref = oracle.reference_mxfp4(packed, scales, x16.astype(np.float32), rows, cols)
+    pb, sb, xb, yb = ctx.buffer(packed), ctx.buffer(scales), ctx.buffer(x16), ctx.empty(rows * 4)
+    gw.mxfp4_gemv(ctx, pb, sb, xb, gw.F16, yb, rows, cols)
+    got = yb.download(np.float32, rows)
+    assert gemv_metric(got, ref) < 1e-3
+    for b in (pb, sb, xb, yb):
+        b.free()
+
+
+def test_gemv_hand_case(ctx):
+    """DequantGEMVTests.swift:64-77: 16 x 0x22 (code 2 = 1.0), scale 127, x = 1 -> 32."""
+    y = _run_gemv(ctx, np.full(16, 0x22, np.uint8), np.array([127], np.uint8),
+                  np.ones(32, np.float16), gw.F16, 1, 32)
+    assert y[0] == 32.0
+
+
+@pytest.mark.parametrize("x_dtype", [gw.F32, gw.F16, gw.BF16])
+def test_gemv_config0_shape(ctx, x_dtype):
+    """5760 x 2880, nibbles U{0..15}, scales U{119..127},
+    fp32 bias N(0, 0.02); x ~ N(0,1) in each supported dtype."""
+    r = rng(7)
+    rows, cols = 5760, 2880
+    packed, scales = mxfp4_matrix(r, rows, cols)
+    bias = (r.standard_normal(rows) * 0.02).astype(np.float32)
+    xf = r.standard_normal(cols).astype(np.float32)
+    if x_dtype == gw.F32:
+        x, xw = xf, xf
+    elif x_dtype == gw.F16:
+        x = xf.astype(np.float16)
+        xw = x.astype(np.float32)
+    else:
+        x, xw = normal_bf16(r, cols)
+    ref = oracle.gemv_bias(packed, scales, bias, xw, rows, cols)
+    got = _run_gemv(ctx, packed, scales, x, x_dtype, rows, cols, bias=bias, bias_dtype=gw.F32)
+    assert gemv_metric(got, ref) < 1e-3
+    # float64 brute force bounds the oracle's own rounding too
+    w = oracle.decode(packed, scales, rows * cols // 32).astype(np.float64).reshape(rows, cols)
+    exact = w @ xw.astype(np.float64) + bias
+    assert gemv_metric(got, exact) < 1e-4
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 32), (3, 64), (17, 768), (5, 4096), (33, 2048),
+                                       (7, 32 * 600)])
+def test_gemv_ragged_shapes(ctx, rows, cols):
+    r = rng(rows * 1000 + cols)
+    packed, scales = mxfp4_matrix(r, rows, cols)
+    bits, bias = bias_bf16(r, rows)
+    xb16, xw = normal_bf16(r, cols)
+    ref = oracle.gemv_bias(packed, scales, bias, xw, rows, cols)
+    got = _run_gemv(ctx, packed, scales, xb16, gw.BF16, rows, cols, bias=bits, bias_dtype=gw.BF16)
+    assert gemv_metric(got, ref) < 1e-3
+
+
+def test_gemv_edge_scales(ctx):
+    """Subnormal scale bytes 0/1, the largest scale 254 and NaN 0xFF flow through the GEMV
+    as the CPU reference computes them."""
+    r = rng(3)
+    rows, cols = 8, 256
+    packed, scales = mxfp4_matrix(r, rows, cols)
+    scales = scales.reshape(rows, -1)
+    scales[1, :] = 0
+    scales[2, :] = 1
+    scales[3, 3] = 254
+    scales[4, 5] = 255
+    scales = scales.ravel()
+    x = np.ones(cols, np.float16)
+    ref = oracle.reference_mxfp4(packed, scales, x.astype(np.float32), rows, cols)
+    got = _run_gemv(ctx, packed, scales, x, gw.F16, rows, cols)
+    assert np.isnan(got[4]) and np.isnan(ref[4])
+    keep = np.arange(rows) != 4
+    assert np.allclose(got[keep], ref[keep], rtol=1e-6, atol=0)
+
+
+def test_gemv_shape_errors(ctx):
+    b = ctx.empty(1024)
+    with pytest.raises(gw.GodwitError) as e:
+        gw.mxfp4_gemv(ctx, b, b, b, gw.F16, b, 4, 48)
+    assert e.value.status == 2   # GW_ERR_SHAPE: cols % 32
+    b.free()
+
+
+GATE = np.array([-4, -2, -1, -0.5, 0, 0.5, 1, 2, 4, 8, -8, 0.1], np.float32)
+UP = np.array([1, -1, 2, 0.5, 3, -2, 1, 0.25, -1, 2, 1, -3], np.float32)
+
+
+def _run_activation(ctx, kind, gate, up):
+    gu = np.empty(2 * gate.size, np.float32)
+    gu[0::2], gu[1::2] = gate, up
+    gb, ob = ctx.buffer(gu), ctx.empty(gate.size * 2)
+    gw.expert_activation(ctx, kind, gb, ob, gate.size, 7.0, 1.702)
+    out = ob.download(np.float16, gate.size)
+    gb.free()
+    ob.free()
+    return out, gu
+
+
+def test_swiglu_fixed_vectors(ctx):
+    """ActivationTests.swift:62-83: silu(gate) * up within 0.01."""
+    out, gu = _run_activation(ctx, "silu", GATE, UP)
+    want = GATE / (1 + np.exp(-GATE.astype(np.float64))) * UP
+    assert np.all(np.abs(out.astype(np.float64) - want) < 0.01)
+    ref = oracle.activation(oracle.ACT_SWIGLU, gu)
+    assert np.max(np.abs(out.astype(np.float32) - ref.astype(np.float32))
+                  / np.maximum(np.abs(ref.astype(np.float32)), 1e-3)) <= 2 ** -10
+
+
+def test_gptoss_activation_vectors(ctx):
+    """gptoss_expert_activation (expert.metal:82-102) against the CPU closed form of
+    ArchitectureSpecTests.swift:80-84 (the reference has no GPU test for it)."""
+    r = rng(5)
+    gate = np.concatenate([GATE, r.standard_normal(4000).astype(np.float32) * 20])
+    up = np.concatenate([UP, r.standard_normal(4000).astype(np.float32) * 20])
+    out, gu = _run_activation(ctx, "gptOssClampedGLU", gate, up)
+    g = np.minimum(gate.astype(np.float64), 7)
+    u = np.clip(up.astype(np.float64), -7, 7)
+    want = (u + 1) * (g / (1 + np.exp(-1.702 * g)))
+    assert np.all(np.abs(out.astype(np.float64) - want) <= 0.01 * np.maximum(1, np.abs(want)))
+    ref = oracle.activation(oracle.ACT_GPTOSS, gu).astype(np.float32)
+    o = out.astype(np.float32)
+    # identical up to one fp16 ulp (exp may differ by an fp32 ulp before rounding)
+    assert np.all(np.abs(o - ref) <= np.spacing(np.abs(ref).astype(np.float16)).astype(np.float32))
+
+
+def test_accumulate(ctx):
+    r = rng(11)
+    src = r.standard_normal(2880).astype(np.float32)
+    dst = r.standard_normal(2880).astype(np.float32)
+    sb, db = ctx.buffer(src), ctx.buffer(dst)
+    gw.expert_accumulate(ctx, sb, db, 0.37, 2880)
+    got = db.download(np.float32, 2880)
+    assert np.array_equal(got, oracle.accumulate(src, dst, 0.37))
+    sb.free()
+    db.free()
+
+
+def test_router_logits(ctx):
+    """bf16_gemv_bias (router.metal:18-34) for 128 experts, bf16 weights and bias."""
+    r = rng(13)
+    E, H = 128, 2880
+    wbits, wf = normal_bf16(r, E * H)
+    wf = wf * 0.02
+    wbits = oracle.f32_to_bf16_bits(wf)
+    wf = oracle.bf16_bits_to_f32(wbits)
+    bbits, bf = bias_bf16(r, E)
+    x16 = r.standard_normal(H).astype(np.float16)
+    router = gw.Router(ctx, E, H, 4)
+    wb, bb = ctx.buffer(wbits), ctx.buffer(bbits)
+    got = router.logits(x16, wb, bb)
+    ref = oracle.router_logits(wf, bf, x16.astype(np.float32), E, H)
+    assert gemv_metric(got, ref) < 1e-5
+    d = router.route(x16, wb, bb)
+    ids, w = oracle.router_select(got, 4)
+    assert d.experts == list(ids) and np.allclose(d.weights, w, rtol=0, atol=0)
+    wb.free()
+    bb.free()
