@@ -697,7 +697,8 @@ static int run_plan(gw_expert_runner *r, HostPlan &hp, const int64_t offsets[GW_
              (long long)r->hidden);
     {
         ProfScope ps(ctx, "gate_up");
-        GW_HIP(gw::launch_gate_up(L, r->plans + slot, q.ntokens, inputs, x_dt, (int)r->hidden,
+        GW_HIP(gw::launch_gate_up(L, r->plans + slot, nullptr, q.ntokens, inputs, x_dt,
+                                  (int)r->hidden,
                                   (int)r->inter, sec, r->bias_dt, r->act_buf, r->act, r->limit,
                                   r->alpha));
     }
@@ -911,21 +912,31 @@ extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args
                                  a->tokens));
         logits = r->logits;
     }
-    {
-        ProfScope ps(ctx, "route");
-        GW_HIP(gw::launch_route(L, logits, (int)a->expert_count, (int)a->top_k, a->tokens,
-                                a->experts_base, a->expert_stride, r->route_plan,
-                                a->routing_ids, a->routing_weights));
-    }
     GW_CHECK(gw::gate_up_lds_bytes((int)r->hidden, a->x_dtype, a->tokens) <= gw::kLdsBudget,
              GW_ERR_SHAPE, "%d tokens of width %lld exceed the LDS budget", a->tokens,
              (long long)r->hidden);
+    gw::RouteArgs route;
+    route.logits = logits;
+    route.experts = (int)a->expert_count;
+    route.top_k = (int)a->top_k;
+    route.tokens = a->tokens;
+    route.experts_base = a->experts_base;
+    route.stride = a->expert_stride;
+    route.ids_out = a->routing_ids;
+    route.w_out = a->routing_weights;
+    // Up to 256 experts the gate_up kernel routes in its prologue; beyond that
+    // the route kernel builds the plan first.
+    const bool fused = a->expert_count <= gw::kFusedRouteExperts;
+    if (!fused) {
+        ProfScope ps(ctx, "route");
+        GW_HIP(gw::launch_route(L, route, r->route_plan));
+    }
     const gw::Sections sec = sections_of(r->offsets);
     {
         ProfScope ps(ctx, "gate_up");
-        GW_HIP(gw::launch_gate_up(L, r->route_plan, a->tokens, a->x, a->x_dtype, (int)r->hidden,
-                                  (int)r->inter, sec, r->bias_dt, r->act_buf, r->act, r->limit,
-                                  r->alpha));
+        GW_HIP(gw::launch_gate_up(L, r->route_plan, fused ? &route : nullptr, a->tokens, a->x,
+                                  a->x_dtype, (int)r->hidden, (int)r->inter, sec, r->bias_dt,
+                                  r->act_buf, r->act, r->limit, r->alpha));
     }
     {
         ProfScope ps(ctx, "down");

@@ -146,20 +146,37 @@ template <> __device__ __forceinline__ float block_dot<DT_F32>(const WBlock<DT_F
 // --- activation vector staging ---------------------------------------------
 
 // Copies one activation vector of `n` elements (n % 32 == 0) of dtype XK from
-// global memory into LDS layout XL<XK>.  All threads of the block participate.
+// global memory into LDS layout XL<XK>, using threads [tid0, tid0 + nthr) of
+// the block.  16-byte loads when the source is 16-byte aligned; the loop is
+// unrolled so a thread's loads are all in flight before its first LDS store.
+template <int XK>
+__device__ __forceinline__ void stage_vector(uint32_t *dst, const void *src, int n, int tid,
+                                             int nthr)
+{
+    constexpr int BD = XL<XK>::kBlockDw;
+    if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+        constexpr int Q = XK == DT_F32 ? 8 : 4;        // 16-byte chunks of data per block
+        constexpr int BQ = BD / 4;                      // 16-byte chunks per block in LDS
+        const uint4 *s = static_cast<const uint4 *>(src);
+        uint4 *d = reinterpret_cast<uint4 *>(dst);
+        const int n4 = XK == DT_F32 ? n / 4 : n / 8;
+#pragma unroll 4
+        for (int i = tid; i < n4; i += nthr) d[(i / Q) * BQ + (i % Q)] = s[i];
+    } else if constexpr (XK == DT_F32) {
+        const float *s = static_cast<const float *>(src);
+#pragma unroll 4
+        for (int i = tid; i < n; i += nthr) dst[(i >> 5) * BD + (i & 31)] = __float_as_uint(s[i]);
+    } else {
+        const uint32_t *s = static_cast<const uint32_t *>(src);   // element pairs
+#pragma unroll 4
+        for (int i = tid; i < n / 2; i += nthr) dst[(i >> 4) * BD + (i & 15)] = s[i];
+    }
+}
+
 template <int XK>
 __device__ __forceinline__ void stage_vector(uint32_t *dst, const void *src, int n)
 {
-    constexpr int BD = XL<XK>::kBlockDw;
-    if constexpr (XK == DT_F32) {
-        const float *s = static_cast<const float *>(src);
-        for (int i = threadIdx.x; i < n; i += blockDim.x)
-            dst[(i >> 5) * BD + (i & 31)] = __float_as_uint(s[i]);
-    } else {
-        const uint32_t *s = static_cast<const uint32_t *>(src);   // element pairs
-        for (int i = threadIdx.x; i < n / 2; i += blockDim.x)
-            dst[(i >> 4) * BD + (i & 15)] = s[i];
-    }
+    stage_vector<XK>(dst, src, n, threadIdx.x, blockDim.x);
 }
 
 // --- small numerics ----------------------------------------------------------

@@ -15,6 +15,8 @@
 // Rows are split over a fixed grid in contiguous, balanced ranges (the
 // reference's persistent kernel, expert.metal:138-183, strides rows over 64
 // threadgroups instead).
+#include <type_traits>
+
 #include "gw_device.h"
 #include "gw_launch.h"
 
@@ -22,17 +24,47 @@ namespace gw {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kMMax = 8;   // column blocks per lane per row chunk
+// Weight streams are read through explicitly global (address space 1)
+// pointers.  Expert bases come out of the LDS-resident plan as generic
+// pointers; left generic, the loads become flat loads, which also count
+// against lgkmcnt, so every LDS read of the activations would wait for all
+// outstanding weight loads and the double buffering below would be lost.
+typedef const __attribute__((address_space(1))) u32x4 g_u32x4;
+typedef const __attribute__((address_space(1))) uint8_t g_u8;
+
+__device__ __forceinline__ u32x4 load_block(const uint8_t *row, int cb)
+{
+    return __builtin_nontemporal_load((g_u32x4 *)row + cb);
+}
+
+__device__ __forceinline__ uint32_t load_scale(const uint8_t *row, int cb)
+{
+    return ((g_u8 *)row)[cb];
+}
+
+// Shape classes: TPR lanes per row, M column blocks per lane (per chunk of
+// M*TPR blocks).  Compile-time, so every stage issues a fixed number of loads
+// and the compiler can wait for exactly the older stage (s_waitcnt vmcnt(N))
+// instead of draining the prefetched one too.
+template <int TPR_, int M_> struct Shape {
+    static constexpr int TPR = TPR_;
+    static constexpr int M = M_;
+};
+using S0 = Shape<8, 1>;    // bpr <= 8
+using S1 = Shape<8, 3>;    // bpr <= 24   (Qwen3 down: 24)
+using S2 = Shape<16, 4>;   // bpr <= 64   (Qwen3 gate_up: 64)
+using S3 = Shape<16, 6>;   // bpr <= 96   (GPT-OSS: 90)
+using S4 = Shape<16, 8>;   // wider rows, in chunks of 128 blocks
 
 RowShape row_shape(int bpr)
 {
-    // Pick lanes-per-row so M*TPR covers bpr with little waste.
     RowShape s;
+    s.chunks = 1;
     if (bpr <= 8) { s.tpr = 8; s.m = 1; }
-    else if (bpr <= 24) { s.tpr = 8; s.m = (bpr + 7) / 8; }
-    else { s.tpr = 16; s.m = (bpr + 15) / 16; }
-    if (s.m > kMMax) { s.chunks = (bpr + kMMax * s.tpr - 1) / (kMMax * s.tpr); s.m = kMMax; }
-    else s.chunks = 1;
+    else if (bpr <= 24) { s.tpr = 8; s.m = 3; }
+    else if (bpr <= 64) { s.tpr = 16; s.m = 4; }
+    else if (bpr <= 96) { s.tpr = 16; s.m = 6; }
+    else { s.tpr = 16; s.m = 8; s.chunks = (bpr + 127) / 128; }
     return s;
 }
 
@@ -50,17 +82,43 @@ __device__ __forceinline__ void widen_u(const u32x4 &w, WBlock<DT_F32> &o)
 template <int MT> struct RowRef {
     const uint8_t *packed;   // first block of the row
     const uint8_t *scales;   // first scale byte of the row
+    const uint8_t *bias;     // the row's bias element (any readable address if none)
     int ntok;                // activation vectors this row is dotted with
     int xoff[MT];            // LDS dword offset of each vector
 };
 
-template <int MT> struct Stage {
-    u32x4 w[kMMax];
-    uint32_t s[kMMax];
+template <int MT, int M> struct Stage {
+    u32x4 w[M];
+    uint32_t s[M];
+    uint32_t bw;             // aligned dword holding the row's bias
+    int bshift;              // bit offset of a bf16 bias within bw
     int item, chunk, ntok;
     int xoff[MT];
     bool valid;
 };
+
+// The bias element is read with the stage as the aligned dword containing it
+// (one load whatever the dtype), so the epilogue needs no young load.
+__device__ __forceinline__ float decode_bias(uint32_t bw, int bshift, int bias_dt)
+{
+    if (bias_dt < 0) return 0.0f;
+    if (bias_dt == DT_F32) return __uint_as_float(bw);
+    const uint16_t b = (uint16_t)(bw >> bshift);
+    return bias_dt == DT_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+// a = q*d + r for 0 <= a < 2^22, without a loop or an integer divide: the
+// float quotient is off by at most one and is corrected with selects (the
+// engine keeps control flow out of its load path).
+__device__ __forceinline__ void divmod_small(int a, int d, float inv_d, int &q, int &r)
+{
+    q = (int)((float)a * inv_d);
+    r = a - q * d;
+    q = r < 0 ? q - 1 : q;
+    r = r < 0 ? r + d : r;
+    q = r >= d ? q + 1 : q;
+    r = r >= d ? r - d : r;
+}
 
 template <int TPR> __device__ __forceinline__ float seg_sum(float v)
 {
@@ -69,47 +127,49 @@ template <int TPR> __device__ __forceinline__ float seg_sum(float v)
     return v;
 }
 
-template <int MT, int TPR, class RowFn>
-__device__ __forceinline__ void issue(Stage<MT> &S, int it, int chunks, int M, int bpr,
+// Issues the M block loads (and M scale loads) of one stage.  Every lane issues
+// all of them: a row past the end re-reads the last row, a column past the end
+// re-reads the row's last block; consume() ignores those values.
+template <int MT, class SH, class RowFn>
+__device__ __forceinline__ void issue(Stage<MT, SH::M> &S, int it, int chunks, int bpr,
                                       int n_items, RowFn &rowfn)
 {
-    constexpr int RG = kNT / TPR;
-    const int rg = it / chunks;
+    constexpr int TPR = SH::TPR, M = SH::M, RG = kNT / TPR;
+    const int rg = chunks == 1 ? it : it / chunks;
     const int c = it - rg * chunks;
     const int seg = threadIdx.x / TPR, lane = threadIdx.x % TPR;
     const int item = rg * RG + seg;
     S.item = item;
     S.chunk = c;
     S.valid = item < n_items;
-    RowRef<MT> ref;
-    ref.ntok = 0;
-    if (S.valid) ref = rowfn(item);
-    S.ntok = ref.ntok;
+    const RowRef<MT> ref = rowfn(S.valid ? item : n_items - 1);
+    S.ntok = S.valid ? ref.ntok : 0;
 #pragma unroll
-    for (int t = 0; t < MT; ++t) S.xoff[t] = S.valid ? ref.xoff[t] : 0;
-    const int cb0 = c * kMMax * TPR + lane;
+    for (int t = 0; t < MT; ++t) S.xoff[t] = ref.xoff[t];
+    const int cb0 = c * M * TPR + lane;
 #pragma unroll
-    for (int m = 0; m < kMMax; ++m) {
-        const int cb = cb0 + m * TPR;
-        if (m < M && S.valid && cb < bpr) {
-            S.w[m] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4 *>(ref.packed) + cb);
-            S.s[m] = ref.scales[cb];
-        }
+    for (int m = 0; m < M; ++m) {
+        const int cb = min(cb0 + m * TPR, bpr - 1);
+        S.w[m] = load_block(ref.packed, cb);
+        S.s[m] = load_scale(ref.scales, cb);
     }
+    const uintptr_t ba = reinterpret_cast<uintptr_t>(ref.bias);
+    S.bshift = (int)(ba & 2u) * 8;
+    S.bw = *(const __attribute__((address_space(1))) uint32_t *)(ba & ~(uintptr_t)3);
 }
 
-template <int XK, int MT, int TPR, class EpiFn>
-__device__ __forceinline__ void consume(Stage<MT> &S, float (&acc)[MT], int chunks, int M,
+template <int XK, int MT, class SH, class EpiFn>
+__device__ __forceinline__ void consume(Stage<MT, SH::M> &S, float (&acc)[MT], int chunks,
                                         int bpr, const uint32_t *xs, EpiFn &epi)
 {
+    constexpr int TPR = SH::TPR, M = SH::M;
     constexpr int BD = XL<XK>::kBlockDw;
     const int lane = threadIdx.x % TPR;
-    const int cb0 = S.chunk * kMMax * TPR + lane;
+    const int cb0 = S.chunk * M * TPR + lane;
 #pragma unroll
-    for (int m = 0; m < kMMax; ++m) {
+    for (int m = 0; m < M; ++m) {
         const int cb = cb0 + m * TPR;
-        if (m < M && S.valid && cb < bpr) {
+        if (S.valid && cb < bpr) {
             WBlock<XK> wb;
             widen_u(S.w[m], wb);
             const float sc = decode_scale(S.s[m]);
@@ -122,56 +182,218 @@ __device__ __forceinline__ void consume(Stage<MT> &S, float (&acc)[MT], int chun
     if (S.chunk == chunks - 1) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) acc[t] = seg_sum<TPR>(acc[t]);
-        epi(S.item, S.valid, S.ntok, acc);
+        epi(S.item, S.valid, S.ntok, acc, S.bw, S.bshift);
 #pragma unroll
         for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
     }
 }
 
 // Runs `n_items` rows (RowFn maps item -> RowRef) through the engine, calling
-// EpiFn(item, valid, ntok, acc) once per row group with every lane holding its
-// row's fp32 sums.  All threads of the workgroup must call it.
-template <int XK, int MT, int TPR, class RowFn, class EpiFn>
-__device__ __forceinline__ void row_engine(int n_items, int chunks, int M, int bpr,
+// EpiFn(item, valid, ntok, acc, bias_word, bias_shift) once per row group with
+// every lane holding its row's fp32 sums.  All threads of the workgroup must
+// call it.
+//
+// Stages go in straight-line batches of kDepth: all loads of a batch are
+// issued (unconditionally; stages past the end re-read the last row and are
+// never consumed), then the stages are consumed in order.  With no control
+// flow between a load and its use, the compiler waits for exactly the stage it
+// consumes (s_waitcnt vmcnt(N)) while the younger stages stay in flight.
+// Grids are sized so a workgroup's rows fit one batch on the decode shapes.
+constexpr int kDepth = 3;
+
+template <int XK, int MT, class SH, class RowFn, class EpiFn>
+__device__ __forceinline__ void row_engine(int n_items, int chunks, int bpr,
                                            const uint32_t *xs, RowFn rowfn, EpiFn epi)
 {
-    constexpr int RG = kNT / TPR;
+    constexpr int RG = kNT / SH::TPR;
     const int nit = ((n_items + RG - 1) / RG) * chunks;
     float acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
-    Stage<MT> A, B;
-    if (nit > 0) issue<MT, TPR>(A, 0, chunks, M, bpr, n_items, rowfn);
-    for (int it = 0; it < nit; it += 2) {
-        if (it + 1 < nit) issue<MT, TPR>(B, it + 1, chunks, M, bpr, n_items, rowfn);
-        consume<XK, MT, TPR>(A, acc, chunks, M, bpr, xs, epi);
-        if (it + 1 < nit) {
-            if (it + 2 < nit) issue<MT, TPR>(A, it + 2, chunks, M, bpr, n_items, rowfn);
-            consume<XK, MT, TPR>(B, acc, chunks, M, bpr, xs, epi);
-        }
+    for (int base = 0; base < nit; base += kDepth) {
+        Stage<MT, SH::M> S[kDepth];
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) issue<MT, SH>(S[d], base + d, chunks, bpr, n_items, rowfn);
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) consume<XK, MT, SH>(S[d], acc, chunks, bpr, xs, epi);
     }
 }
 
+static_assert(sizeof(Plan) % 16 == 0, "plans are copied in 16-byte chunks");
+
 __device__ __forceinline__ void copy_plan(Plan *dst, const Plan *src)
 {
-    const uint32_t *s = reinterpret_cast<const uint32_t *>(src);
-    uint32_t *d = reinterpret_cast<uint32_t *>(dst);
-    for (int i = threadIdx.x; i < (int)(sizeof(Plan) / 4); i += blockDim.x) d[i] = s[i];
+    const uint4 *s = reinterpret_cast<const uint4 *>(src);
+    uint4 *d = reinterpret_cast<uint4 *>(dst);
+    for (int i = threadIdx.x; i < (int)(sizeof(Plan) / 16); i += blockDim.x) d[i] = s[i];
 }
+
+// ---------------------------------------------------------------------------
+// Routing by one wave (Router.select, Router.swift:78-98, plus the demand map
+// of TransformerLayer.swift:175-181), register resident.
+//
+// The selection sort's permutation lives in registers: lane l holds positions
+// l, l+64, ... (R per lane) as (expert id, logit) pairs.  At position p the
+// reference keeps the first position >= p holding the largest logit (strict
+// `>` scan), or p itself when logits[order[p]] is NaN; positions are swapped
+// exactly as `order.swapAt(p, best)` does, so ties resolve as in the reference.
+// ---------------------------------------------------------------------------
+
+template <int R>
+__device__ __forceinline__ void route_wave(const float *__restrict__ logits, int E, int K,
+                                           int T, const uint8_t *experts_base, int64_t stride,
+                                           Plan *plan, int32_t *ids_out, float *w_out)
+{
+    const int lane = threadIdx.x & 63;
+    int my_e = -1;
+    float my_w = 0.0f;
+    for (int t = 0; t < T; ++t) {
+        int ord[R];
+        float ov[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int i = lane + 64 * r;
+            ord[r] = i;
+            ov[r] = i < E ? logits[(int64_t)t * E + i] : 0.0f;
+        }
+        for (int pos = 0; pos < K; ++pos) {
+            float bv = 0.0f;
+            int bp = -1;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int i = lane + 64 * r;
+                const float v = ov[r];
+                if (i >= pos && i < E && !__builtin_isnan(v) && (bp < 0 || v > bv)) {
+                    bv = v;
+                    bp = i;
+                }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float v2 = __shfl_xor(bv, o);
+                const int p2 = __shfl_xor(bp, o);
+                const bool take = p2 >= 0 && (bp < 0 || v2 > bv || (v2 == bv && p2 < bp));
+                bv = take ? v2 : bv;
+                bp = take ? p2 : bp;
+            }
+            const int pr = pos >> 6, pl = pos & 63;
+            float v_pos = 0.0f;
+            int o_pos = 0;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (r == pr) {
+                    v_pos = __shfl(ov[r], pl);
+                    o_pos = __shfl(ord[r], pl);
+                }
+            const int best = (bp < 0 || __builtin_isnan(v_pos)) ? pos : bp;
+            const int br = best >> 6, bl = best & 63;
+            float v_b = 0.0f;
+            int o_b = 0;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (r == br) {
+                    v_b = __shfl(ov[r], bl);
+                    o_b = __shfl(ord[r], bl);
+                }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (r == pr && lane == pl) {
+                    ord[r] = o_b;
+                    ov[r] = v_b;
+                }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (r == br && lane == bl) {
+                    ord[r] = o_pos;
+                    ov[r] = v_pos;
+                }
+        }
+        // Positions 0..K-1 are lanes 0..K-1, register 0.  Softmax over the K
+        // selected logits with the maximum subtracted, summed in order.
+        const int sid = ord[0];
+        const float sv = ov[0];
+        float peak = __shfl(sv, 0);
+        for (int i = 1; i < K; ++i) {
+            const float v = __shfl(sv, i);
+            if (v > peak) peak = v;
+        }
+        const float ex = expf(sv - peak);
+        float total = 0.0f;
+        for (int i = 0; i < K; ++i) total += __shfl(ex, i);
+        const float w = ex / total;
+        const int src = lane - t * K;
+        const bool mine = src >= 0 && src < K;
+        const int e_src = __shfl(sid, mine ? src : 0);
+        const float w_src = __shfl(w, mine ? src : 0);
+        if (mine) {
+            my_e = e_src;
+            my_w = w_src;
+        }
+        if (ids_out && lane < K) ids_out[(int64_t)t * K + lane] = sid;
+        if (w_out && lane < K) w_out[(int64_t)t * K + lane] = w;
+    }
+
+    // Expert-major grouping of the T*K (token, rank) entries by first appearance.
+    const int n = T * K;
+    int first = -1, before = 0, same = 0;
+    for (int j = 0; j < n; ++j) {
+        const int ej = __shfl(my_e, j);
+        if (lane < n && ej == my_e) {
+            if (first < 0) first = j;
+            if (j < lane) ++before;
+            ++same;
+        }
+    }
+    const bool leader = lane < n && first == lane;
+    const unsigned long long leaders = __ballot(leader);
+    int slot0 = 0;
+    for (int j = 0; j < n; ++j) {
+        const int fj = __shfl(first, j);
+        if (lane < n && fj < first) ++slot0;
+    }
+    if (lane < n) {
+        const int gi = __popcll(leaders & ((1ull << first) - 1ull));
+        const int slot = slot0 + before;
+        const int t = lane / K, r = lane - (lane / K) * K;
+        plan->slot_token[slot] = t;
+        plan->slot_group[slot] = gi;
+        plan->slot_weight[slot] = my_w;
+        plan->tok_slots[t][r] = slot;
+        if (leader) {
+            plan->group_base[gi] = experts_base + (int64_t)my_e * stride;
+            plan->group_slot0[gi] = slot0;
+            plan->group_ntok[gi] = same;
+        }
+    }
+    if (lane < T) {
+        plan->tok_global[lane] = lane;
+        plan->tok_nslots[lane] = K;
+    }
+    if (lane == 0) {
+        plan->ngroups = __popcll(leaders);
+        plan->nslots = n;
+        plan->ntokens = T;
+        plan->pad0 = 0;
+    }
+}
+
+constexpr int kFusedRouteR = 4;      // fused routing handles up to 256 experts
+constexpr int kMaxExperts = 1024;    // the standalone route kernel, up to 1024
 
 // ---------------------------------------------------------------------------
 // Standalone GEMV (mxfp4_gemv / mxfp4_gemv_bias*, dequant_gemv.metal:37-67,
 // expert.metal:46-368)
 // ---------------------------------------------------------------------------
 
-template <int XK, int TPR>
+template <int XK, class SH>
 __global__ __launch_bounds__(kNT) void gemv_kernel(const uint8_t *__restrict__ packed,
                                                    const uint8_t *__restrict__ scales,
                                                    const void *__restrict__ bias, int bias_dt,
                                                    const void *__restrict__ x,
                                                    float *__restrict__ y, int rows, int bpr,
-                                                   int M, int chunks)
+                                                   int chunks)
 {
+    constexpr int TPR = SH::TPR;
     extern __shared__ uint32_t lds[];
     uint32_t *xs = lds;
     stage_vector<XK>(xs, x, bpr * 32);
@@ -179,22 +401,21 @@ __global__ __launch_bounds__(kNT) void gemv_kernel(const uint8_t *__restrict__ p
     const int r0 = (int)((int64_t)blockIdx.x * rows / gridDim.x);
     const int r1 = (int)((int64_t)(blockIdx.x + 1) * rows / gridDim.x);
     const int64_t row_bytes = (int64_t)bpr * 16;
+    const int bsz = bias_dt == DT_F32 ? 4 : 2;
     auto rowfn = [&](int item) {
         RowRef<1> r;
         const int64_t row = r0 + item;
         r.packed = packed + row * row_bytes;
         r.scales = scales + row * bpr;
+        r.bias = bias_dt >= 0 ? static_cast<const uint8_t *>(bias) + row * bsz : r.scales;
         r.ntok = 1;
         r.xoff[0] = 0;
         return r;
     };
-    auto epi = [&](int item, bool valid, int, float (&acc)[1]) {
-        if (valid && (threadIdx.x % TPR) == 0) {
-            const int row = r0 + item;
-            y[row] = acc[0] + load_bias(bias, bias_dt, row);
-        }
+    auto epi = [&](int item, bool valid, int, float (&acc)[1], uint32_t bw, int bsh) {
+        if (valid && (threadIdx.x % TPR) == 0) y[r0 + item] = acc[0] + decode_bias(bw, bsh, bias_dt);
     };
-    row_engine<XK, 1, TPR>(r1 - r0, chunks, M, bpr, xs, rowfn, epi);
+    row_engine<XK, 1, SH>(r1 - r0, chunks, bpr, xs, rowfn, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -204,12 +425,13 @@ __global__ __launch_bounds__(kNT) void gemv_kernel(const uint8_t *__restrict__ p
 // of one wave, so the activation is applied straight from the reduction.
 // ---------------------------------------------------------------------------
 
-template <int XK, int MT, int TPR>
+template <int XK, int MT, class SH>
 __global__ __launch_bounds__(kNT) void gate_up_kernel(
-    const Plan *__restrict__ gplan, const void *__restrict__ x, int hidden, int inter,
-    Sections sec, int bias_dt, uint16_t *__restrict__ act, int act_kind, float limit,
-    float alpha, int max_tokens, int M, int chunks)
+    Plan *__restrict__ gplan, RouteArgs route, const void *__restrict__ x, int hidden,
+    int inter, Sections sec, int bias_dt, uint16_t *__restrict__ act, int act_kind,
+    float limit, float alpha, int max_tokens, int chunks)
 {
+    constexpr int TPR = SH::TPR;
     extern __shared__ uint32_t lds[];
     constexpr int BD = XL<XK>::kBlockDw;
     constexpr int ES = XK == DT_F32 ? 4 : 2;
@@ -217,27 +439,59 @@ __global__ __launch_bounds__(kNT) void gate_up_kernel(
     uint32_t *xs = lds + sizeof(Plan) / 4;
     const int bpr = hidden >> 5;
     const int xstride = bpr * BD;
-    copy_plan(plan, gplan);
-    __syncthreads();
-    const int ntokens = plan->ntokens;
-    for (int t = 0; t < ntokens && t < max_tokens; ++t)
-        stage_vector<XK>(xs + t * xstride,
-                         static_cast<const char *>(x) + (int64_t)plan->tok_global[t] * hidden * ES,
-                         hidden);
-    __syncthreads();
+    if (route.logits) {
+        // Wave 0 routes (every workgroup, redundantly: 4 x 128 logits) while the
+        // other waves stage the inputs, which are rows 0..T-1 of x.
+        if (threadIdx.x < 64) {
+            route_wave<kFusedRouteR>(route.logits, route.experts, route.top_k, route.tokens,
+                                     route.experts_base, route.stride, plan,
+                                     blockIdx.x == 0 ? route.ids_out : nullptr,
+                                     blockIdx.x == 0 ? route.w_out : nullptr);
+        } else {
+            for (int t = 0; t < route.tokens && t < max_tokens; ++t)
+                stage_vector<XK>(xs + t * xstride,
+                                 static_cast<const char *>(x) + (int64_t)t * hidden * ES, hidden,
+                                 threadIdx.x - 64, kNT - 64);
+        }
+        __syncthreads();
+        if (blockIdx.x == 0) copy_plan(gplan, plan);   // for the down kernel
+    } else {
+        copy_plan(plan, gplan);
+        __syncthreads();
+        const int ntokens = plan->ntokens;
+        for (int t = 0; t < ntokens && t < max_tokens; ++t)
+            stage_vector<XK>(xs + t * xstride,
+                             static_cast<const char *>(x) +
+                                 (int64_t)plan->tok_global[t] * hidden * ES,
+                             hidden);
+        __syncthreads();
+    }
 
     const int64_t total = (int64_t)plan->ngroups * inter;   // (group, pair) space
     const int64_t p0 = (int64_t)blockIdx.x * total / gridDim.x;
     const int64_t p1 = (int64_t)(blockIdx.x + 1) * total / gridDim.x;
     const int64_t row_bytes = (int64_t)bpr * 16;
+    const int bsz = bias_dt == DT_F32 ? 4 : 2;
+    // (group, pair) of the range start, once; items step through pairs with
+    // 32-bit arithmetic (a workgroup's range spans few groups).
+    const int g_start = (int)(p0 / inter);
+    const int i_start = (int)(p0 - (int64_t)g_start * inter);
+    const float inv_inter = 1.0f / (float)inter;
+    auto locate = [&](int item, int &g, int &i) {
+        int q, r;
+        divmod_small(i_start + (item >> 1), inter, inv_inter, q, r);
+        g = g_start + q;
+        i = r;
+    };
     auto rowfn = [&](int item) {
         RowRef<MT> r;
-        const int64_t p = p0 + (item >> 1);
-        const int g = (int)(p / inter);
-        const int64_t row = 2 * (p - (int64_t)g * inter) + (item & 1);
+        int g, i;
+        locate(item, g, i);
+        const int row = 2 * i + (item & 1);
         const uint8_t *base = plan->group_base[g];
         r.packed = base + sec.gu_blocks + row * row_bytes;
         r.scales = base + sec.gu_scales + row * bpr;
+        r.bias = bias_dt >= 0 ? base + sec.gu_bias + row * bsz : r.scales;
         r.ntok = plan->group_ntok[g];
         const int s0 = plan->group_slot0[g];
 #pragma unroll
@@ -245,18 +499,17 @@ __global__ __launch_bounds__(kNT) void gate_up_kernel(
             r.xoff[t] = t < r.ntok ? plan->slot_token[s0 + t] * xstride : 0;
         return r;
     };
-    auto epi = [&](int item, bool valid, int ntok, float (&acc)[MT]) {
+    auto epi = [&](int item, bool valid, int ntok, float (&acc)[MT], uint32_t bw, int bsh) {
         float up[MT];
 #pragma unroll
         for (int t = 0; t < MT; ++t) up[t] = __shfl_down(acc[t], TPR);
+        const float b_own = decode_bias(bw, bsh, bias_dt);
+        const float b_next = __shfl_down(b_own, TPR);
         if (valid && (item & 1) == 0 && (threadIdx.x % TPR) == 0) {
-            const int64_t p = p0 + (item >> 1);
-            const int g = (int)(p / inter);
-            const int64_t i = p - (int64_t)g * inter;
-            const uint8_t *base = plan->group_base[g];
-            const void *bias = bias_dt >= 0 ? (const void *)(base + sec.gu_bias) : nullptr;
-            const float bg = load_bias(bias, bias_dt, 2 * i);
-            const float bu = load_bias(bias, bias_dt, 2 * i + 1);
+            int g, i;
+            locate(item, g, i);
+            const float bg = b_own;    // gate row 2i
+            const float bu = b_next;   // up row 2i+1 (the next segment)
             const int s0 = plan->group_slot0[g];
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
@@ -268,7 +521,7 @@ __global__ __launch_bounds__(kNT) void gate_up_kernel(
             }
         }
     };
-    row_engine<XK, MT, TPR>((int)(2 * (p1 - p0)), chunks, M, bpr, xs, rowfn, epi);
+    row_engine<XK, MT, SH>((int)(2 * (p1 - p0)), chunks, bpr, xs, rowfn, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -277,12 +530,13 @@ __global__ __launch_bounds__(kNT) void gate_up_kernel(
 // combine happens in LDS without atomics, in each token's slot order.
 // ---------------------------------------------------------------------------
 
-template <int MT, int TPR>
+template <int MT, class SH>
 __global__ __launch_bounds__(kNT) void down_kernel(
     const Plan *__restrict__ gplan, const uint16_t *__restrict__ act, int hidden, int inter,
     Sections sec, int bias_dt, float *__restrict__ out, uint16_t *__restrict__ out_bf16,
-    int accumulate, int smax, int nmax, int M, int chunks)
+    int accumulate, int smax, int nmax, int chunks, int prestage)
 {
+    constexpr int TPR = SH::TPR;
     extern __shared__ uint32_t lds[];
     constexpr int BD = XL<DT_F16>::kBlockDw;
     Plan *plan = reinterpret_cast<Plan *>(lds);
@@ -290,7 +544,12 @@ __global__ __launch_bounds__(kNT) void down_kernel(
     const int astride = bpr * BD;
     uint32_t *as = lds + sizeof(Plan) / 4;                          // [smax][astride]
     float *vals = reinterpret_cast<float *>(as + smax * astride);   // [kMaxSlots][nmax]
+    // Activations are stored slot-major, so the first `prestage` slots (the
+    // whole first chunk when it holds every slot) are staged without waiting
+    // for the plan; both copies are in flight together.
     copy_plan(plan, gplan);
+    for (int s = 0; s < prestage; ++s)
+        stage_vector<DT_F16>(as + s * astride, act + (int64_t)s * inter, inter);
     __syncthreads();
 
     const int r0 = (int)((int64_t)blockIdx.x * hidden / gridDim.x);
@@ -298,6 +557,7 @@ __global__ __launch_bounds__(kNT) void down_kernel(
     const int n = r1 - r0;
     const int ngroups = plan->ngroups;
     const int64_t row_bytes = (int64_t)bpr * 16;
+    const int bsz = bias_dt == DT_F32 ? 4 : 2;
 
     int g = 0;
     while (g < ngroups) {
@@ -309,41 +569,44 @@ __global__ __launch_bounds__(kNT) void down_kernel(
             ++g1;
         }
         if (g1 == g) break;   // a group wider than the staging area (the host prevents it)
-        for (int s = s0; s < s1; ++s)
-            stage_vector<DT_F16>(as + (s - s0) * astride, act + (int64_t)s * inter, inter);
-        __syncthreads();
+        const int staged = s0 == 0 ? prestage : 0;      // slots already in LDS
+        if (s1 > s0 + staged) {
+            for (int s = s0 + staged; s < s1; ++s)
+                stage_vector<DT_F16>(as + (s - s0) * astride, act + (int64_t)s * inter, inter);
+            __syncthreads();
+        }
         const int gbase = g;
+        const float inv_n = 1.0f / (float)n;
+        auto split = [&](int item, int &gl, int &q) { divmod_small(item, n, inv_n, gl, q); };
         auto rowfn = [&](int item) {
             RowRef<MT> r;
-            const int gl = item / n;
-            const int q = item - gl * n;
+            int gl, q;
+            split(item, gl, q);
             const int gg = gbase + gl;
             const uint8_t *base = plan->group_base[gg];
             const int64_t row = r0 + q;
             r.packed = base + sec.dn_blocks + row * row_bytes;
             r.scales = base + sec.dn_scales + row * bpr;
+            r.bias = bias_dt >= 0 ? base + sec.dn_bias + row * bsz : r.scales;
             r.ntok = plan->group_ntok[gg];
             const int sl = plan->group_slot0[gg] - s0;
 #pragma unroll
             for (int t = 0; t < MT; ++t) r.xoff[t] = (sl + (t < r.ntok ? t : 0)) * astride;
             return r;
         };
-        auto epi = [&](int item, bool valid, int ntok, float (&acc)[MT]) {
+        auto epi = [&](int item, bool valid, int ntok, float (&acc)[MT], uint32_t bw, int bsh) {
             if (valid && (threadIdx.x % TPR) == 0) {
-                const int gl = item / n;
-                const int q = item - gl * n;
+                int gl, q;
+                split(item, gl, q);
                 const int gg = gbase + gl;
-                const void *bias = bias_dt >= 0
-                                       ? (const void *)(plan->group_base[gg] + sec.dn_bias)
-                                       : nullptr;
-                const float b = load_bias(bias, bias_dt, r0 + q);
+                const float b = decode_bias(bw, bsh, bias_dt);
                 const int sg = plan->group_slot0[gg];
 #pragma unroll
                 for (int t = 0; t < MT; ++t)
                     if (t < ntok) vals[(sg + t) * nmax + q] = acc[t] + b;
             }
         };
-        row_engine<DT_F16, MT, TPR>((g1 - g) * n, chunks, M, bpr, as, rowfn, epi);
+        row_engine<DT_F16, MT, SH>((g1 - g) * n, chunks, bpr, as, rowfn, epi);
         __syncthreads();
         g = g1;
     }
@@ -388,119 +651,16 @@ __global__ __launch_bounds__(256) void router_kernel(const void *__restrict__ W,
     if (lane == 0) logits[(int64_t)t * E + e] = acc + (b ? load_as_f32(b, b_dt, e) : 0.0f);
 }
 
-constexpr int kMaxExperts = 1024;
-
-// One wave.  Selection replicates the reference's partial selection sort
-// exactly, including its tie behaviour: at position p the sort keeps the
-// first position (in the partially permuted order) holding the largest
-// non-NaN logit, or p itself when logits[order[p]] is NaN.
-__global__ __launch_bounds__(64) void route_kernel(const float *__restrict__ logits, int E,
-                                                   int K, int T,
-                                                   const uint8_t *__restrict__ experts_base,
-                                                   int64_t stride, Plan *__restrict__ plan,
-                                                   int32_t *__restrict__ ids_out,
-                                                   float *__restrict__ w_out)
+// Standalone routing (more than 256 experts, or a host that wants the plan
+// only): one wave builds the plan in LDS and copies it out.
+__global__ __launch_bounds__(64) void route_kernel(RouteArgs route, Plan *__restrict__ gplan)
 {
-    __shared__ float lg[kMaxExperts];
-    __shared__ int ord[kMaxExperts];
-    __shared__ int sel_id[kMaxSlots];
-    __shared__ float sel_w[kMaxSlots];
-    __shared__ int first_of[kMaxSlots];
-    const int lane = threadIdx.x;
-
-    for (int t = 0; t < T; ++t) {
-        for (int i = lane; i < E; i += 64) {
-            lg[i] = logits[(int64_t)t * E + i];
-            ord[i] = i;
-        }
-        __syncthreads();
-        for (int pos = 0; pos < K; ++pos) {
-            float bv = 0.0f;
-            int bp = -1;
-            for (int i = pos + lane; i < E; i += 64) {
-                const float v = lg[ord[i]];
-                if (!__builtin_isnan(v) && (bp < 0 || v > bv)) { bv = v; bp = i; }
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o);
-                const int op = __shfl_xor(bp, o);
-                const bool take = op >= 0 && (bp < 0 || ov > bv || (ov == bv && op < bp));
-                bv = take ? ov : bv;
-                bp = take ? op : bp;
-            }
-            if (lane == 0) {
-                int best = bp;
-                if (__builtin_isnan(lg[ord[pos]]) || best < 0) best = pos;
-                const int tmp = ord[pos];
-                ord[pos] = ord[best];
-                ord[best] = tmp;
-            }
-            __syncthreads();
-        }
-        if (lane == 0) {
-            float peak = 0.0f;
-            for (int i = 0; i < K; ++i) {
-                const float v = lg[ord[i]];
-                if (i == 0 || v > peak) peak = v;
-            }
-            float e[kMaxTopK];
-            float total = 0.0f;
-            for (int i = 0; i < K; ++i) { e[i] = expf(lg[ord[i]] - peak); total += e[i]; }
-            for (int i = 0; i < K; ++i) {
-                sel_id[t * K + i] = ord[i];
-                sel_w[t * K + i] = e[i] / total;
-                if (ids_out) ids_out[(int64_t)t * K + i] = ord[i];
-                if (w_out) w_out[(int64_t)t * K + i] = e[i] / total;
-            }
-        }
-        __syncthreads();
-    }
-
-    // Expert-major grouping of the T*K (token, rank) entries by first appearance.
-    const int n = T * K;
-    int my_e = -1, first = lane, before = 0, same = 0;
-    if (lane < n) {
-        my_e = sel_id[lane];
-        first = -1;
-        for (int j = 0; j < n; ++j) {
-            if (sel_id[j] == my_e) {
-                if (first < 0) first = j;
-                if (j < lane) ++before;
-                ++same;
-            }
-        }
-        first_of[lane] = first;
-    }
+    __shared__ __align__(16) Plan plan;
+    route_wave<kMaxExperts / 64>(route.logits, route.experts, route.top_k, route.tokens,
+                                 route.experts_base, route.stride, &plan, route.ids_out,
+                                 route.w_out);
     __syncthreads();
-    const bool leader = lane < n && first == lane;
-    const unsigned long long leaders = __ballot(leader);
-    if (lane < n) {
-        const int gi = __popcll(leaders & ((1ull << first) - 1ull));
-        int slot0 = 0;
-        for (int j = 0; j < n; ++j) slot0 += first_of[j] < first ? 1 : 0;
-        const int slot = slot0 + before;
-        const int t = lane / K, r = lane - (lane / K) * K;
-        plan->slot_token[slot] = t;
-        plan->slot_group[slot] = gi;
-        plan->slot_weight[slot] = sel_w[lane];
-        plan->tok_slots[t][r] = slot;
-        if (leader) {
-            plan->group_base[gi] = experts_base + (int64_t)my_e * stride;
-            plan->group_slot0[gi] = slot0;
-            plan->group_ntok[gi] = same;
-        }
-    }
-    if (lane < T) {
-        plan->tok_global[lane] = lane;
-        plan->tok_nslots[lane] = K;
-    }
-    if (lane == 0) {
-        plan->ngroups = __popcll(leaders);
-        plan->nslots = n;
-        plan->ntokens = T;
-        plan->pad0 = 0;
-    }
+    copy_plan(gplan, &plan);
 }
 
 // ---------------------------------------------------------------------------
@@ -611,18 +771,14 @@ hipError_t launch_dequant(const Launch &L, const uint8_t *packed, const uint8_t 
 
 static int x_block_dw(int x_dt) { return x_dt == DT_F32 ? 36 : 20; }
 
-template <int XK>
-static hipError_t gemv_dispatch(const Launch &L, const RowShape &s, dim3 grid, size_t lds,
-                                const uint8_t *packed, const uint8_t *scales, const void *bias,
-                                int bias_dt, const void *x, float *y, int rows, int bpr)
+// Calls f(SH{}) with the shape class row_shape() chose.
+template <class F> static void with_shape(const RowShape &s, F &&f)
 {
-    if (s.tpr == 8)
-        hipLaunchKernelGGL((gemv_kernel<XK, 8>), grid, dim3(kNT), lds, L.stream, packed, scales,
-                           bias, bias_dt, x, y, rows, bpr, s.m, s.chunks);
-    else
-        hipLaunchKernelGGL((gemv_kernel<XK, 16>), grid, dim3(kNT), lds, L.stream, packed,
-                           scales, bias, bias_dt, x, y, rows, bpr, s.m, s.chunks);
-    return hipGetLastError();
+    if (s.tpr == 8 && s.m == 1) f(S0{});
+    else if (s.tpr == 8) f(S1{});
+    else if (s.m == 4) f(S2{});
+    else if (s.m == 6) f(S3{});
+    else f(S4{});
 }
 
 hipError_t launch_gemv(const Launch &L, const uint8_t *packed, const uint8_t *scales,
@@ -636,14 +792,19 @@ hipError_t launch_gemv(const Launch &L, const uint8_t *packed, const uint8_t *sc
     int grid = L.grid_a > 0 ? L.grid_a : 2 * L.cus;
     grid = grid < div_up(rows, rg) ? grid : div_up(rows, rg);
     const size_t lds = (size_t)bpr * x_block_dw(x_dt) * 4;
-    if (x_dt == DT_F32)
-        return gemv_dispatch<DT_F32>(L, s, dim3(grid), lds, packed, scales, bias, bias_dt, x, y,
-                                     rows, bpr);
-    if (x_dt == DT_F16)
-        return gemv_dispatch<DT_F16>(L, s, dim3(grid), lds, packed, scales, bias, bias_dt, x, y,
-                                     rows, bpr);
-    return gemv_dispatch<DT_BF16>(L, s, dim3(grid), lds, packed, scales, bias, bias_dt, x, y,
-                                  rows, bpr);
+    with_shape(s, [&](auto sh) {
+        using SH = decltype(sh);
+        if (x_dt == DT_F32)
+            hipLaunchKernelGGL((gemv_kernel<DT_F32, SH>), dim3(grid), dim3(kNT), lds, L.stream,
+                               packed, scales, bias, bias_dt, x, y, rows, bpr, s.chunks);
+        else if (x_dt == DT_F16)
+            hipLaunchKernelGGL((gemv_kernel<DT_F16, SH>), dim3(grid), dim3(kNT), lds, L.stream,
+                               packed, scales, bias, bias_dt, x, y, rows, bpr, s.chunks);
+        else
+            hipLaunchKernelGGL((gemv_kernel<DT_BF16, SH>), dim3(grid), dim3(kNT), lds, L.stream,
+                               packed, scales, bias, bias_dt, x, y, rows, bpr, s.chunks);
+    });
+    return hipGetLastError();
 }
 
 int gate_up_lds_bytes(int hidden, int x_dt, int max_tokens)
@@ -651,41 +812,42 @@ int gate_up_lds_bytes(int hidden, int x_dt, int max_tokens)
     return (int)sizeof(Plan) + max_tokens * (hidden / 32) * x_block_dw(x_dt) * 4;
 }
 
-template <int XK, int MT>
-static hipError_t gate_up_dispatch(const Launch &L, const RowShape &s, dim3 grid, size_t lds,
-                                   const Plan *plan, int max_tokens, const void *x, int hidden,
-                                   int inter, const Sections &sec, int bias_dt, uint16_t *act,
-                                   int act_kind, float limit, float alpha)
+hipError_t launch_gate_up(const Launch &L, Plan *plan, const RouteArgs *route, int max_tokens,
+                          const void *x, int x_dt, int hidden, int inter, const Sections &sec,
+                          int bias_dt, uint16_t *act, int act_kind, float limit, float alpha)
 {
-    if (s.tpr == 8)
-        hipLaunchKernelGGL((gate_up_kernel<XK, MT, 8>), grid, dim3(kNT), lds, L.stream, plan, x,
-                           hidden, inter, sec, bias_dt, act, act_kind, limit, alpha,
-                           max_tokens, s.m, s.chunks);
-    else
-        hipLaunchKernelGGL((gate_up_kernel<XK, MT, 16>), grid, dim3(kNT), lds, L.stream, plan,
-                           x, hidden, inter, sec, bias_dt, act, act_kind, limit, alpha,
-                           max_tokens, s.m, s.chunks);
-    return hipGetLastError();
-}
-
-hipError_t launch_gate_up(const Launch &L, const Plan *plan, int max_tokens, const void *x,
-                          int x_dt, int hidden, int inter, const Sections &sec, int bias_dt,
-                          uint16_t *act, int act_kind, float limit, float alpha)
-{
+    RouteArgs r = {};
+    if (route) {
+        if (route->experts > 64 * kFusedRouteR || route->top_k > kMaxTopK ||
+            route->tokens > kMaxTokens || route->tokens != max_tokens)
+            return hipErrorInvalidValue;
+        r = *route;
+    }
     const RowShape s = row_shape(hidden / 32);
     const int grid = L.grid_a > 0 ? L.grid_a : 2 * L.cus;
     const size_t lds = (size_t)gate_up_lds_bytes(hidden, x_dt, max_tokens);
-    const bool one = max_tokens == 1;
-#define GW_GU(XK)                                                                             \
-    return one ? gate_up_dispatch<XK, 1>(L, s, dim3(grid), lds, plan, max_tokens, x, hidden, \
-                                         inter, sec, bias_dt, act, act_kind, limit, alpha)   \
-               : gate_up_dispatch<XK, kMaxTokens>(L, s, dim3(grid), lds, plan, max_tokens,   \
-                                                  x, hidden, inter, sec, bias_dt, act,       \
-                                                  act_kind, limit, alpha)
-    if (x_dt == DT_F32) { GW_GU(DT_F32); }
-    if (x_dt == DT_F16) { GW_GU(DT_F16); }
-    GW_GU(DT_BF16);
-#undef GW_GU
+    with_shape(s, [&](auto sh) {
+        using SH = decltype(sh);
+        auto go = [&](auto xk, auto mt) {
+            constexpr int XK = decltype(xk)::value, MT = decltype(mt)::value;
+            hipLaunchKernelGGL((gate_up_kernel<XK, MT, SH>), dim3(grid), dim3(kNT), lds,
+                               L.stream, plan, r, x, hidden, inter, sec, bias_dt, act, act_kind,
+                               limit, alpha, max_tokens, s.chunks);
+        };
+        using One = std::integral_constant<int, 1>;
+        using Many = std::integral_constant<int, kMaxTokens>;
+        if (x_dt == DT_F32) {
+            if (max_tokens == 1) go(std::integral_constant<int, DT_F32>{}, One{});
+            else go(std::integral_constant<int, DT_F32>{}, Many{});
+        } else if (x_dt == DT_F16) {
+            if (max_tokens == 1) go(std::integral_constant<int, DT_F16>{}, One{});
+            else go(std::integral_constant<int, DT_F16>{}, Many{});
+        } else {
+            if (max_tokens == 1) go(std::integral_constant<int, DT_BF16>{}, One{});
+            else go(std::integral_constant<int, DT_BF16>{}, Many{});
+        }
+    });
+    return hipGetLastError();
 }
 
 int down_lds_bytes(int hidden, int inter, int grid, int smax)
@@ -694,12 +856,26 @@ int down_lds_bytes(int hidden, int inter, int grid, int smax)
     return (int)sizeof(Plan) + smax * (inter / 32) * 20 * 4 + kMaxSlots * nmax * 4;
 }
 
+template <int MT>
+static void down_dispatch(const Launch &L, const RowShape &s, int grid, size_t lds,
+                          const Plan *plan, const uint16_t *act, int hidden, int inter,
+                          const Sections &sec, int bias_dt, float *out, uint16_t *out_bf16,
+                          int accumulate, int smax, int nmax, int prestage)
+{
+    with_shape(s, [&](auto sh) {
+        using SH = decltype(sh);
+        hipLaunchKernelGGL((down_kernel<MT, SH>), dim3(grid), dim3(kNT), lds, L.stream, plan,
+                           act, hidden, inter, sec, bias_dt, out, out_bf16, accumulate, smax,
+                           nmax, s.chunks, prestage);
+    });
+}
+
 hipError_t launch_down(const Launch &L, const Plan *plan, int max_tokens, int max_slots,
                        const uint16_t *act, int hidden, int inter, const Sections &sec,
                        int bias_dt, float *out, uint16_t *out_bf16, int accumulate)
 {
     const RowShape s = row_shape(inter / 32);
-    int grid = L.grid_b > 0 ? L.grid_b : L.cus;
+    int grid = L.grid_b > 0 ? L.grid_b : 2 * L.cus;
     if (grid > hidden) grid = hidden;
     // As many staged slots as fit the LDS budget, at least a full group.
     int smax = max_slots;
@@ -714,25 +890,13 @@ hipError_t launch_down(const Launch &L, const Plan *plan, int max_tokens, int ma
     if (smax < need) return hipErrorInvalidValue;
     const int nmax = (hidden + grid - 1) / grid;
     const size_t lds = (size_t)down_lds_bytes(hidden, inter, grid, smax);
-    if (max_tokens == 1) {
-        if (s.tpr == 8)
-            hipLaunchKernelGGL((down_kernel<1, 8>), dim3(grid), dim3(kNT), lds, L.stream, plan,
-                               act, hidden, inter, sec, bias_dt, out, out_bf16, accumulate, smax,
-                               nmax, s.m, s.chunks);
-        else
-            hipLaunchKernelGGL((down_kernel<1, 16>), dim3(grid), dim3(kNT), lds, L.stream, plan,
-                               act, hidden, inter, sec, bias_dt, out, out_bf16, accumulate, smax,
-                               nmax, s.m, s.chunks);
-    } else {
-        if (s.tpr == 8)
-            hipLaunchKernelGGL((down_kernel<kMaxTokens, 8>), dim3(grid), dim3(kNT), lds,
-                               L.stream, plan, act, hidden, inter, sec, bias_dt, out, out_bf16,
-                               accumulate, smax, nmax, s.m, s.chunks);
-        else
-            hipLaunchKernelGGL((down_kernel<kMaxTokens, 16>), dim3(grid), dim3(kNT), lds,
-                               L.stream, plan, act, hidden, inter, sec, bias_dt, out, out_bf16,
-                               accumulate, smax, nmax, s.m, s.chunks);
-    }
+    const int prestage = max_slots < smax ? max_slots : smax;
+    if (max_tokens == 1)
+        down_dispatch<1>(L, s, grid, lds, plan, act, hidden, inter, sec, bias_dt, out, out_bf16,
+                         accumulate, smax, nmax, prestage);
+    else
+        down_dispatch<kMaxTokens>(L, s, grid, lds, plan, act, hidden, inter, sec, bias_dt, out,
+                                  out_bf16, accumulate, smax, nmax, prestage);
     return hipGetLastError();
 }
 
@@ -765,14 +929,12 @@ hipError_t launch_router(const Launch &L, const void *W, int w_dt, const void *b
     return hipGetLastError();
 }
 
-hipError_t launch_route(const Launch &L, const float *logits, int experts, int top_k,
-                        int tokens, const uint8_t *experts_base, int64_t stride, Plan *plan,
-                        int32_t *ids_out, float *w_out)
+hipError_t launch_route(const Launch &L, const RouteArgs &route, Plan *plan)
 {
-    if (experts > kMaxExperts || top_k > kMaxTopK || tokens > kMaxTokens || top_k > experts)
+    if (route.experts > kMaxExperts || route.top_k > kMaxTopK || route.tokens > kMaxTokens ||
+        route.top_k > route.experts)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(route_kernel, dim3(1), dim3(64), 0, L.stream, logits, experts, top_k,
-                       tokens, experts_base, stride, plan, ids_out, w_out);
+    hipLaunchKernelGGL(route_kernel, dim3(1), dim3(64), 0, L.stream, route, plan);
     return hipGetLastError();
 }
 

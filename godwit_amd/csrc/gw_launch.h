@@ -15,6 +15,17 @@ struct Launch {
     int grid_b;     // workgroups of the down kernel (0 = default)
 };
 
+// Device routing from logits (Router.select + the demand map), done by the
+// route kernel or fused into the gate_up kernel's prologue.
+struct RouteArgs {
+    const float *logits;          // [tokens, experts]; null = the plan is given
+    int experts, top_k, tokens;
+    const uint8_t *experts_base;  // expert e at experts_base + e * stride
+    int64_t stride;
+    int32_t *ids_out;             // optional [tokens, top_k]
+    float *w_out;                 // optional [tokens, top_k]
+};
+
 // Lanes per row and blocks per lane chosen for a row of `bpr` MXFP4 blocks.
 struct RowShape { int tpr; int m; int chunks; };
 RowShape row_shape(int bpr);
@@ -31,12 +42,13 @@ hipError_t launch_accumulate(const Launch &L, const float *src, float *dst, floa
 hipError_t launch_router(const Launch &L, const void *W, int w_dt, const void *b, int b_dt,
                          const void *x, int x_dt, float *logits, int experts, int hidden,
                          int tokens);
-hipError_t launch_route(const Launch &L, const float *logits, int experts, int top_k,
-                        int tokens, const uint8_t *experts_base, int64_t stride, Plan *plan,
-                        int32_t *ids_out, float *w_out);
-hipError_t launch_gate_up(const Launch &L, const Plan *plan, int max_tokens, const void *x,
-                          int x_dt, int hidden, int inter, const Sections &sec, int bias_dt,
-                          uint16_t *act, int act_kind, float limit, float alpha);
+hipError_t launch_route(const Launch &L, const RouteArgs &route, Plan *plan);
+// route == null: the plan is read from `plan`; otherwise every workgroup routes
+// and workgroup 0 writes the plan to `plan` for the down kernel.
+hipError_t launch_gate_up(const Launch &L, Plan *plan, const RouteArgs *route, int max_tokens,
+                          const void *x, int x_dt, int hidden, int inter, const Sections &sec,
+                          int bias_dt, uint16_t *act, int act_kind, float limit, float alpha);
+constexpr int kFusedRouteExperts = 256;
 hipError_t launch_down(const Launch &L, const Plan *plan, int max_tokens, int max_slots,
                        const uint16_t *act, int hidden, int inter, const Sections &sec,
                        int bias_dt, float *out, uint16_t *out_bf16, int accumulate);

@@ -275,6 +275,42 @@ def test_layer_qwen3_decode(ctx, tokens):
         _close(got[t], ref[t])
 
 
+@pytest.mark.parametrize("experts,top_k,tokens", [(128, 8, 8), (64, 4, 3), (300, 4, 2)])
+def test_layer_routing_ties_exact(ctx, experts, top_k, tokens):
+    """Device routing reproduces Router.select's partial selection sort exactly, ties
+    included: logits drawn from 6 distinct values, so most top-k picks are ties
+    broken by the sort's swap history.  300 experts exercises the standalone route
+    kernel, the others the routing fused into the gate_up kernel."""
+    shape = SMALL
+    H = shape["hidden"]
+    layout, experts_d, buf = _make_layer(ctx, shape, experts, 1000 + experts)
+    runner = gw.ExpertRunner(ctx, H, shape["inter"], shape["act"])
+    r = rng(1001)
+    logits = r.choice(np.array([-1.0, 0.0, 0.5, 1.0, 2.0, 3.0], np.float32),
+                      size=(tokens, experts)).astype(np.float32)
+    xbits, xw = normal_bf16(r, tokens * H)
+    lb, xb = ctx.buffer(logits), ctx.buffer(xbits)
+    out = ctx.empty(tokens * H * 4)
+    ids_b, w_b = ctx.empty(tokens * top_k * 4), ctx.empty(tokens * top_k * 4)
+    runner.layer_forward(buf.ptr, layout.stride, experts, top_k, xb.ptr, gw.BF16, tokens,
+                         out.ptr, logits=lb.ptr, routing_ids=ids_b.ptr, routing_weights=w_b.ptr)
+    ctx.synchronize()
+    ids = ids_b.download(np.int32, tokens * top_k).reshape(tokens, top_k)
+    wts = w_b.download(np.float32, tokens * top_k).reshape(tokens, top_k)
+    got = out.download(np.float32, tokens * H).reshape(tokens, H)
+    for t in range(tokens):
+        rid, rw = oracle.router_select(logits[t], top_k)
+        assert list(ids[t]) == list(rid), (t, list(ids[t]), list(rid))
+        assert np.allclose(wts[t], rw, rtol=1e-6, atol=1e-7)
+    ref, _, _ = oracle.moe_layer([e.oracle_expert() for e in experts_d], top_k, logits, xw, H,
+                                 shape["inter"], shape["oact"])
+    for t in range(tokens):
+        _close(got[t], ref[t])
+    for b in (lb, xb, out, ids_b, w_b, buf):
+        b.free()
+    runner.close()
+
+
 def test_layer_graph_replay_matches_eager(ctx):
     """A captured 3-layer chain replayed several times equals the eager result each time."""
     shape = SMALL
