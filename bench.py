@@ -197,16 +197,23 @@ def main() -> int:
                            step_logits)
             token()
         ctx.synchronize()
-        for name in ("route", "gate_up", "down"):
+        for name in ("moe_layer", "route", "gate_up", "down"):
             ms, n = ctx.profile(name)
-            kernels[name] = {"launches": n, "avg_us": ms / max(n, 1) * 1e3}
+            if n:
+                kernels[name] = {"launches": n, "avg_us": ms / n * 1e3}
         ctx.set_profiling(False)
-        gu_us = kernels["gate_up"]["avg_us"]
-        achieved = gate_up_bytes(lay) / (gu_us * 1e-6) / 1e9
+        if "moe_layer" in kernels:
+            dom, nbytes = "moe_layer", bytes_token // L
+            desc = ("moe_layer_kernel (one launch per layer: route + MXFP4 gate_up GEMV + "
+                    "SwiGLU + down GEMV + weighted combine)")
+        else:
+            dom, nbytes = "gate_up", gate_up_bytes(lay)
+            desc = "gate_up_kernel (fused MXFP4 gate_up GEMV + bias + SwiGLU)"
+        k_us = kernels[dom]["avg_us"]
+        achieved = nbytes / (k_us * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                    "kernel": "gate_up_kernel (fused MXFP4 gate_up GEMV + bias + SwiGLU)",
-                    "bytes_per_launch": gate_up_bytes(lay), "avg_launch_us": round(gu_us, 3)}
+                    "kernel": desc, "bytes_per_launch": nbytes, "avg_launch_us": round(k_us, 3)}
         log("kernels: " + ", ".join(f"{k} {v['avg_us']:.2f} us x{v['launches']}"
                                     for k, v in kernels.items()))
 

@@ -373,6 +373,13 @@ class ExpertRunner:
         a.routing_weights = routing_weights or None
         check(lib.gw_moe_layer_forward(self.handle, ctypes.byref(a)))
 
+    def sync_errors(self) -> int:
+        """Failed in-kernel exchanges of the one-token layer kernel since creation
+        (0 when every result is valid).  Waits for the runner's stream."""
+        n = ctypes.c_uint32(0)
+        check(lib.gw_expert_runner_sync_errors(self.handle, ctypes.byref(n)))
+        return int(n.value)
+
     def close(self) -> None:
         for b in (self._x, self._y):
             if b is not None:

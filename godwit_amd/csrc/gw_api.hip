@@ -541,9 +541,22 @@ struct gw_expert_runner {
     uint16_t *act_buf = nullptr;     // [kMaxSlots, inter] fp16 activations
     float *logits = nullptr;         // [kMaxTokens, kMaxExperts]
     Plan *staging = nullptr;         // pinned host mirror of `plans`
+    unsigned *sync_buf = nullptr;    // fused layer exchange: counters | epochs | error word
+    bool fused_enabled = true;       // GODWIT_FUSED_LAYER=0 at creation turns it off
     int ring_next = 0;
     int ring_used = 0;
 };
+
+static constexpr int kSyncEpochWords = 8192;   // >= any fused grid (2 x CUs)
+
+static gw::SyncArgs sync_of(gw_expert_runner *r)
+{
+    gw::SyncArgs s;
+    s.counters = r->sync_buf;
+    s.epochs = r->sync_buf + gw::kSyncWords;
+    s.err = r->sync_buf + gw::kSyncWords + kSyncEpochWords;
+    return s;
+}
 
 extern "C" int gw_expert_runner_destroy(gw_expert_runner *r)
 {
@@ -554,6 +567,7 @@ extern "C" int gw_expert_runner_destroy(gw_expert_runner *r)
     (void)hipFree(r->act_buf);
     (void)hipFree(r->logits);
     (void)hipHostFree(r->staging);
+    (void)hipFree(r->sync_buf);
     delete r;
     return GW_OK;
 }
@@ -590,12 +604,25 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     if (e == hipSuccess)
         e = hipMalloc((void **)&r->logits, sizeof(float) * gw::kMaxTokens * kMaxExperts);
     if (e == hipSuccess) e = hipHostMalloc((void **)&r->staging, sizeof(Plan) * kPlanRing);
+    const size_t sync_bytes = sizeof(unsigned) * (gw::kSyncWords + kSyncEpochWords + 64);
+    if (e == hipSuccess) e = hipMalloc((void **)&r->sync_buf, sync_bytes);
+    if (e == hipSuccess) e = hipMemset(r->sync_buf, 0, sync_bytes);
     if (e != hipSuccess) {
         gw_expert_runner_destroy(r);
         return fail(e == hipErrorOutOfMemory ? GW_ERR_OOM : GW_ERR_HIP, "runner scratch: %s",
                     hipGetErrorString(e));
     }
+    const char *env = getenv("GODWIT_FUSED_LAYER");
+    r->fused_enabled = !(env && env[0] == '0');
     *out = r;
+    return GW_OK;
+}
+
+extern "C" int gw_expert_runner_sync_errors(gw_expert_runner *r, uint32_t *count)
+{
+    GW_CHECK(r && count, GW_ERR_ARG, "null argument");
+    GW_HIP(hipStreamSynchronize(r->ctx->stream));
+    GW_HIP(hipMemcpy(count, sync_of(r).err, sizeof(uint32_t), hipMemcpyDeviceToHost));
     return GW_OK;
 }
 
@@ -924,6 +951,20 @@ extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args
     route.stride = a->expert_stride;
     route.ids_out = a->routing_ids;
     route.w_out = a->routing_weights;
+    const gw::Sections sec = sections_of(r->offsets);
+    // One token: the whole layer in one kernel when the shape and the
+    // occupancy allow it.
+    if (a->tokens == 1 && r->fused_enabled) {
+        const int grid = gw::fused_layer_grid(L, (int)r->hidden, (int)r->inter, a->x_dtype,
+                                              (int)a->top_k, (int)a->expert_count);
+        if (grid > 0 && grid <= kSyncEpochWords) {
+            ProfScope ps(ctx, "moe_layer");
+            GW_HIP(gw::launch_fused_layer(L, grid, route, a->x, a->x_dtype, (int)r->hidden,
+                                          (int)r->inter, sec, r->bias_dt, r->act_buf, r->act,
+                                          r->limit, r->alpha, a->out, a->out_bf16, sync_of(r)));
+            return GW_OK;
+        }
+    }
     // Up to 256 experts the gate_up kernel routes in its prologue; beyond that
     // the route kernel builds the plan first.
     const bool fused = a->expert_count <= gw::kFusedRouteExperts;
@@ -931,7 +972,6 @@ extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args
         ProfScope ps(ctx, "route");
         GW_HIP(gw::launch_route(L, route, r->route_plan));
     }
-    const gw::Sections sec = sections_of(r->offsets);
     {
         ProfScope ps(ctx, "gate_up");
         GW_HIP(gw::launch_gate_up(L, r->route_plan, fused ? &route : nullptr, a->tokens, a->x,

@@ -120,12 +120,20 @@ __device__ __forceinline__ void divmod_small(int a, int d, float inv_d, int &q, 
     r = r >= d ? r - d : r;
 }
 
+// Sum over the TPR lanes of a row segment with DPP butterflies inside a
+// 16-lane row (pair swap, quad swap, half mirror, mirror): every lane ends with
+// the same bits (each step adds two equal partial sums in either order).
+#define GW_DPPF(x, ctrl) __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), (ctrl), 0xF, 0xF, false))
 template <int TPR> __device__ __forceinline__ float seg_sum(float v)
 {
-#pragma unroll
-    for (int o = TPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    static_assert(TPR == 8 || TPR == 16, "row segments are 8 or 16 lanes");
+    v += GW_DPPF(v, 0xB1);                      // quad_perm [1,0,3,2]
+    v += GW_DPPF(v, 0x4E);                      // quad_perm [2,3,0,1]
+    v += GW_DPPF(v, 0x141);                     // row_half_mirror
+    if constexpr (TPR == 16) v += GW_DPPF(v, 0x140);   // row_mirror
     return v;
 }
+#undef GW_DPPF
 
 // Issues the M block loads (and M scale loads) of one stage.  Every lane issues
 // all of them: a row past the end re-reads the last row, a column past the end
@@ -239,6 +247,49 @@ __device__ __forceinline__ void copy_plan(Plan *dst, const Plan *src)
 // exactly as `order.swapAt(p, best)` does, so ties resolve as in the reference.
 // ---------------------------------------------------------------------------
 
+// Wave-wide unsigned max / min: DPP within each 16-lane row (quad swaps, half
+// mirror, mirror), then the four rows through v_readlane.  ALU latency only;
+// the whole wave must be active.
+#define GW_DPP(x, ctrl) ((uint32_t)__builtin_amdgcn_update_dpp((int)(x), (int)(x), (ctrl), 0xF, 0xF, false))
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x)
+{
+    x = max(x, GW_DPP(x, 0xB1));    // quad_perm [1,0,3,2]
+    x = max(x, GW_DPP(x, 0x4E));    // quad_perm [2,3,0,1]
+    x = max(x, GW_DPP(x, 0x141));   // row_half_mirror
+    x = max(x, GW_DPP(x, 0x140));   // row_mirror
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0);
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32);
+    const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+    return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x)
+{
+    x = min(x, GW_DPP(x, 0xB1));
+    x = min(x, GW_DPP(x, 0x4E));
+    x = min(x, GW_DPP(x, 0x141));
+    x = min(x, GW_DPP(x, 0x140));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0);
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32);
+    const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+    return min(min(a, b), min(c, d));
+}
+#undef GW_DPP
+
+// Float -> unsigned key with the same order; 0 is reserved for "no candidate"
+// (NaN and out-of-range positions never win, as `>` never picks them).
+__device__ __forceinline__ uint32_t order_key(float v)
+{
+    const uint32_t u = __float_as_uint(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
 template <int R>
 __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int E, int K,
                                            int T, const uint8_t *experts_base, int64_t stride,
@@ -257,43 +308,43 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
             ov[r] = i < E ? logits[(int64_t)t * E + i] : 0.0f;
         }
         for (int pos = 0; pos < K; ++pos) {
-            float bv = 0.0f;
-            int bp = -1;
+            // Largest logit among positions >= pos, then the smallest position
+            // holding it: the first one the reference's strict `>` scan keeps.
+            uint32_t km = 0;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int i = lane + 64 * r;
-                const float v = ov[r];
-                if (i >= pos && i < E && !__builtin_isnan(v) && (bp < 0 || v > bv)) {
-                    bv = v;
-                    bp = i;
-                }
+                const uint32_t k = (i >= pos && i < E && !__builtin_isnan(ov[r])) ? order_key(ov[r]) : 0u;
+                km = max(km, k);
             }
+            const uint32_t kmax = wave_max_u32(km);
+            uint32_t pmin = 0xFFFFFFFFu;
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float v2 = __shfl_xor(bv, o);
-                const int p2 = __shfl_xor(bp, o);
-                const bool take = p2 >= 0 && (bp < 0 || v2 > bv || (v2 == bv && p2 < bp));
-                bv = take ? v2 : bv;
-                bp = take ? p2 : bp;
+            for (int r = 0; r < R; ++r) {
+                const int i = lane + 64 * r;
+                const bool hit = kmax != 0u && i >= pos && i < E && !__builtin_isnan(ov[r]) &&
+                                 order_key(ov[r]) == kmax;
+                pmin = hit ? min(pmin, (uint32_t)i) : pmin;
             }
+            const uint32_t bp = wave_min_u32(pmin);
             const int pr = pos >> 6, pl = pos & 63;
             float v_pos = 0.0f;
             int o_pos = 0;
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 if (r == pr) {
-                    v_pos = __shfl(ov[r], pl);
-                    o_pos = __shfl(ord[r], pl);
+                    v_pos = lane_value(ov[r], pl);
+                    o_pos = __builtin_amdgcn_readlane(ord[r], pl);
                 }
-            const int best = (bp < 0 || __builtin_isnan(v_pos)) ? pos : bp;
+            const int best = (bp == 0xFFFFFFFFu || __builtin_isnan(v_pos)) ? pos : (int)bp;
             const int br = best >> 6, bl = best & 63;
             float v_b = 0.0f;
             int o_b = 0;
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 if (r == br) {
-                    v_b = __shfl(ov[r], bl);
-                    o_b = __shfl(ord[r], bl);
+                    v_b = lane_value(ov[r], bl);
+                    o_b = __builtin_amdgcn_readlane(ord[r], bl);
                 }
 #pragma unroll
             for (int r = 0; r < R; ++r)
@@ -312,19 +363,27 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
         // selected logits with the maximum subtracted, summed in order.
         const int sid = ord[0];
         const float sv = ov[0];
-        float peak = __shfl(sv, 0);
+        float peak = lane_value(sv, 0);
         for (int i = 1; i < K; ++i) {
-            const float v = __shfl(sv, i);
+            const float v = lane_value(sv, i);
             if (v > peak) peak = v;
         }
         const float ex = expf(sv - peak);
         float total = 0.0f;
-        for (int i = 0; i < K; ++i) total += __shfl(ex, i);
+        for (int i = 0; i < K; ++i) total += lane_value(ex, i);
         const float w = ex / total;
         const int src = lane - t * K;
         const bool mine = src >= 0 && src < K;
-        const int e_src = __shfl(sid, mine ? src : 0);
-        const float w_src = __shfl(w, mine ? src : 0);
+        int e_src = 0;
+        float w_src = 0.0f;
+        for (int i = 0; i < K; ++i) {   // entry (t, i) moves to lane t*K + i
+            const int ei = __builtin_amdgcn_readlane(sid, i);
+            const float wi = lane_value(w, i);
+            if (src == i) {
+                e_src = ei;
+                w_src = wi;
+            }
+        }
         if (mine) {
             my_e = e_src;
             my_w = w_src;
@@ -337,7 +396,7 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
     const int n = T * K;
     int first = -1, before = 0, same = 0;
     for (int j = 0; j < n; ++j) {
-        const int ej = __shfl(my_e, j);
+        const int ej = __builtin_amdgcn_readlane(my_e, j);
         if (lane < n && ej == my_e) {
             if (first < 0) first = j;
             if (j < lane) ++before;
@@ -348,7 +407,7 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
     const unsigned long long leaders = __ballot(leader);
     int slot0 = 0;
     for (int j = 0; j < n; ++j) {
-        const int fj = __shfl(first, j);
+        const int fj = __builtin_amdgcn_readlane(first, j);
         if (lane < n && fj < first) ++slot0;
     }
     if (lane < n) {
@@ -651,6 +710,242 @@ __global__ __launch_bounds__(256) void router_kernel(const void *__restrict__ W,
     if (lane == 0) logits[(int64_t)t * E + e] = acc + (b ? load_as_f32(b, b_dt, e) : 0.0f);
 }
 
+// ---------------------------------------------------------------------------
+// Fused decode layer (one token): route -> gate_up + activation -> down +
+// weighted combine in ONE kernel.  Every workgroup owns a slice of the gate_up
+// rows and a slice of the output rows.  It issues the loads of both slices up
+// front, computes its gate_up rows and writes their activations with coherent
+// (sc1) stores, then signals one of 16 counters (spread over separate lines so
+// arrivals do not serialise on one address) and waits, with a bounded spin,
+// until every workgroup has signalled.  By then its down weights are already
+// in registers: it stages all activations (sc1 loads), finishes the down rows
+// and combines them in router order.  The grid must be co-resident (the host
+// checks occupancy); a wait that gives up sets *sync.err instead of hanging.
+// ---------------------------------------------------------------------------
+
+constexpr int kDownDepth = 2;
+constexpr int kSyncCounters = 16;
+constexpr int kSyncStride = 64;            // uint32 apart: one 256-byte line each
+constexpr unsigned kSpinLimit = 1u << 18;
+
+__device__ __forceinline__ void store_coherent_u16(uint16_t *p, uint16_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Buffer resource word 3 for raw (untyped) buffer access, and the cache-policy
+// bit that makes a load device-coherent (sc1): the same access a relaxed
+// agent-scope atomic load performs, but batchable.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+constexpr int kCachePolicySc1 = 16;
+constexpr int kActBatch = 8;
+
+template <int XK, class SG, class SD>
+__global__ __launch_bounds__(kNT) void moe_layer_kernel(
+    RouteArgs route, const void *__restrict__ x, int hidden, int inter, Sections sec,
+    int bias_dt, uint16_t *__restrict__ act, int act_kind, float limit, float alpha,
+    float *__restrict__ out, uint16_t *__restrict__ out_bf16, SyncArgs sync, int chunks_g,
+    int chunks_d, int nmax)
+{
+    extern __shared__ uint32_t lds[];
+    constexpr int BDX = XL<XK>::kBlockDw;
+    constexpr int BDA = XL<DT_F16>::kBlockDw;
+    constexpr int TPRG = SG::TPR, TPRD = SD::TPR;
+    __shared__ unsigned s_epoch;
+    Plan *plan = reinterpret_cast<Plan *>(lds);
+    const int bpr_g = hidden >> 5, bpr_d = inter >> 5;
+    const int xstride = bpr_g * BDX, astride = bpr_d * BDA;
+    const int K = route.top_k;
+    uint32_t *xs = lds + sizeof(Plan) / 4;                     // [xstride]
+    uint32_t *as = xs + xstride;                                // [K][astride]
+    float *vals = reinterpret_cast<float *>(as + K * astride);  // [K][nmax]
+
+    if (threadIdx.x < 64) {
+        route_wave<kFusedRouteR>(route.logits, route.experts, K, 1, route.experts_base,
+                                 route.stride, plan, blockIdx.x == 0 ? route.ids_out : nullptr,
+                                 blockIdx.x == 0 ? route.w_out : nullptr);
+        if (threadIdx.x == 0) s_epoch = sync.epochs[blockIdx.x];
+    } else {
+        stage_vector<XK>(xs, x, hidden, threadIdx.x - 64, kNT - 64);
+    }
+    __syncthreads();
+
+    const int G = gridDim.x;
+    const int64_t row_bytes_g = (int64_t)bpr_g * 16, row_bytes_d = (int64_t)bpr_d * 16;
+    const int bsz = bias_dt == DT_F32 ? 4 : 2;
+
+    // gate_up slice: (expert, pair) range [p0, p1)
+    const int64_t totg = (int64_t)K * inter;
+    const int64_t p0 = (int64_t)blockIdx.x * totg / G;
+    const int64_t p1 = (int64_t)(blockIdx.x + 1) * totg / G;
+    const int ng_items = (int)(2 * (p1 - p0));
+    const int g_start = (int)(p0 / inter);
+    const int i_start = (int)(p0 - (int64_t)g_start * inter);
+    const float inv_inter = 1.0f / (float)inter;
+    auto locate = [&](int item, int &g, int &i) {
+        int q, r;
+        divmod_small(i_start + (item >> 1), inter, inv_inter, q, r);
+        g = g_start + q;
+        i = r;
+    };
+    auto rowfn_g = [&](int item) {
+        RowRef<1> r;
+        int g, i;
+        locate(item, g, i);
+        const int row = 2 * i + (item & 1);
+        const uint8_t *base = plan->group_base[g];
+        r.packed = base + sec.gu_blocks + row * row_bytes_g;
+        r.scales = base + sec.gu_scales + row * bpr_g;
+        r.bias = bias_dt >= 0 ? base + sec.gu_bias + row * bsz : r.scales;
+        r.ntok = 1;
+        r.xoff[0] = 0;
+        return r;
+    };
+    auto epi_g = [&](int item, bool valid, int, float (&acc)[1], uint32_t bw, int bsh) {
+        const float up = __shfl_down(acc[0], TPRG);
+        const float b_own = decode_bias(bw, bsh, bias_dt);
+        const float b_next = __shfl_down(b_own, TPRG);
+        if (valid && (item & 1) == 0 && (threadIdx.x % TPRG) == 0) {
+            int g, i;
+            locate(item, g, i);
+            const float v = apply_activation(act_kind, acc[0] + b_own, up + b_next, limit, alpha);
+            store_coherent_u16(act + (int64_t)plan->group_slot0[g] * inter + i,
+                               f32_to_f16_bits(v));
+        }
+    };
+
+    // down slice: output rows [r0, r1) of every selected expert
+    const int r0 = (int)((int64_t)blockIdx.x * hidden / G);
+    const int r1 = (int)((int64_t)(blockIdx.x + 1) * hidden / G);
+    const int n = r1 - r0;
+    const int nd_items = K * n;
+    const float inv_n = 1.0f / (float)n;
+    auto rowfn_d = [&](int item) {
+        RowRef<1> r;
+        int gl, q;
+        divmod_small(item, n, inv_n, gl, q);
+        const uint8_t *base = plan->group_base[gl];
+        const int64_t row = r0 + q;
+        r.packed = base + sec.dn_blocks + row * row_bytes_d;
+        r.scales = base + sec.dn_scales + row * bpr_d;
+        r.bias = bias_dt >= 0 ? base + sec.dn_bias + row * bsz : r.scales;
+        r.ntok = 1;
+        r.xoff[0] = plan->group_slot0[gl] * astride;
+        return r;
+    };
+    auto epi_d = [&](int item, bool valid, int, float (&acc)[1], uint32_t bw, int bsh) {
+        if (valid && (threadIdx.x % TPRD) == 0) {
+            int gl, q;
+            divmod_small(item, n, inv_n, gl, q);
+            vals[plan->group_slot0[gl] * nmax + q] = acc[0] + decode_bias(bw, bsh, bias_dt);
+        }
+    };
+
+    constexpr int RGG = kNT / TPRG, RGD = kNT / TPRD;
+    const int ng = ((ng_items + RGG - 1) / RGG) * chunks_g;
+    const int nd = ((nd_items + RGD - 1) / RGD) * chunks_d;
+    float acc[1] = {0.0f};
+
+    // Both slices' first batches go out together.
+    Stage<1, SG::M> Sg[kDepth];
+    Stage<1, SD::M> Sd[kDownDepth];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) issue<1, SG>(Sg[d], d, chunks_g, bpr_g, ng_items, rowfn_g);
+#pragma unroll
+    for (int d = 0; d < kDownDepth; ++d) issue<1, SD>(Sd[d], d, chunks_d, bpr_d, nd_items, rowfn_d);
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) consume<XK, 1, SG>(Sg[d], acc, chunks_g, bpr_g, xs, epi_g);
+    for (int base = kDepth; base < ng; base += kDepth) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d)
+            issue<1, SG>(Sg[d], base + d, chunks_g, bpr_g, ng_items, rowfn_g);
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) consume<XK, 1, SG>(Sg[d], acc, chunks_g, bpr_g, xs, epi_g);
+    }
+
+    // Signal: this workgroup's activations are stored (every wave waits for its
+    // own stores), then one relaxed add on this workgroup's counter.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const unsigned epoch1 = s_epoch + 1;
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(sync.counters + (blockIdx.x % kSyncCounters) * kSyncStride, 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x < 64) {
+        const int c = threadIdx.x;
+        const unsigned target =
+            c < kSyncCounters ? epoch1 * (unsigned)((G - c + kSyncCounters - 1) / kSyncCounters) : 0u;
+        unsigned spins = 0;
+        while (true) {
+            bool ok = true;
+            if (c < kSyncCounters)   // wrap-safe: counters only ever grow by whole launches
+                ok = (int)(__hip_atomic_load(sync.counters + c * kSyncStride, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT) - target) >= 0;
+            if (__all(ok)) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > kSpinLimit) {
+                if (c == 0) atomicOr(sync.err, 1u);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+
+    // Every activation is now visible: stage them with coherent (sc1) buffer
+    // loads, issued as one batch per thread.  A buffer load past the buffer's
+    // end returns zero instead of faulting; such lanes write nothing.
+    {
+        const int q4 = inter >> 3;                 // 16-byte groups per slot
+        const int total = K * q4;
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            act, 0, total * 16, kBufferRsrcWord3);
+        const float inv_q4 = 1.0f / (float)q4;
+        for (int base = 0; base < total; base += kActBatch * kNT) {
+            u32x4 v[kActBatch];
+#pragma unroll
+            for (int u = 0; u < kActBatch; ++u)
+                v[u] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rsrc, (base + u * kNT + (int)threadIdx.x) * 16, 0, kCachePolicySc1);
+#pragma unroll
+            for (int u = 0; u < kActBatch; ++u) {
+                const int i = base + u * kNT + (int)threadIdx.x;
+                if (i < total) {
+                    int sidx, j4;
+                    divmod_small(i, q4, inv_q4, sidx, j4);
+                    const int j = j4 * 4;
+                    *reinterpret_cast<u32x4 *>(as + sidx * astride + (j >> 4) * BDA + (j & 15)) =
+                        v[u];
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int d = 0; d < kDownDepth; ++d) consume<DT_F16, 1, SD>(Sd[d], acc, chunks_d, bpr_d, as, epi_d);
+    for (int base = kDownDepth; base < nd; base += kDownDepth) {
+#pragma unroll
+        for (int d = 0; d < kDownDepth; ++d)
+            issue<1, SD>(Sd[d], base + d, chunks_d, bpr_d, nd_items, rowfn_d);
+#pragma unroll
+        for (int d = 0; d < kDownDepth; ++d)
+            consume<DT_F16, 1, SD>(Sd[d], acc, chunks_d, bpr_d, as, epi_d);
+    }
+    __syncthreads();
+
+    // Combine in router order: dst = 0; dst += out_e * w_e (expert_accumulate).
+    for (int q = threadIdx.x; q < n; q += kNT) {
+        float dst = 0.0f;
+        for (int k = 0; k < plan->tok_nslots[0]; ++k) {
+            const int sl = plan->tok_slots[0][k];
+            dst = add_scaled_rn(dst, vals[sl * nmax + q], plan->slot_weight[sl]);
+        }
+        out[r0 + q] = dst;
+        if (out_bf16) out_bf16[r0 + q] = f32_to_bf16_bits(dst);
+    }
+    if (threadIdx.x == 0) sync.epochs[blockIdx.x] = epoch1;
+}
+
 // Standalone routing (more than 256 experts, or a host that wants the plan
 // only): one wave builds the plan in LDS and copies it out.
 __global__ __launch_bounds__(64) void route_kernel(RouteArgs route, Plan *__restrict__ gplan)
@@ -868,6 +1163,98 @@ static void down_dispatch(const Launch &L, const RowShape &s, int grid, size_t l
                            act, hidden, inter, sec, bias_dt, out, out_bf16, accumulate, smax,
                            nmax, s.chunks, prestage);
     });
+}
+
+int fused_layer_lds_bytes(int hidden, int inter, int x_dt, int top_k, int grid)
+{
+    const int nmax = (hidden + grid - 1) / grid;
+    return (int)sizeof(Plan) + (hidden / 32) * x_block_dw(x_dt) * 4 +
+           top_k * (inter / 32) * 20 * 4 + top_k * nmax * 4;
+}
+
+// Which (gate_up, down) shape classes the fused kernel is built for.
+static int fused_shape_pair(int hidden, int inter)
+{
+    const RowShape g = row_shape(hidden / 32), d = row_shape(inter / 32);
+    if (g.tpr == 16 && g.m == 6 && d.tpr == 16 && d.m == 6) return 0;   // GPT-OSS 2880/2880
+    if (g.tpr == 16 && g.m == 4 && d.tpr == 8 && d.m == 3) return 1;    // Qwen3 2048/768
+    return -1;
+}
+
+template <int XK, class SG, class SD>
+static const void *fused_fn()
+{
+    return reinterpret_cast<const void *>(&moe_layer_kernel<XK, SG, SD>);
+}
+
+static const void *fused_kernel_ptr(int x_dt, int pair)
+{
+    if (pair == 0) {
+        if (x_dt == DT_F32) return fused_fn<DT_F32, S3, S3>();
+        if (x_dt == DT_F16) return fused_fn<DT_F16, S3, S3>();
+        return fused_fn<DT_BF16, S3, S3>();
+    }
+    if (x_dt == DT_F32) return fused_fn<DT_F32, S2, S1>();
+    if (x_dt == DT_F16) return fused_fn<DT_F16, S2, S1>();
+    return fused_fn<DT_BF16, S2, S1>();
+}
+
+int fused_layer_grid(const Launch &L, int hidden, int inter, int x_dt, int top_k, int experts)
+{
+    const int pair = fused_shape_pair(hidden, inter);
+    if (pair < 0 || experts > 64 * kFusedRouteR || top_k > kMaxTopK) return 0;
+    const int grid = 2 * L.cus;
+    if ((int64_t)top_k * inter < grid || hidden < grid) return 0;
+    const int lds = fused_layer_lds_bytes(hidden, inter, x_dt, top_k, grid);
+    if (lds > kLdsBudget) return 0;
+    // Resident workgroups per CU, cached per (shape pair, x dtype, LDS bytes).
+    static int cache_key[2][3] = {{-1, -1, -1}, {-1, -1, -1}};
+    static int cache_occ[2][3];
+    const int xi = x_dt == DT_F32 ? 0 : x_dt == DT_F16 ? 1 : 2;
+    int occ = 0;
+    if (cache_key[pair][xi] == lds) {
+        occ = cache_occ[pair][xi];
+    } else {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fused_kernel_ptr(x_dt, pair), kNT,
+                                                         (size_t)lds) != hipSuccess)
+            return 0;
+        cache_occ[pair][xi] = occ;
+        cache_key[pair][xi] = lds;
+    }
+    return occ * L.cus >= grid ? grid : 0;   // the exchange needs the whole grid resident
+}
+
+hipError_t launch_fused_layer(const Launch &L, int grid, const RouteArgs &route, const void *x,
+                              int x_dt, int hidden, int inter, const Sections &sec, int bias_dt,
+                              uint16_t *act, int act_kind, float limit, float alpha, float *out,
+                              uint16_t *out_bf16, const SyncArgs &sync)
+{
+    const int pair = fused_shape_pair(hidden, inter);
+    if (pair < 0 || route.tokens != 1 || grid <= 0) return hipErrorInvalidValue;
+    const RowShape g = row_shape(hidden / 32), d = row_shape(inter / 32);
+    const int nmax = (hidden + grid - 1) / grid;
+    const size_t lds = (size_t)fused_layer_lds_bytes(hidden, inter, x_dt, route.top_k, grid);
+    auto go = [&](auto xk, auto sg, auto sd) {
+        constexpr int XK = decltype(xk)::value;
+        using SG = decltype(sg);
+        using SD = decltype(sd);
+        hipLaunchKernelGGL((moe_layer_kernel<XK, SG, SD>), dim3(grid), dim3(kNT), lds, L.stream,
+                           route, x, hidden, inter, sec, bias_dt, act, act_kind, limit, alpha,
+                           out, out_bf16, sync, g.chunks, d.chunks, nmax);
+    };
+    using F32c = std::integral_constant<int, DT_F32>;
+    using F16c = std::integral_constant<int, DT_F16>;
+    using B16c = std::integral_constant<int, DT_BF16>;
+    if (pair == 0) {
+        if (x_dt == DT_F32) go(F32c{}, S3{}, S3{});
+        else if (x_dt == DT_F16) go(F16c{}, S3{}, S3{});
+        else go(B16c{}, S3{}, S3{});
+    } else {
+        if (x_dt == DT_F32) go(F32c{}, S2{}, S1{});
+        else if (x_dt == DT_F16) go(F16c{}, S2{}, S1{});
+        else go(B16c{}, S2{}, S1{});
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_down(const Launch &L, const Plan *plan, int max_tokens, int max_slots,

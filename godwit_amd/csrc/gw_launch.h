@@ -26,6 +26,14 @@ struct RouteArgs {
     float *w_out;                 // optional [tokens, top_k]
 };
 
+// State of the fused layer kernel's in-kernel exchange (owned by a runner).
+struct SyncArgs {
+    unsigned *counters;   // 16 counters, 256 bytes apart
+    unsigned *epochs;     // per workgroup: launches it has completed
+    unsigned *err;        // nonzero once a bounded wait gave up
+};
+constexpr int kSyncWords = 16 * 64;
+
 // Lanes per row and blocks per lane chosen for a row of `bpr` MXFP4 blocks.
 struct RowShape { int tpr; int m; int chunks; };
 RowShape row_shape(int bpr);
@@ -52,6 +60,13 @@ constexpr int kFusedRouteExperts = 256;
 hipError_t launch_down(const Launch &L, const Plan *plan, int max_tokens, int max_slots,
                        const uint16_t *act, int hidden, int inter, const Sections &sec,
                        int bias_dt, float *out, uint16_t *out_bf16, int accumulate);
+// Grid of the fused one-token layer kernel for this shape (0 = not available:
+// shape not built, too few rows per workgroup, or the grid cannot be resident).
+int fused_layer_grid(const Launch &L, int hidden, int inter, int x_dt, int top_k, int experts);
+hipError_t launch_fused_layer(const Launch &L, int grid, const RouteArgs &route, const void *x,
+                              int x_dt, int hidden, int inter, const Sections &sec, int bias_dt,
+                              uint16_t *act, int act_kind, float limit, float alpha, float *out,
+                              uint16_t *out_bf16, const SyncArgs &sync);
 hipError_t launch_fill_u8(const Launch &L, void *dst, size_t count, int lo, int hi,
                           uint64_t seed);
 hipError_t launch_fill_normal(const Launch &L, void *dst, int dt, size_t count, float mean,
