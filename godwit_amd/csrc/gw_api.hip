@@ -101,24 +101,31 @@ static hipEvent_t take_event(gw_context *ctx)
 }
 
 // Brackets one launch with events when profiling (never inside a capture).
+// Times one kernel launch under a name.  launch(L) hands the launcher an
+// event pair that the kernel's own dispatch records (hipExtLaunchKernel), so
+// the figure is the kernel's duration, without the gaps that separate event
+// packets would add around it.
 struct ProfScope {
     gw_context *ctx;
     const char *name;
-    hipEvent_t start = nullptr;
-    ProfScope(gw_context *c, const char *n) : ctx(c), name(n)
+    hipEvent_t start = nullptr, end = nullptr;
+    ProfScope(gw_context *c, const char *n) : ctx(c), name(n) {}
+    gw::Launch launch(gw::Launch L)
     {
-        if (ctx->profiling && !ctx->capturing) {
+        if (ctx->profiling && !ctx->capturing && !start) {
             start = take_event(ctx);
-            if (start) (void)hipEventRecord(start, ctx->stream);
+            end = start ? take_event(ctx) : nullptr;
+            if (start && end) {
+                L.ev_start = start;
+                L.ev_stop = end;
+            }
         }
+        return L;
     }
     ~ProfScope()
     {
-        if (!start) return;
-        hipEvent_t end = take_event(ctx);
-        if (!end) return;
-        (void)hipEventRecord(end, ctx->stream);
-        ctx->events.push_back({name, start, end});
+        if (start && end) ctx->events.push_back({name, start, end});
+        else if (start) ctx->event_pool.push_back(start);
     }
 };
 
@@ -215,7 +222,12 @@ static int collect_events(gw_context *ctx)
     GW_HIP(hipStreamSynchronize(ctx->stream));
     for (auto &p : ctx->events) {
         float ms = 0.0f;
-        GW_HIP(hipEventElapsedTime(&ms, p.start, p.end));
+        // A launcher that returned before launching (empty input) left its
+        // events unrecorded: that entry is skipped.
+        if (hipEventElapsedTime(&ms, p.start, p.end) != hipSuccess) {
+            (void)hipGetLastError();
+            continue;
+        }
         bool found = false;
         for (auto &t : ctx->totals) {
             if (t.first == p.name) {
@@ -327,7 +339,7 @@ extern "C" int gw_fill_uniform_u8(gw_context *ctx, void *dst, size_t count, int 
     GW_CHECK(count == 0 || dst, GW_ERR_ARG, "null pointer");
     GW_CHECK(lo >= 0 && hi <= 255 && lo <= hi, GW_ERR_ARG, "bad range [%d, %d]", lo, hi);
     ProfScope ps(ctx, "fill");
-    GW_HIP(gw::launch_fill_u8(launch_of(ctx), dst, count, lo, hi, seed));
+    GW_HIP(gw::launch_fill_u8(ps.launch(launch_of(ctx)), dst, count, lo, hi, seed));
     return GW_OK;
 }
 
@@ -338,7 +350,7 @@ extern "C" int gw_fill_normal(gw_context *ctx, void *dst, gw_dtype dtype, size_t
     GW_CHECK(count == 0 || dst, GW_ERR_ARG, "null pointer");
     GW_CHECK(dtype_ok(dtype), GW_ERR_ARG, "bad dtype %d", (int)dtype);
     ProfScope ps(ctx, "fill");
-    GW_HIP(gw::launch_fill_normal(launch_of(ctx), dst, dtype, count, mean, stddev, seed));
+    GW_HIP(gw::launch_fill_normal(ps.launch(launch_of(ctx)), dst, dtype, count, mean, stddev, seed));
     return GW_OK;
 }
 
@@ -395,7 +407,7 @@ extern "C" int gw_mxfp4_dequant(gw_context *ctx, const uint8_t *packed, const ui
     GW_CHECK(aligned16(packed) && aligned16(out), GW_ERR_ARG,
              "packed and out must be 16-byte aligned");
     ProfScope ps(ctx, "dequant");
-    GW_HIP(gw::launch_dequant(launch_of(ctx), packed, scales, blocks, out));
+    GW_HIP(gw::launch_dequant(ps.launch(launch_of(ctx)), packed, scales, blocks, out));
     return GW_OK;
 }
 
@@ -430,7 +442,7 @@ extern "C" int gw_mxfp4_gemv_bias(gw_context *ctx, const uint8_t *packed, const 
         return GW_OK;
     }
     ProfScope ps(ctx, "gemv");
-    GW_HIP(gw::launch_gemv(launch_of(ctx), packed, scales, bias, bias ? (int)bias_dtype : -1, x,
+    GW_HIP(gw::launch_gemv(ps.launch(launch_of(ctx)), packed, scales, bias, bias ? (int)bias_dtype : -1, x,
                            x_dtype, y, (int)rows, (int)cols));
     return GW_OK;
 }
@@ -452,7 +464,7 @@ extern "C" int gw_expert_activation(gw_context *ctx, gw_activation kind, const f
     if (width == 0) return GW_OK;
     GW_CHECK(gate_up && out_f16, GW_ERR_ARG, "null pointer");
     ProfScope ps(ctx, "activation");
-    GW_HIP(gw::launch_activation(launch_of(ctx), (int)kind, gate_up, out_f16, width, limit,
+    GW_HIP(gw::launch_activation(ps.launch(launch_of(ctx)), (int)kind, gate_up, out_f16, width, limit,
                                  alpha));
     return GW_OK;
 }
@@ -465,7 +477,7 @@ extern "C" int gw_expert_accumulate(gw_context *ctx, const float *expert_out, fl
     if (width == 0) return GW_OK;
     GW_CHECK(expert_out && dst, GW_ERR_ARG, "null pointer");
     ProfScope ps(ctx, "accumulate");
-    GW_HIP(gw::launch_accumulate(launch_of(ctx), expert_out, dst, weight, width));
+    GW_HIP(gw::launch_accumulate(ps.launch(launch_of(ctx)), expert_out, dst, weight, width));
     return GW_OK;
 }
 
@@ -482,7 +494,7 @@ extern "C" int gw_router_logits(gw_context *ctx, const void *weight, gw_dtype we
     if (experts == 0 || tokens == 0) return GW_OK;
     GW_CHECK(weight && x && logits, GW_ERR_ARG, "null pointer");
     ProfScope ps(ctx, "router");
-    GW_HIP(gw::launch_router(launch_of(ctx), weight, weight_dtype, bias,
+    GW_HIP(gw::launch_router(ps.launch(launch_of(ctx)), weight, weight_dtype, bias,
                              bias ? (int)bias_dtype : -1, x, x_dtype, logits, (int)experts,
                              (int)hidden, tokens));
     return GW_OK;
@@ -542,7 +554,7 @@ struct gw_expert_runner {
     float *logits = nullptr;         // [kMaxTokens, kMaxExperts]
     Plan *staging = nullptr;         // pinned host mirror of `plans`
     unsigned *sync_buf = nullptr;    // fused layer exchange: counters | epochs | error word
-    bool fused_enabled = true;       // GODWIT_FUSED_LAYER=0 at creation turns it off
+    bool fused_enabled = false;      // GODWIT_FUSED_LAYER=1 at creation turns it on
     int ring_next = 0;
     int ring_used = 0;
 };
@@ -613,7 +625,7 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
                     hipGetErrorString(e));
     }
     const char *env = getenv("GODWIT_FUSED_LAYER");
-    r->fused_enabled = !(env && env[0] == '0');
+    r->fused_enabled = env && env[0] == '1';
     *out = r;
     return GW_OK;
 }
@@ -724,14 +736,14 @@ static int run_plan(gw_expert_runner *r, HostPlan &hp, const int64_t offsets[GW_
              (long long)r->hidden);
     {
         ProfScope ps(ctx, "gate_up");
-        GW_HIP(gw::launch_gate_up(L, r->plans + slot, nullptr, q.ntokens, inputs, x_dt,
+        GW_HIP(gw::launch_gate_up(ps.launch(L), r->plans + slot, nullptr, q.ntokens, inputs, x_dt,
                                   (int)r->hidden,
                                   (int)r->inter, sec, r->bias_dt, r->act_buf, r->act, r->limit,
                                   r->alpha));
     }
     {
         ProfScope ps(ctx, "down");
-        GW_HIP(gw::launch_down(L, r->plans + slot, q.ntokens, q.nslots, r->act_buf,
+        GW_HIP(gw::launch_down(ps.launch(L), r->plans + slot, q.ntokens, q.nslots, r->act_buf,
                                (int)r->hidden, (int)r->inter, sec, r->bias_dt, outputs, nullptr,
                                accumulate));
     }
@@ -933,7 +945,7 @@ extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args
     if (!logits) {
         GW_CHECK(dtype_ok(a->router_weight_dtype), GW_ERR_ARG, "bad router dtype");
         ProfScope ps(ctx, "router");
-        GW_HIP(gw::launch_router(L, a->router_weight, a->router_weight_dtype, a->router_bias,
+        GW_HIP(gw::launch_router(ps.launch(L), a->router_weight, a->router_weight_dtype, a->router_bias,
                                  a->router_bias ? (int)a->router_bias_dtype : -1, a->x,
                                  a->x_dtype, r->logits, (int)a->expert_count, (int)r->hidden,
                                  a->tokens));
@@ -959,7 +971,7 @@ extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args
                                               (int)a->top_k, (int)a->expert_count);
         if (grid > 0 && grid <= kSyncEpochWords) {
             ProfScope ps(ctx, "moe_layer");
-            GW_HIP(gw::launch_fused_layer(L, grid, route, a->x, a->x_dtype, (int)r->hidden,
+            GW_HIP(gw::launch_fused_layer(ps.launch(L), grid, route, a->x, a->x_dtype, (int)r->hidden,
                                           (int)r->inter, sec, r->bias_dt, r->act_buf, r->act,
                                           r->limit, r->alpha, a->out, a->out_bf16, sync_of(r)));
             return GW_OK;
@@ -970,17 +982,17 @@ extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args
     const bool fused = a->expert_count <= gw::kFusedRouteExperts;
     if (!fused) {
         ProfScope ps(ctx, "route");
-        GW_HIP(gw::launch_route(L, route, r->route_plan));
+        GW_HIP(gw::launch_route(ps.launch(L), route, r->route_plan));
     }
     {
         ProfScope ps(ctx, "gate_up");
-        GW_HIP(gw::launch_gate_up(L, r->route_plan, fused ? &route : nullptr, a->tokens, a->x,
+        GW_HIP(gw::launch_gate_up(ps.launch(L), r->route_plan, fused ? &route : nullptr, a->tokens, a->x,
                                   a->x_dtype, (int)r->hidden, (int)r->inter, sec, r->bias_dt,
                                   r->act_buf, r->act, r->limit, r->alpha));
     }
     {
         ProfScope ps(ctx, "down");
-        GW_HIP(gw::launch_down(L, r->route_plan, a->tokens, (int)(a->tokens * a->top_k), r->act_buf,
+        GW_HIP(gw::launch_down(ps.launch(L), r->route_plan, a->tokens, (int)(a->tokens * a->top_k), r->act_buf,
                                (int)r->hidden, (int)r->inter, sec, r->bias_dt, a->out,
                                a->out_bf16, 0));
     }

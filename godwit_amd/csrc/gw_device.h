@@ -87,10 +87,13 @@ template <> __device__ __forceinline__ void widen<DT_F32>(const uint4 &w, WBlock
 template <int XK> __device__ __forceinline__ float block_dot(const WBlock<XK> &w,
                                                             const uint32_t *xb);
 
-template <> __device__ __forceinline__ float block_dot<DT_BF16>(const WBlock<DT_BF16> &w,
-                                                               const uint32_t *xb)
+// The same dot with the activation block already in registers (16-bit x).
+template <int XK> __device__ __forceinline__ float block_dot_r(const WBlock<XK> &w,
+                                                              const uint4 (&x)[4]);
+
+template <> __device__ __forceinline__ float block_dot_r<DT_BF16>(const WBlock<DT_BF16> &w,
+                                                                 const uint4 (&xv)[4])
 {
-    const uint4 *xv = reinterpret_cast<const uint4 *>(xb);
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -107,10 +110,9 @@ template <> __device__ __forceinline__ float block_dot<DT_BF16>(const WBlock<DT_
     return a0 + a1;
 }
 
-template <> __device__ __forceinline__ float block_dot<DT_F16>(const WBlock<DT_F16> &w,
-                                                              const uint32_t *xb)
+template <> __device__ __forceinline__ float block_dot_r<DT_F16>(const WBlock<DT_F16> &w,
+                                                                const uint4 (&xv)[4])
 {
-    const uint4 *xv = reinterpret_cast<const uint4 *>(xb);
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -125,6 +127,22 @@ template <> __device__ __forceinline__ float block_dot<DT_F16>(const WBlock<DT_F
                                     __builtin_bit_cast(f16x2, x.w), a1, false);
     }
     return a0 + a1;
+}
+
+template <> __device__ __forceinline__ float block_dot<DT_BF16>(const WBlock<DT_BF16> &w,
+                                                               const uint32_t *xb)
+{
+    const uint4 *xv = reinterpret_cast<const uint4 *>(xb);
+    const uint4 x[4] = {xv[0], xv[1], xv[2], xv[3]};
+    return block_dot_r<DT_BF16>(w, x);
+}
+
+template <> __device__ __forceinline__ float block_dot<DT_F16>(const WBlock<DT_F16> &w,
+                                                              const uint32_t *xb)
+{
+    const uint4 *xv = reinterpret_cast<const uint4 *>(xb);
+    const uint4 x[4] = {xv[0], xv[1], xv[2], xv[3]};
+    return block_dot_r<DT_F16>(w, x);
 }
 
 template <> __device__ __forceinline__ float block_dot<DT_F32>(const WBlock<DT_F32> &w,
@@ -155,13 +173,26 @@ __device__ __forceinline__ void stage_vector(uint32_t *dst, const void *src, int
 {
     constexpr int BD = XL<XK>::kBlockDw;
     if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+        // Batches of 4 loads per thread in flight together.  Indices are
+        // clamped rather than guarded, so loads and stores are unconditional
+        // (a guard lets the compiler sink each load to its store, one round
+        // trip per load); the clamped duplicates store equal values.
         constexpr int Q = XK == DT_F32 ? 8 : 4;        // 16-byte chunks of data per block
         constexpr int BQ = BD / 4;                      // 16-byte chunks per block in LDS
         const uint4 *s = static_cast<const uint4 *>(src);
         uint4 *d = reinterpret_cast<uint4 *>(dst);
         const int n4 = XK == DT_F32 ? n / 4 : n / 8;
-#pragma unroll 4
-        for (int i = tid; i < n4; i += nthr) d[(i / Q) * BQ + (i % Q)] = s[i];
+        for (int base = 0; base < n4; base += 4 * nthr) {
+            uint4 v[4];
+            int idx[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                idx[u] = min(base + u * nthr + tid, n4 - 1);
+                v[u] = s[idx[u]];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) d[(idx[u] / Q) * BQ + (idx[u] % Q)] = v[u];
+        }
     } else if constexpr (XK == DT_F32) {
         const float *s = static_cast<const float *>(src);
 #pragma unroll 4

@@ -9,18 +9,32 @@
 //     them with v_dot2c_f32_{bf16,f16} (or v_fma_f32 for f32 x), one fp32
 //     partial per block scaled by its e8m0 scale, accumulated per lane;
 //   * the row sum is a TPR-lane shuffle reduction;
-//   * loads for the next row group are issued before the current one is
-//     consumed (register double buffering), so a workgroup keeps two row
-//     groups of weights in flight.
+//   * a ring of row groups (stages) in registers keeps several groups' loads
+//     in flight; on the decode shapes the ring holds a workgroup's whole share,
+//     so every load goes out at once and compute follows the data.
 // Rows are split over a fixed grid in contiguous, balanced ranges (the
 // reference's persistent kernel, expert.metal:138-183, strides rows over 64
 // threadgroups instead).
+#include <hip/hip_ext.h>
+
 #include <type_traits>
 
 #include "gw_device.h"
 #include "gw_launch.h"
 
 namespace gw {
+
+// Launches on the Launch's stream; when the Launch carries a start/stop event
+// pair (profiling), they are attached to the kernel's own dispatch, so they
+// time the kernel alone, not the gaps around it.
+#define GW_LAUNCH(KERNEL, GRID, BLOCK, LDS, L, ...)                                          \
+    do {                                                                                      \
+        if ((L).ev_start)                                                                     \
+            hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, (L).stream, (L).ev_start,          \
+                                  (L).ev_stop, 0, __VA_ARGS__);                               \
+        else                                                                                  \
+            hipLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, (L).stream, __VA_ARGS__);            \
+    } while (0)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -46,15 +60,33 @@ __device__ __forceinline__ uint32_t load_scale(const uint8_t *row, int cb)
 // M*TPR blocks).  Compile-time, so every stage issues a fixed number of loads
 // and the compiler can wait for exactly the older stage (s_waitcnt vmcnt(N))
 // instead of draining the prefetched one too.
-template <int TPR_, int M_> struct Shape {
+template <int TPR_, int M_, bool CHUNKED_ = false> struct Shape {
     static constexpr int TPR = TPR_;
     static constexpr int M = M_;
+    static constexpr bool CHUNKED = CHUNKED_;   // rows may span several chunks
 };
 using S0 = Shape<8, 1>;    // bpr <= 8
 using S1 = Shape<8, 3>;    // bpr <= 24   (Qwen3 down: 24)
 using S2 = Shape<16, 4>;   // bpr <= 64   (Qwen3 gate_up: 64)
 using S3 = Shape<16, 6>;   // bpr <= 96   (GPT-OSS: 90)
-using S4 = Shape<16, 8>;   // wider rows, in chunks of 128 blocks
+using S4 = Shape<16, 8, true>;   // wider rows, in chunks of 128 blocks
+
+// A lane sees the same activation blocks in every stage (blocks lane + m*TPR
+// of one chunk), so when every row is dotted with the same 16-bit vector
+// (UNIFORM: one token, one shared input) and rows are unchunked, the blocks
+// are read from LDS once, into registers, instead of once per stage.  (The
+// down projection dots each expert's rows with that expert's own activation,
+// so it never qualifies.)
+template <int XK, int MT, class SH, bool UNIFORM> struct XRegs {
+    static constexpr bool kOn = UNIFORM && MT == 1 && XK != DT_F32 && !SH::CHUNKED;
+    uint4 v[kOn ? SH::M : 1][4];
+};
+
+// Stages in flight per engine: a decode workgroup's gate_up share is three
+// 16-row stages (GPT-OSS, 512 workgroups) and its down share two.
+constexpr int kGateUpDepth = 3;
+constexpr int kDownDepth = 2;
+constexpr int kGemvDepth = 3;
 
 RowShape row_shape(int bpr)
 {
@@ -120,6 +152,17 @@ __device__ __forceinline__ void divmod_small(int a, int d, float inv_d, int &q, 
     r = r >= d ? r - d : r;
 }
 
+// This workgroup's share [lo, hi) of `total` items in balanced contiguous
+// ranges (the first total % G workgroups take one more), with one 32-bit
+// division instead of 64-bit products and quotients.
+__device__ __forceinline__ void slice_of(int total, int &lo, int &hi)
+{
+    const unsigned G = gridDim.x, b = blockIdx.x;
+    const unsigned q = (unsigned)total / G, r = (unsigned)total - q * G;
+    lo = (int)(b * q + min(b, r));
+    hi = lo + (int)q + (b < r ? 1 : 0);
+}
+
 // Sum over the TPR lanes of a row segment with DPP butterflies inside a
 // 16-lane row (pair swap, quad swap, half mirror, mirror): every lane ends with
 // the same bits (each step adds two equal partial sums in either order).
@@ -136,8 +179,9 @@ template <int TPR> __device__ __forceinline__ float seg_sum(float v)
 #undef GW_DPPF
 
 // Issues the M block loads (and M scale loads) of one stage.  Every lane issues
-// all of them: a row past the end re-reads the last row, a column past the end
-// re-reads the row's last block; consume() ignores those values.
+// all of them: a column past the end re-reads the row's last block, and a row
+// past the end reads the last row's first block on every lane (one cache line
+// per load instruction); consume() ignores those values.
 template <int MT, class SH, class RowFn>
 __device__ __forceinline__ void issue(Stage<MT, SH::M> &S, int it, int chunks, int bpr,
                                       int n_items, RowFn &rowfn)
@@ -157,7 +201,7 @@ __device__ __forceinline__ void issue(Stage<MT, SH::M> &S, int it, int chunks, i
     const int cb0 = c * M * TPR + lane;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-        const int cb = min(cb0 + m * TPR, bpr - 1);
+        const int cb = S.valid ? min(cb0 + m * TPR, bpr - 1) : 0;
         S.w[m] = load_block(ref.packed, cb);
         S.s[m] = load_scale(ref.scales, cb);
     }
@@ -166,25 +210,51 @@ __device__ __forceinline__ void issue(Stage<MT, SH::M> &S, int it, int chunks, i
     S.bw = *(const __attribute__((address_space(1))) uint32_t *)(ba & ~(uintptr_t)3);
 }
 
-template <int XK, int MT, class SH, class EpiFn>
+template <int XK, int MT, class SH, bool U>
+__device__ __forceinline__ void load_xregs(XRegs<XK, MT, SH, U> &X, const uint32_t *xs, int bpr)
+{
+    if constexpr (XRegs<XK, MT, SH, U>::kOn) {
+        constexpr int BD = XL<XK>::kBlockDw;
+        const int lane = threadIdx.x % SH::TPR;
+#pragma unroll
+        for (int m = 0; m < SH::M; ++m) {
+            const int cb = lane + m * SH::TPR;
+            const uint4 *xv = reinterpret_cast<const uint4 *>(xs + (cb < bpr ? cb : 0) * BD);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) X.v[m][q] = xv[q];
+        }
+    }
+}
+
+template <int XK, int MT, class SH, bool U, class EpiFn>
 __device__ __forceinline__ void consume(Stage<MT, SH::M> &S, float (&acc)[MT], int chunks,
-                                        int bpr, const uint32_t *xs, EpiFn &epi)
+                                        int bpr, const uint32_t *xs,
+                                        const XRegs<XK, MT, SH, U> &X, EpiFn &epi)
 {
     constexpr int TPR = SH::TPR, M = SH::M;
     constexpr int BD = XL<XK>::kBlockDw;
     const int lane = threadIdx.x % TPR;
     const int cb0 = S.chunk * M * TPR + lane;
+    // Every block is computed; a block past the row's end (or of a row past
+    // the end) contributes through a select, never a branch.  Its activation
+    // read stays inside the staged vectors' LDS (block 0 for such rows).
 #pragma unroll
     for (int m = 0; m < M; ++m) {
         const int cb = cb0 + m * TPR;
-        if (S.valid && cb < bpr) {
-            WBlock<XK> wb;
-            widen_u(S.w[m], wb);
-            const float sc = decode_scale(S.s[m]);
-            const uint32_t *xb = xs + cb * BD;
+        const bool use = S.valid && cb < bpr;
+        WBlock<XK> wb;
+        widen_u(S.w[m], wb);
+        const float sc = decode_scale(S.s[m]);
+        if constexpr (XRegs<XK, MT, SH, U>::kOn) {
+            const float d = block_dot_r<XK>(wb, X.v[m]) * sc;
+            acc[0] += use ? d : 0.0f;
+        } else {
+            const uint32_t *xb = xs + (use ? cb : 0) * BD;
 #pragma unroll
-            for (int t = 0; t < MT; ++t)
-                if (t < S.ntok) acc[t] += block_dot<XK>(wb, xb + S.xoff[t]) * sc;
+            for (int t = 0; t < MT; ++t) {
+                const float d = block_dot<XK>(wb, xb + S.xoff[t]) * sc;
+                acc[t] += (use && t < S.ntok) ? d : 0.0f;
+            }
         }
     }
     if (S.chunk == chunks - 1) {
@@ -196,35 +266,66 @@ __device__ __forceinline__ void consume(Stage<MT, SH::M> &S, float (&acc)[MT], i
     }
 }
 
-// Runs `n_items` rows (RowFn maps item -> RowRef) through the engine, calling
-// EpiFn(item, valid, ntok, acc, bias_word, bias_shift) once per row group with
-// every lane holding its row's fp32 sums.  All threads of the workgroup must
-// call it.
-//
-// Stages go in straight-line batches of kDepth: all loads of a batch are
-// issued (unconditionally; stages past the end re-read the last row and are
-// never consumed), then the stages are consumed in order.  With no control
-// flow between a load and its use, the compiler waits for exactly the stage it
-// consumes (s_waitcnt vmcnt(N)) while the younger stages stay in flight.
-// Grids are sized so a workgroup's rows fit one batch on the decode shapes.
-constexpr int kDepth = 3;
+// A ring of D stages in registers.  prime() issues the first D stages (the
+// loads only); run() consumes every stage in order and reissues each ring
+// slot D stages ahead, so up to D stages are in flight.  On the decode shapes
+// D covers a workgroup's whole share, so all of its loads go out at once and
+// compute follows the data as it arrives; a launch is one pass, not a steady
+// state, so a shallower ring leaves the memory system idle while every
+// workgroup computes its first stage.
+template <int D, int MT, class SH> struct EngineRing {
+    Stage<MT, SH::M> S[D];
+};
 
-template <int XK, int MT, class SH, class RowFn, class EpiFn>
-__device__ __forceinline__ void row_engine(int n_items, int chunks, int bpr,
-                                           const uint32_t *xs, RowFn rowfn, EpiFn epi)
+template <int D, int MT, class SH, class RowFn>
+__device__ __forceinline__ void engine_prime(EngineRing<D, MT, SH> &E, int n_items, int chunks,
+                                             int bpr, RowFn &rowfn)
+{
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue<MT, SH>(E.S[d], d, chunks, bpr, n_items, rowfn);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// The scheduling barriers keep every issue ahead of the next consume: left
+// free, the scheduler sinks loads below that consume's wait (their addresses
+// come from LDS).  Stages past the end are never issued by run(); prime()
+// issues them unconditionally (one line per load), so the compiler always
+// waits for exactly the stage it consumes (s_waitcnt vmcnt(N)).
+template <int D, int XK, int MT, class SH, bool UNIFORM, class RowFn, class EpiFn>
+__device__ __forceinline__ void engine_run(EngineRing<D, MT, SH> &E, int n_items, int chunks,
+                                           int bpr, const uint32_t *xs, RowFn &rowfn, EpiFn &epi)
 {
     constexpr int RG = kNT / SH::TPR;
     const int nit = ((n_items + RG - 1) / RG) * chunks;
+    XRegs<XK, MT, SH, UNIFORM> X;
+    load_xregs(X, xs, bpr);
     float acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
-    for (int base = 0; base < nit; base += kDepth) {
-        Stage<MT, SH::M> S[kDepth];
+    for (int base = 0; base < nit; base += D) {
 #pragma unroll
-        for (int d = 0; d < kDepth; ++d) issue<MT, SH>(S[d], base + d, chunks, bpr, n_items, rowfn);
-#pragma unroll
-        for (int d = 0; d < kDepth; ++d) consume<XK, MT, SH>(S[d], acc, chunks, bpr, xs, epi);
+        for (int d = 0; d < D; ++d) {
+            if (base + d < nit) {
+                consume(E.S[d], acc, chunks, bpr, xs, X, epi);
+                if (base + d + D < nit) issue<MT, SH>(E.S[d], base + d + D, chunks, bpr, n_items, rowfn);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
+}
+
+// Runs `n_items` rows (RowFn maps item -> RowRef) through the engine, calling
+// EpiFn(item, valid, ntok, acc, bias_word, bias_shift) once per row group with
+// every lane holding its row's fp32 sums.  All threads of the workgroup must
+// call it.  The loop body holds one copy of each ring slot's (consume, issue)
+// pair, so the code stays small.
+template <int D, int XK, int MT, class SH, bool UNIFORM, class RowFn, class EpiFn>
+__device__ __forceinline__ void row_engine(int n_items, int chunks, int bpr,
+                                           const uint32_t *xs, RowFn rowfn, EpiFn epi)
+{
+    EngineRing<D, MT, SH> E;
+    engine_prime<D, MT, SH>(E, n_items, chunks, bpr, rowfn);
+    engine_run<D, XK, MT, SH, UNIFORM>(E, n_items, chunks, bpr, xs, rowfn, epi);
 }
 
 static_assert(sizeof(Plan) % 16 == 0, "plans are copied in 16-byte chunks");
@@ -281,9 +382,37 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t x)
 // (NaN and out-of-range positions never win, as `>` never picks them).
 __device__ __forceinline__ uint32_t order_key(float v)
 {
-    const uint32_t u = __float_as_uint(v);
+    const uint32_t u = v == 0.0f ? 0u : __float_as_uint(v);   // -0 and +0 compare equal
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+
+// Wave-wide max / min left in every lane, entirely in VALU: DPP-combined
+// steps inside each 16-lane row, then v_permlane16_swap / v_permlane32_swap
+// exchange rows and halves (gfx950), so no value goes through an SGPR.
+#define GW_DPPC(x, ctrl) ((uint32_t)__builtin_amdgcn_mov_dpp((int)(x), (ctrl), 0xF, 0xF, true))
+__device__ __forceinline__ uint32_t wave_allmax_u32(uint32_t x)
+{
+    x = max(x, GW_DPPC(x, 0xB1));
+    x = max(x, GW_DPPC(x, 0x4E));
+    x = max(x, GW_DPPC(x, 0x141));
+    x = max(x, GW_DPPC(x, 0x140));
+    const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = max(p[0], p[1]);
+    const auto q = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return max(q[0], q[1]);
+}
+__device__ __forceinline__ uint32_t wave_allmin_u32(uint32_t x)
+{
+    x = min(x, GW_DPPC(x, 0xB1));
+    x = min(x, GW_DPPC(x, 0x4E));
+    x = min(x, GW_DPPC(x, 0x141));
+    x = min(x, GW_DPPC(x, 0x140));
+    const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = min(p[0], p[1]);
+    const auto q = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return min(q[0], q[1]);
+}
+#undef GW_DPPC
 
 __device__ __forceinline__ float lane_value(float v, int lane)
 {
@@ -436,6 +565,101 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
     }
 }
 
+// Routing of ONE token by one wave, branch-free: Router.select's selection
+// sort (Router.swift:78-98) tracked per element instead of per position.
+// Lane l holds elements l, l+64, ... (R per lane) with their current position
+// in the sort's permutation.  Step p picks the largest logit among unselected
+// elements, the smallest current position among ties (the strict `>` scan
+// from p keeps the first), or the element at p itself when its logit is NaN
+// (nothing compares greater than NaN); then it swaps positions exactly as
+// `order.swapAt(p, best)`.  The plan is the single-token demand map: group,
+// slot and rank k are the k-th selected expert.
+template <int R>
+__device__ __forceinline__ void route_one(const float *__restrict__ logits, int E, int K,
+                                          const uint8_t *experts_base, int64_t stride,
+                                          Plan *plan, int32_t *ids_out, float *w_out)
+{
+    const int lane = threadIdx.x & 63;
+    float v[R];
+    uint32_t cp[R];
+    bool sel[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = lane + 64 * r;
+        v[r] = logits[min(i, E - 1)];
+        cp[r] = (uint32_t)i;
+        sel[r] = i >= E;            // elements past E never take part
+    }
+    int sid = 0;                    // lane k < K: expert of rank k
+    float sv = 0.0f;                // and its logit
+    for (int pos = 0; pos < K; ++pos) {
+        uint32_t km = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            km = max(km, (sel[r] || __builtin_isnan(v[r])) ? 0u : order_key(v[r]));
+        const uint32_t kmax = wave_allmax_u32(km);
+        uint32_t pm = 0xFFFFFFFFu;
+        bool nan_here = false;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const bool cand = !sel[r] && !__builtin_isnan(v[r]) && kmax != 0u &&
+                              order_key(v[r]) == kmax;
+            pm = cand ? min(pm, cp[r]) : pm;
+            nan_here |= !sel[r] && cp[r] == (uint32_t)pos && __builtin_isnan(v[r]);
+        }
+        const uint32_t pmin = wave_allmin_u32(pm);
+        const bool nan_at_pos = __ballot(nan_here) != 0ull;
+        const uint32_t best = (pmin == 0xFFFFFFFFu || nan_at_pos) ? (uint32_t)pos : pmin;
+        int my_id = 0;
+        float my_v = 0.0f;
+        bool mine = false;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const bool at_best = !sel[r] && cp[r] == best;
+            const bool at_pos = !sel[r] && cp[r] == (uint32_t)pos;
+            my_id = at_best ? lane + 64 * r : my_id;
+            my_v = at_best ? v[r] : my_v;
+            mine |= at_best;
+            cp[r] = at_best ? (uint32_t)pos : (at_pos ? best : cp[r]);
+            sel[r] = sel[r] || at_best;
+        }
+        const int src = (int)__builtin_ctzll(__ballot(mine));
+        const int id = __builtin_amdgcn_readlane(my_id, src);
+        const float val = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), src));
+        sid = lane == pos ? id : sid;
+        sv = lane == pos ? val : sv;
+    }
+    // Softmax over the K selected logits (peak subtracted, summed in rank order).
+    float peak = lane_value(sv, 0);
+    for (int i = 1; i < K; ++i) {
+        const float x = lane_value(sv, i);
+        peak = x > peak ? x : peak;
+    }
+    const float ex = expf(sv - peak);
+    float total = 0.0f;
+    for (int i = 0; i < K; ++i) total += lane_value(ex, i);
+    const float w = ex / total;
+    if (lane < K) {
+        if (ids_out) ids_out[lane] = sid;
+        if (w_out) w_out[lane] = w;
+        plan->group_base[lane] = experts_base + (int64_t)sid * stride;
+        plan->group_slot0[lane] = lane;
+        plan->group_ntok[lane] = 1;
+        plan->slot_token[lane] = 0;
+        plan->slot_group[lane] = lane;
+        plan->slot_weight[lane] = w;
+        plan->tok_slots[0][lane] = lane;
+    }
+    if (lane == 0) {
+        plan->tok_global[0] = 0;
+        plan->tok_nslots[0] = K;
+        plan->ngroups = K;
+        plan->nslots = K;
+        plan->ntokens = 1;
+        plan->pad0 = 0;
+    }
+}
+
 constexpr int kFusedRouteR = 4;      // fused routing handles up to 256 experts
 constexpr int kMaxExperts = 1024;    // the standalone route kernel, up to 1024
 
@@ -453,12 +677,12 @@ __global__ __launch_bounds__(kNT) void gemv_kernel(const uint8_t *__restrict__ p
                                                    int chunks)
 {
     constexpr int TPR = SH::TPR;
-    extern __shared__ uint32_t lds[];
+    extern __shared__ __align__(16) uint32_t lds[];
     uint32_t *xs = lds;
     stage_vector<XK>(xs, x, bpr * 32);
     __syncthreads();
-    const int r0 = (int)((int64_t)blockIdx.x * rows / gridDim.x);
-    const int r1 = (int)((int64_t)(blockIdx.x + 1) * rows / gridDim.x);
+    int r0, r1;
+    slice_of(rows, r0, r1);
     const int64_t row_bytes = (int64_t)bpr * 16;
     const int bsz = bias_dt == DT_F32 ? 4 : 2;
     auto rowfn = [&](int item) {
@@ -474,7 +698,7 @@ __global__ __launch_bounds__(kNT) void gemv_kernel(const uint8_t *__restrict__ p
     auto epi = [&](int item, bool valid, int, float (&acc)[1], uint32_t bw, int bsh) {
         if (valid && (threadIdx.x % TPR) == 0) y[r0 + item] = acc[0] + decode_bias(bw, bsh, bias_dt);
     };
-    row_engine<XK, 1, SH>(r1 - r0, chunks, bpr, xs, rowfn, epi);
+    row_engine<kGemvDepth, XK, 1, SH, true>(r1 - r0, chunks, bpr, xs, rowfn, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -491,7 +715,7 @@ __global__ __launch_bounds__(kNT) void gate_up_kernel(
     float limit, float alpha, int max_tokens, int chunks)
 {
     constexpr int TPR = SH::TPR;
-    extern __shared__ uint32_t lds[];
+    extern __shared__ __align__(16) uint32_t lds[];
     constexpr int BD = XL<XK>::kBlockDw;
     constexpr int ES = XK == DT_F32 ? 4 : 2;
     Plan *plan = reinterpret_cast<Plan *>(lds);
@@ -502,10 +726,16 @@ __global__ __launch_bounds__(kNT) void gate_up_kernel(
         // Wave 0 routes (every workgroup, redundantly: 4 x 128 logits) while the
         // other waves stage the inputs, which are rows 0..T-1 of x.
         if (threadIdx.x < 64) {
-            route_wave<kFusedRouteR>(route.logits, route.experts, route.top_k, route.tokens,
-                                     route.experts_base, route.stride, plan,
-                                     blockIdx.x == 0 ? route.ids_out : nullptr,
-                                     blockIdx.x == 0 ? route.w_out : nullptr);
+            if (route.tokens == 1)
+                route_one<kFusedRouteR>(route.logits, route.experts, route.top_k,
+                                        route.experts_base, route.stride, plan,
+                                        blockIdx.x == 0 ? route.ids_out : nullptr,
+                                        blockIdx.x == 0 ? route.w_out : nullptr);
+            else
+                route_wave<kFusedRouteR>(route.logits, route.experts, route.top_k, route.tokens,
+                                         route.experts_base, route.stride, plan,
+                                         blockIdx.x == 0 ? route.ids_out : nullptr,
+                                         blockIdx.x == 0 ? route.w_out : nullptr);
         } else {
             for (int t = 0; t < route.tokens && t < max_tokens; ++t)
                 stage_vector<XK>(xs + t * xstride,
@@ -526,15 +756,14 @@ __global__ __launch_bounds__(kNT) void gate_up_kernel(
         __syncthreads();
     }
 
-    const int64_t total = (int64_t)plan->ngroups * inter;   // (group, pair) space
-    const int64_t p0 = (int64_t)blockIdx.x * total / gridDim.x;
-    const int64_t p1 = (int64_t)(blockIdx.x + 1) * total / gridDim.x;
+    int p0, p1;                                        // (group, pair) space
+    slice_of(plan->ngroups * inter, p0, p1);
     const int64_t row_bytes = (int64_t)bpr * 16;
     const int bsz = bias_dt == DT_F32 ? 4 : 2;
     // (group, pair) of the range start, once; items step through pairs with
     // 32-bit arithmetic (a workgroup's range spans few groups).
-    const int g_start = (int)(p0 / inter);
-    const int i_start = (int)(p0 - (int64_t)g_start * inter);
+    const int g_start = (int)((unsigned)p0 / (unsigned)inter);
+    const int i_start = p0 - g_start * inter;
     const float inv_inter = 1.0f / (float)inter;
     auto locate = [&](int item, int &g, int &i) {
         int q, r;
@@ -580,7 +809,8 @@ __global__ __launch_bounds__(kNT) void gate_up_kernel(
             }
         }
     };
-    row_engine<XK, MT, SH>((int)(2 * (p1 - p0)), chunks, bpr, xs, rowfn, epi);
+    row_engine<(MT == 1 ? kGateUpDepth : 2), XK, MT, SH, true>(2 * (p1 - p0), chunks, bpr, xs,
+                                                                rowfn, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -596,7 +826,7 @@ __global__ __launch_bounds__(kNT) void down_kernel(
     int accumulate, int smax, int nmax, int chunks, int prestage)
 {
     constexpr int TPR = SH::TPR;
-    extern __shared__ uint32_t lds[];
+    extern __shared__ __align__(16) uint32_t lds[];
     constexpr int BD = XL<DT_F16>::kBlockDw;
     Plan *plan = reinterpret_cast<Plan *>(lds);
     const int bpr = inter >> 5;
@@ -611,8 +841,8 @@ __global__ __launch_bounds__(kNT) void down_kernel(
         stage_vector<DT_F16>(as + s * astride, act + (int64_t)s * inter, inter);
     __syncthreads();
 
-    const int r0 = (int)((int64_t)blockIdx.x * hidden / gridDim.x);
-    const int r1 = (int)((int64_t)(blockIdx.x + 1) * hidden / gridDim.x);
+    int r0, r1;
+    slice_of(hidden, r0, r1);
     const int n = r1 - r0;
     const int ngroups = plan->ngroups;
     const int64_t row_bytes = (int64_t)bpr * 16;
@@ -665,7 +895,8 @@ __global__ __launch_bounds__(kNT) void down_kernel(
                     if (t < ntok) vals[(sg + t) * nmax + q] = acc[t] + b;
             }
         };
-        row_engine<DT_F16, MT, SH>((g1 - g) * n, chunks, bpr, as, rowfn, epi);
+        row_engine<(MT == 1 ? kDownDepth : 2), DT_F16, MT, SH, false>((g1 - g) * n, chunks, bpr,
+                                                                    as, rowfn, epi);
         __syncthreads();
         g = g1;
     }
@@ -713,19 +944,17 @@ __global__ __launch_bounds__(256) void router_kernel(const void *__restrict__ W,
 // ---------------------------------------------------------------------------
 // Fused decode layer (one token): route -> gate_up + activation -> down +
 // weighted combine in ONE kernel.  Every workgroup owns a slice of the gate_up
-// rows and a slice of the output rows.  It issues the loads of both slices up
-// front, computes its gate_up rows and writes their activations with coherent
-// (sc1) stores, then signals one of 16 counters (spread over separate lines so
-// arrivals do not serialise on one address) and waits, with a bounded spin,
-// until every workgroup has signalled.  By then its down weights are already
-// in registers: it stages all activations (sc1 loads), finishes the down rows
+// rows and a slice of the output rows.  It computes its gate_up rows and
+// writes their activations with coherent (sc1) stores, then signals one of 16
+// counters (spread over separate lines so arrivals do not serialise on one
+// address) and waits, with a bounded spin, until every workgroup has
+// signalled.  It then stages all activations (sc1 loads), runs its down rows
 // and combines them in router order.  The grid must be co-resident (the host
 // checks occupancy); a wait that gives up sets *sync.err instead of hanging.
 // ---------------------------------------------------------------------------
 
-constexpr int kDownDepth = 2;
 constexpr int kSyncCounters = 16;
-constexpr int kSyncStride = 64;            // uint32 apart: one 256-byte line each
+constexpr int kSyncStride = 1088;          // uint32 apart: 4 KiB + 256 B, a separate page and line each
 constexpr unsigned kSpinLimit = 1u << 18;
 
 __device__ __forceinline__ void store_coherent_u16(uint16_t *p, uint16_t v)
@@ -747,24 +976,29 @@ __global__ __launch_bounds__(kNT) void moe_layer_kernel(
     float *__restrict__ out, uint16_t *__restrict__ out_bf16, SyncArgs sync, int chunks_g,
     int chunks_d, int nmax)
 {
-    extern __shared__ uint32_t lds[];
+    extern __shared__ __align__(16) uint32_t lds[];
     constexpr int BDX = XL<XK>::kBlockDw;
     constexpr int BDA = XL<DT_F16>::kBlockDw;
     constexpr int TPRG = SG::TPR, TPRD = SD::TPR;
-    __shared__ unsigned s_epoch;
     Plan *plan = reinterpret_cast<Plan *>(lds);
     const int bpr_g = hidden >> 5, bpr_d = inter >> 5;
     const int xstride = bpr_g * BDX, astride = bpr_d * BDA;
     const int K = route.top_k;
+    // Launches this workgroup has completed (uniform; written back at the end).
+    // Kept in a register: a static __shared__ variable here would shift the
+    // dynamic LDS off its 16-byte alignment and split every ds_read_b128.
+    const unsigned epoch1 = sync.epochs[blockIdx.x] + 1;
     uint32_t *xs = lds + sizeof(Plan) / 4;                     // [xstride]
     uint32_t *as = xs + xstride;                                // [K][astride]
     float *vals = reinterpret_cast<float *>(as + K * astride);  // [K][nmax]
+    // This workgroup's fp16 activations until they are stored; the area is
+    // free until the exchange (it later holds all experts' activations).
+    uint16_t *act_loc = reinterpret_cast<uint16_t *>(as);
 
     if (threadIdx.x < 64) {
-        route_wave<kFusedRouteR>(route.logits, route.experts, K, 1, route.experts_base,
-                                 route.stride, plan, blockIdx.x == 0 ? route.ids_out : nullptr,
-                                 blockIdx.x == 0 ? route.w_out : nullptr);
-        if (threadIdx.x == 0) s_epoch = sync.epochs[blockIdx.x];
+        route_one<kFusedRouteR>(route.logits, route.experts, K, route.experts_base,
+                                route.stride, plan, blockIdx.x == 0 ? route.ids_out : nullptr,
+                                blockIdx.x == 0 ? route.w_out : nullptr);
     } else {
         stage_vector<XK>(xs, x, hidden, threadIdx.x - 64, kNT - 64);
     }
@@ -775,13 +1009,12 @@ __global__ __launch_bounds__(kNT) void moe_layer_kernel(
     const int bsz = bias_dt == DT_F32 ? 4 : 2;
 
     // gate_up slice: (expert, pair) range [p0, p1)
-    const int64_t totg = (int64_t)K * inter;
-    const int64_t p0 = (int64_t)blockIdx.x * totg / G;
-    const int64_t p1 = (int64_t)(blockIdx.x + 1) * totg / G;
-    const int ng_items = (int)(2 * (p1 - p0));
-    const int g_start = (int)(p0 / inter);
-    const int i_start = (int)(p0 - (int64_t)g_start * inter);
+    int p0, p1;
+    slice_of(K * inter, p0, p1);
+    const int ng_items = 2 * (p1 - p0);
     const float inv_inter = 1.0f / (float)inter;
+    int g_start, i_start;
+    divmod_small(p0, inter, inv_inter, g_start, i_start);
     auto locate = [&](int item, int &g, int &i) {
         int q, r;
         divmod_small(i_start + (item >> 1), inter, inv_inter, q, r);
@@ -806,17 +1039,14 @@ __global__ __launch_bounds__(kNT) void moe_layer_kernel(
         const float b_own = decode_bias(bw, bsh, bias_dt);
         const float b_next = __shfl_down(b_own, TPRG);
         if (valid && (item & 1) == 0 && (threadIdx.x % TPRG) == 0) {
-            int g, i;
-            locate(item, g, i);
             const float v = apply_activation(act_kind, acc[0] + b_own, up + b_next, limit, alpha);
-            store_coherent_u16(act + (int64_t)plan->group_slot0[g] * inter + i,
-                               f32_to_f16_bits(v));
+            act_loc[item >> 1] = f32_to_f16_bits(v);
         }
     };
 
     // down slice: output rows [r0, r1) of every selected expert
-    const int r0 = (int)((int64_t)blockIdx.x * hidden / G);
-    const int r1 = (int)((int64_t)(blockIdx.x + 1) * hidden / G);
+    int r0, r1;
+    slice_of(hidden, r0, r1);
     const int n = r1 - r0;
     const int nd_items = K * n;
     const float inv_n = 1.0f / (float)n;
@@ -841,55 +1071,63 @@ __global__ __launch_bounds__(kNT) void moe_layer_kernel(
         }
     };
 
-    constexpr int RGG = kNT / TPRG, RGD = kNT / TPRD;
-    const int ng = ((ng_items + RGG - 1) / RGG) * chunks_g;
-    const int nd = ((nd_items + RGD - 1) / RGD) * chunks_d;
-    float acc[1] = {0.0f};
+    EngineRing<kGateUpDepth, 1, SG> gu;
+    engine_prime<kGateUpDepth, 1, SG>(gu, ng_items, chunks_g, bpr_g, rowfn_g);
+    engine_run<kGateUpDepth, XK, 1, SG, true>(gu, ng_items, chunks_g, bpr_g, xs, rowfn_g, epi_g);
+    __syncthreads();
 
-    // Both slices' first batches go out together.
-    Stage<1, SG::M> Sg[kDepth];
-    Stage<1, SD::M> Sd[kDownDepth];
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) issue<1, SG>(Sg[d], d, chunks_g, bpr_g, ng_items, rowfn_g);
-#pragma unroll
-    for (int d = 0; d < kDownDepth; ++d) issue<1, SD>(Sd[d], d, chunks_d, bpr_d, nd_items, rowfn_d);
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) consume<XK, 1, SG>(Sg[d], acc, chunks_g, bpr_g, xs, epi_g);
-    for (int base = kDepth; base < ng; base += kDepth) {
-#pragma unroll
-        for (int d = 0; d < kDepth; ++d)
-            issue<1, SG>(Sg[d], base + d, chunks_g, bpr_g, ng_items, rowfn_g);
-#pragma unroll
-        for (int d = 0; d < kDepth; ++d) consume<XK, 1, SG>(Sg[d], acc, chunks_g, bpr_g, xs, epi_g);
+    // The workgroup's activations leave in one batch of coherent (sc1) stores
+    // (a store per gate_up stage would make every later stage's loads wait for
+    // its write-through), then each wave waits for its own stores and one
+    // relaxed add on this workgroup's counter signals them.
+    for (int t = threadIdx.x; t < (p1 - p0); t += kNT) {
+        int g, i;
+        divmod_small(p0 + t, inter, inv_inter, g, i);
+        store_coherent_u16(act + (int64_t)plan->group_slot0[g] * inter + i, act_loc[t]);
     }
-
-    // Signal: this workgroup's activations are stored (every wave waits for its
-    // own stores), then one relaxed add on this workgroup's counter.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    const unsigned epoch1 = s_epoch + 1;
     if (threadIdx.x == 0)
         __hip_atomic_fetch_add(sync.counters + (blockIdx.x % kSyncCounters) * kSyncStride, 1u,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // Lanes 0..15 of wave 0 each watch one counter; counter c receives one add
+    // per launch from every workgroup b with b % 16 == c.  Comparisons are
+    // wrap-safe: the counters only ever grow by whole launches.
+    const int c = threadIdx.x;
+    const unsigned target =
+        c < kSyncCounters ? epoch1 * (unsigned)((G - c + kSyncCounters - 1) / kSyncCounters) : 0u;
+    auto all_arrived = [&]() {
+        bool ok = true;
+        if (c < kSyncCounters)
+            ok = (int)(__hip_atomic_load(sync.counters + c * kSyncStride, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) - target) >= 0;
+        return __all(ok);
+    };
+    // One probe first.  A workgroup that still has to wait loads its first two
+    // down stages meanwhile (they do not depend on the exchange; issued before
+    // the probe they would delay it, as wave 0's loads complete in order).
     if (threadIdx.x < 64) {
-        const int c = threadIdx.x;
-        const unsigned target =
-            c < kSyncCounters ? epoch1 * (unsigned)((G - c + kSyncCounters - 1) / kSyncCounters) : 0u;
-        unsigned spins = 0;
-        while (true) {
-            bool ok = true;
-            if (c < kSyncCounters)   // wrap-safe: counters only ever grow by whole launches
-                ok = (int)(__hip_atomic_load(sync.counters + c * kSyncStride, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT) - target) >= 0;
-            if (__all(ok)) break;
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins > kSpinLimit) {
-                if (c == 0) atomicOr(sync.err, 1u);
-                break;
-            }
-        }
+        const bool done = all_arrived();
+        if (threadIdx.x == 0) plan->pad0 = done ? 1 : 0;
     }
     __syncthreads();
+    const bool waiting = plan->pad0 == 0;
+    EngineRing<kDownDepth, 1, SD> down;
+    if (waiting) {
+        engine_prime<kDownDepth, 1, SD>(down, nd_items, chunks_d, bpr_d, rowfn_d);
+        if (threadIdx.x < 64) {
+            unsigned spins = 0;
+            while (!all_arrived()) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins > kSpinLimit) {
+                    if (threadIdx.x == 0) atomicOr(sync.err, 1u);
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+    }
 
     // Every activation is now visible: stage them with coherent (sc1) buffer
     // loads, issued as one batch per thread.  A buffer load past the buffer's
@@ -921,16 +1159,9 @@ __global__ __launch_bounds__(kNT) void moe_layer_kernel(
     }
     __syncthreads();
 
-#pragma unroll
-    for (int d = 0; d < kDownDepth; ++d) consume<DT_F16, 1, SD>(Sd[d], acc, chunks_d, bpr_d, as, epi_d);
-    for (int base = kDownDepth; base < nd; base += kDownDepth) {
-#pragma unroll
-        for (int d = 0; d < kDownDepth; ++d)
-            issue<1, SD>(Sd[d], base + d, chunks_d, bpr_d, nd_items, rowfn_d);
-#pragma unroll
-        for (int d = 0; d < kDownDepth; ++d)
-            consume<DT_F16, 1, SD>(Sd[d], acc, chunks_d, bpr_d, as, epi_d);
-    }
+    if (!waiting) engine_prime<kDownDepth, 1, SD>(down, nd_items, chunks_d, bpr_d, rowfn_d);
+    engine_run<kDownDepth, DT_F16, 1, SD, false>(down, nd_items, chunks_d, bpr_d, as, rowfn_d,
+                                                 epi_d);
     __syncthreads();
 
     // Combine in router order: dst = 0; dst += out_e * w_e (expert_accumulate).
@@ -1058,9 +1289,9 @@ hipError_t launch_dequant(const Launch &L, const uint8_t *packed, const uint8_t 
 {
     const int64_t words = blocks * 4;
     if (words == 0) return hipSuccess;
-    hipLaunchKernelGGL(dequant_kernel, dim3(div_up(words, 256)), dim3(256), 0, L.stream,
-                       reinterpret_cast<const uint32_t *>(packed), scales, words,
-                       reinterpret_cast<float4 *>(out));
+    GW_LAUNCH(dequant_kernel, dim3(div_up(words, 256)), dim3(256), 0, L,
+              reinterpret_cast<const uint32_t *>(packed), scales, words,
+              reinterpret_cast<float4 *>(out));
     return hipGetLastError();
 }
 
@@ -1090,13 +1321,13 @@ hipError_t launch_gemv(const Launch &L, const uint8_t *packed, const uint8_t *sc
     with_shape(s, [&](auto sh) {
         using SH = decltype(sh);
         if (x_dt == DT_F32)
-            hipLaunchKernelGGL((gemv_kernel<DT_F32, SH>), dim3(grid), dim3(kNT), lds, L.stream,
+            GW_LAUNCH((gemv_kernel<DT_F32, SH>), dim3(grid), dim3(kNT), lds, L,
                                packed, scales, bias, bias_dt, x, y, rows, bpr, s.chunks);
         else if (x_dt == DT_F16)
-            hipLaunchKernelGGL((gemv_kernel<DT_F16, SH>), dim3(grid), dim3(kNT), lds, L.stream,
+            GW_LAUNCH((gemv_kernel<DT_F16, SH>), dim3(grid), dim3(kNT), lds, L,
                                packed, scales, bias, bias_dt, x, y, rows, bpr, s.chunks);
         else
-            hipLaunchKernelGGL((gemv_kernel<DT_BF16, SH>), dim3(grid), dim3(kNT), lds, L.stream,
+            GW_LAUNCH((gemv_kernel<DT_BF16, SH>), dim3(grid), dim3(kNT), lds, L,
                                packed, scales, bias, bias_dt, x, y, rows, bpr, s.chunks);
     });
     return hipGetLastError();
@@ -1125,8 +1356,7 @@ hipError_t launch_gate_up(const Launch &L, Plan *plan, const RouteArgs *route, i
         using SH = decltype(sh);
         auto go = [&](auto xk, auto mt) {
             constexpr int XK = decltype(xk)::value, MT = decltype(mt)::value;
-            hipLaunchKernelGGL((gate_up_kernel<XK, MT, SH>), dim3(grid), dim3(kNT), lds,
-                               L.stream, plan, r, x, hidden, inter, sec, bias_dt, act, act_kind,
+            GW_LAUNCH((gate_up_kernel<XK, MT, SH>), dim3(grid), dim3(kNT), lds, L, plan, r, x, hidden, inter, sec, bias_dt, act, act_kind,
                                limit, alpha, max_tokens, s.chunks);
         };
         using One = std::integral_constant<int, 1>;
@@ -1159,7 +1389,7 @@ static void down_dispatch(const Launch &L, const RowShape &s, int grid, size_t l
 {
     with_shape(s, [&](auto sh) {
         using SH = decltype(sh);
-        hipLaunchKernelGGL((down_kernel<MT, SH>), dim3(grid), dim3(kNT), lds, L.stream, plan,
+        GW_LAUNCH((down_kernel<MT, SH>), dim3(grid), dim3(kNT), lds, L, plan,
                            act, hidden, inter, sec, bias_dt, out, out_bf16, accumulate, smax,
                            nmax, s.chunks, prestage);
     });
@@ -1238,7 +1468,7 @@ hipError_t launch_fused_layer(const Launch &L, int grid, const RouteArgs &route,
         constexpr int XK = decltype(xk)::value;
         using SG = decltype(sg);
         using SD = decltype(sd);
-        hipLaunchKernelGGL((moe_layer_kernel<XK, SG, SD>), dim3(grid), dim3(kNT), lds, L.stream,
+        GW_LAUNCH((moe_layer_kernel<XK, SG, SD>), dim3(grid), dim3(kNT), lds, L,
                            route, x, hidden, inter, sec, bias_dt, act, act_kind, limit, alpha,
                            out, out_bf16, sync, g.chunks, d.chunks, nmax);
     };
@@ -1291,8 +1521,8 @@ hipError_t launch_activation(const Launch &L, int kind, const float *gate_up, ui
                              int64_t width, float limit, float alpha)
 {
     if (width == 0) return hipSuccess;
-    hipLaunchKernelGGL(activation_kernel, dim3(div_up(width, 256)), dim3(256), 0, L.stream,
-                       kind, gate_up, out, width, limit, alpha);
+    GW_LAUNCH(activation_kernel, dim3(div_up(width, 256)), dim3(256), 0, L, kind, gate_up, out,
+              width, limit, alpha);
     return hipGetLastError();
 }
 
@@ -1300,8 +1530,7 @@ hipError_t launch_accumulate(const Launch &L, const float *src, float *dst, floa
                              int64_t width)
 {
     if (width == 0) return hipSuccess;
-    hipLaunchKernelGGL(accumulate_kernel, dim3(div_up(width, 256)), dim3(256), 0, L.stream,
-                       src, dst, w, width);
+    GW_LAUNCH(accumulate_kernel, dim3(div_up(width, 256)), dim3(256), 0, L, src, dst, w, width);
     return hipGetLastError();
 }
 
@@ -1311,8 +1540,8 @@ hipError_t launch_router(const Launch &L, const void *W, int w_dt, const void *b
 {
     const int waves = experts * tokens;
     if (waves == 0) return hipSuccess;
-    hipLaunchKernelGGL(router_kernel, dim3(div_up(waves, 4)), dim3(256), 0, L.stream, W, w_dt,
-                       b, b_dt, x, x_dt, logits, experts, hidden, tokens);
+    GW_LAUNCH(router_kernel, dim3(div_up(waves, 4)), dim3(256), 0, L, W, w_dt, b, b_dt, x, x_dt,
+              logits, experts, hidden, tokens);
     return hipGetLastError();
 }
 
@@ -1321,7 +1550,7 @@ hipError_t launch_route(const Launch &L, const RouteArgs &route, Plan *plan)
     if (route.experts > kMaxExperts || route.top_k > kMaxTopK || route.tokens > kMaxTokens ||
         route.top_k > route.experts)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(route_kernel, dim3(1), dim3(64), 0, L.stream, route, plan);
+    GW_LAUNCH(route_kernel, dim3(1), dim3(64), 0, L, route, plan);
     return hipGetLastError();
 }
 
@@ -1331,8 +1560,8 @@ hipError_t launch_fill_u8(const Launch &L, void *dst, size_t count, int lo, int 
     if (count == 0) return hipSuccess;
     const int64_t threads = ((int64_t)count + 7) / 8;
     const uint32_t range = (uint32_t)(hi - lo + 1);
-    hipLaunchKernelGGL(fill_u8_kernel, dim3(div_up(threads, 256)), dim3(256), 0, L.stream,
-                       static_cast<uint8_t *>(dst), (int64_t)count, (uint32_t)lo, range, seed);
+    GW_LAUNCH(fill_u8_kernel, dim3(div_up(threads, 256)), dim3(256), 0, L,
+              static_cast<uint8_t *>(dst), (int64_t)count, (uint32_t)lo, range, seed);
     return hipGetLastError();
 }
 
@@ -1340,8 +1569,8 @@ hipError_t launch_fill_normal(const Launch &L, void *dst, int dt, size_t count, 
                               float stddev, uint64_t seed)
 {
     if (count == 0) return hipSuccess;
-    hipLaunchKernelGGL(fill_normal_kernel, dim3(div_up((int64_t)count, 256)), dim3(256), 0,
-                       L.stream, dst, dt, (int64_t)count, mean, stddev, seed);
+    GW_LAUNCH(fill_normal_kernel, dim3(div_up((int64_t)count, 256)), dim3(256), 0, L, dst, dt,
+              (int64_t)count, mean, stddev, seed);
     return hipGetLastError();
 }
 

@@ -13,6 +13,8 @@ struct Launch {
     int cus;        // compute units of the device
     int grid_a;     // workgroups of the gate_up kernel (0 = default)
     int grid_b;     // workgroups of the down kernel (0 = default)
+    hipEvent_t ev_start = nullptr;   // set: recorded by the kernel's dispatch (profiling)
+    hipEvent_t ev_stop = nullptr;
 };
 
 // Device routing from logits (Router.select + the demand map), done by the
@@ -28,11 +30,11 @@ struct RouteArgs {
 
 // State of the fused layer kernel's in-kernel exchange (owned by a runner).
 struct SyncArgs {
-    unsigned *counters;   // 16 counters, 256 bytes apart
+    unsigned *counters;   // 16 counters, 4352 bytes apart
     unsigned *epochs;     // per workgroup: launches it has completed
     unsigned *err;        // nonzero once a bounded wait gave up
 };
-constexpr int kSyncWords = 16 * 64;
+constexpr int kSyncWords = 16 * 1088;
 
 // Lanes per row and blocks per lane chosen for a row of `bpr` MXFP4 blocks.
 struct RowShape { int tpr; int m; int chunks; };

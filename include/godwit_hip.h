@@ -267,15 +267,15 @@ typedef struct gw_moe_layer_args {
 
 int gw_moe_layer_forward(gw_expert_runner *runner, const gw_moe_layer_args *args);
 
-/* For one token (the decode step of a single sequence) the layer above runs
- * as ONE kernel whose workgroups exchange the activations through device
- * memory; its waits are bounded, and a wait that gives up is counted here
- * instead of hanging the device.  No counterpart in the reference (there the
- * command buffer's encoder boundaries order the stages).  Blocks until the
- * runner's stream is idle; *count is the number of failed exchanges since
- * the runner was created (0 when every result is valid).  Setting
- * GODWIT_FUSED_LAYER=0 in the environment before creating the runner keeps
- * the two-kernel form for every token count. */
+/* For one token (the decode step of a single sequence) the layer above can
+ * run as ONE kernel whose workgroups exchange the activations through device
+ * memory (enabled by GODWIT_FUSED_LAYER=1 in the environment when the runner
+ * is created; the default is the two-kernel form, which measures faster on
+ * MI355X today).  Its waits are bounded, and a wait that gives up is counted
+ * here instead of hanging the device.  No counterpart in the reference (there
+ * the command buffer's encoder boundaries order the stages).  Blocks until the
+ * runner's stream is idle; *count is the number of failed exchanges since the
+ * runner was created (0 when every result is valid). */
 int gw_expert_runner_sync_errors(gw_expert_runner *runner, uint32_t *count);
 
 /* ---- graphs (replace per-call command buffers with one replayable graph) */

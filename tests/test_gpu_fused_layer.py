@@ -57,6 +57,7 @@ def _kernel_counts(ctx, fn):
 def test_fused_layer_equals_two_kernel_form(ctx, monkeypatch, shape, n_experts, top_k, x_dtype):
     H, F = shape["hidden"], shape["inter"]
     layout, experts, buf = _make_layer(ctx, shape, n_experts, 1200 + n_experts)
+    monkeypatch.setenv("GODWIT_FUSED_LAYER", "1")
     fused = gw.ExpertRunner(ctx, H, F, shape["act"])
     monkeypatch.setenv("GODWIT_FUSED_LAYER", "0")
     split = gw.ExpertRunner(ctx, H, F, shape["act"])
@@ -89,7 +90,7 @@ def test_fused_layer_equals_two_kernel_form(ctx, monkeypatch, shape, n_experts, 
     split.close()
 
 
-def test_fused_layer_graph_chain_replays(ctx):
+def test_fused_layer_graph_chain_replays(ctx, monkeypatch):
     """A captured chain of 12 one-token layers (each layer's bf16 output is the next
     one's input), replayed 6 times: every replay equals the eager chain, the first
     layer matches the oracle, and no exchange ever gave up.  The replays advance the
@@ -97,6 +98,7 @@ def test_fused_layer_graph_chain_replays(ctx):
     shape = GPTOSS
     H, F, n_experts, layers = shape["hidden"], shape["inter"], 16, 12
     layout, experts, buf = _make_layer(ctx, shape, n_experts, 1400)
+    monkeypatch.setenv("GODWIT_FUSED_LAYER", "1")
     runner = gw.ExpertRunner(ctx, H, F, shape["act"])
     r = rng(1401)
     xbits, xw = normal_bf16(r, H)
