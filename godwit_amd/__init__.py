@@ -354,6 +354,16 @@ class ExpertRunner:
                       routing_ids: int = 0, routing_weights: int = 0) -> None:
         """MoE block of TransformerLayer.forward (TransformerLayer.swift:140-238), on the
         device; all pointer arguments are device addresses.  Enqueue only."""
+        a = self._layer_args(experts_base, expert_stride, expert_count, top_k, x, x_dtype,
+                             tokens, out, logits, router_weight, router_weight_dtype,
+                             router_bias, router_bias_dtype, out_bf16, routing_ids,
+                             routing_weights)
+        check(lib.gw_moe_layer_forward(self.handle, ctypes.byref(a)))
+
+    @staticmethod
+    def _layer_args(experts_base, expert_stride, expert_count, top_k, x, x_dtype, tokens, out,
+                    logits, router_weight, router_weight_dtype, router_bias, router_bias_dtype,
+                    out_bf16, routing_ids, routing_weights):
         a = MoeLayerArgsC()
         a.experts_base = experts_base
         a.expert_stride = expert_stride
@@ -371,7 +381,24 @@ class ExpertRunner:
         a.out_bf16 = out_bf16 or None
         a.routing_ids = routing_ids or None
         a.routing_weights = routing_weights or None
-        check(lib.gw_moe_layer_forward(self.handle, ctypes.byref(a)))
+        return a
+
+    def prefill_forward(self, experts_base: int, expert_stride: int, expert_count: int,
+                        top_k: int, x: int, x_dtype: int, tokens: int, out: int,
+                        logits: int = 0, router_weight: int = 0, router_weight_dtype: int = BF16,
+                        router_bias: int = 0, router_bias_dtype: int = BF16, out_bf16: int = 0,
+                        routing_ids: int = 0, routing_weights: int = 0) -> None:
+        """Batched prefill of the MoE block (TransformerLayer.swift:140-238 with T > 1) as
+        grouped GEMMs on the matrix cores; same arguments as layer_forward.  Enqueue only."""
+        a = self._layer_args(experts_base, expert_stride, expert_count, top_k, x, x_dtype,
+                             tokens, out, logits, router_weight, router_weight_dtype,
+                             router_bias, router_bias_dtype, out_bf16, routing_ids,
+                             routing_weights)
+        check(lib.gw_moe_prefill_forward(self.handle, ctypes.byref(a)))
+
+    def reserve_prefill(self, max_tokens: int, top_k: int, expert_count: int) -> None:
+        """Sizes the prefill scratch up front (required before capturing a graph)."""
+        check(lib.gw_expert_runner_reserve_prefill(self.handle, max_tokens, top_k, expert_count))
 
     def sync_errors(self) -> int:
         """Failed in-kernel exchanges of the one-token layer kernel since creation

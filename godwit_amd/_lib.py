@@ -84,11 +84,13 @@ SIGNATURES = {
     "gw_expert_runner_set_bias_dtype": (_I, [_P, _I]),
     "gw_expert_runner_section_offsets": (_I, [_P, _I64 * SECTION_COUNT]),
     "gw_expert_runner_sync_errors": (_I, [_P, ctypes.POINTER(ctypes.c_uint32)]),
+    "gw_expert_runner_reserve_prefill": (_I, [_P, _I32, _I32, _I32]),
     "gw_expert_apply": (_I, [_P, _P, _I, ctypes.POINTER(ExpertWeightsC), _P]),
     "gw_expert_apply_batch": (_I, [_P, _P, _I, _P, _P, _I32, _P]),
     "gw_expert_apply_assignments": (_I, [_P, _P, _I, _P, _I32, _P]),
     "gw_expert_apply_assignments_async": (_I, [_P, _P, _I, _P, _I32, _P]),
     "gw_moe_layer_forward": (_I, [_P, ctypes.POINTER(MoeLayerArgsC)]),
+    "gw_moe_prefill_forward": (_I, [_P, ctypes.POINTER(MoeLayerArgsC)]),
     "gw_graph_begin_capture": (_I, [_P]),
     "gw_graph_end_capture": (_I, [_P, ctypes.POINTER(_P)]),
     "gw_graph_launch": (_I, [_P]),

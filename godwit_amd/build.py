@@ -22,7 +22,8 @@ LIB = os.path.join(HERE, "libgodwit_hip.so")
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["gw_kernels.hip", "gw_api.hip"]
+SOURCES = ["gw_kernels.hip", "gw_prefill.hip", "gw_api.hip"]
+OBJDIR = os.path.join(HERE, "_build")
 
 FLAGS = [
     f"--offload-arch={ARCH}",
@@ -38,16 +39,33 @@ FLAGS = [
 
 
 def build(verbose: bool = True) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-I", os.path.join(HERE, "..", "include"), "-o", tmp, *srcs]
+    """Compiles the sources in parallel (one hipcc per file), then links."""
+    os.makedirs(OBJDIR, exist_ok=True)
+    inc = ["-I", os.path.join(HERE, "..", "include")]
     t0 = time.time()
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError(f"hipcc failed ({proc.returncode})")
-    noise = [ln for ln in (proc.stdout + proc.stderr).splitlines()
-             if ln.strip() and "packed-fp32-ops" not in ln]
+    procs = []
+    for src in SOURCES:
+        obj = os.path.join(OBJDIR, src.replace(".hip", ".o"))
+        cmd = [HIPCC, *[f for f in FLAGS if f != "-shared"], *inc, "-c", "-o", obj,
+               os.path.join(CSRC, src)]
+        procs.append((src, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                                 stderr=subprocess.STDOUT, text=True)))
+    objs, failed, noise = [], False, []
+    for src, obj, proc in procs:
+        out, _ = proc.communicate()
+        noise += [ln for ln in out.splitlines() if ln.strip() and "packed-fp32-ops" not in ln]
+        if proc.returncode != 0:
+            failed = True
+            sys.stderr.write(f"{src}:\n{out}")
+        objs.append(obj)
+    if failed:
+        raise RuntimeError("hipcc failed")
+    tmp = LIB + ".tmp"
+    link = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs],
+                          capture_output=True, text=True)
+    if link.returncode != 0:
+        sys.stderr.write(link.stdout + link.stderr)
+        raise RuntimeError(f"link failed ({link.returncode})")
     if noise and verbose:
         sys.stderr.write("\n".join(noise) + "\n")
     os.replace(tmp, LIB)

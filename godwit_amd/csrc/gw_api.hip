@@ -554,6 +554,9 @@ struct gw_expert_runner {
     float *logits = nullptr;         // [kMaxTokens, kMaxExperts]
     Plan *staging = nullptr;         // pinned host mirror of `plans`
     unsigned *sync_buf = nullptr;    // fused layer exchange: counters | epochs | error word
+    // prefill scratch, sized for pf_tokens tokens x pf_topk ranks x pf_experts
+    int pf_tokens = 0, pf_topk = 0, pf_experts = 0;
+    void *pf_buf = nullptr;
     bool fused_enabled = false;      // GODWIT_FUSED_LAYER=1 at creation turns it on
     int ring_next = 0;
     int ring_used = 0;
@@ -580,6 +583,7 @@ extern "C" int gw_expert_runner_destroy(gw_expert_runner *r)
     (void)hipFree(r->logits);
     (void)hipHostFree(r->staging);
     (void)hipFree(r->sync_buf);
+    (void)hipFree(r->pf_buf);
     delete r;
     return GW_OK;
 }
@@ -927,8 +931,8 @@ extern "C" int gw_expert_apply_assignments(gw_expert_runner *r, const void *inpu
 extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args *a)
 {
     GW_CHECK(r && a, GW_ERR_ARG, "null argument");
-    GW_CHECK(a->tokens >= 1 && a->tokens <= gw::kMaxTokens, GW_ERR_SHAPE,
-             "decode layer takes 1..%d tokens (got %d)", gw::kMaxTokens, a->tokens);
+    if (a->tokens > gw::kMaxTokens) return gw_moe_prefill_forward(r, a);
+    GW_CHECK(a->tokens >= 1, GW_ERR_SHAPE, "tokens must be positive (got %d)", a->tokens);
     GW_CHECK(a->expert_count >= 1 && a->expert_count <= kMaxExperts, GW_ERR_SHAPE,
              "expert_count %lld out of range", (long long)a->expert_count);
     GW_CHECK(a->top_k >= 1 && a->top_k <= gw::kMaxTopK && a->top_k <= a->expert_count,
@@ -996,6 +1000,171 @@ extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args
                                (int)r->hidden, (int)r->inter, sec, r->bias_dt, a->out,
                                a->out_bf16, 0));
     }
+    return GW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// prefill: many tokens through one layer on the matrix cores
+// ---------------------------------------------------------------------------
+
+namespace {
+struct PrefillScratch {
+    float *logits;
+    int32_t *ids;
+    float *weights;
+    int32_t *offsets, *order, *tiles, *ntiles;
+    uint16_t *act;
+    float *y;
+};
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Carves the runner's prefill buffer; returns the bytes needed for (T, K, E).
+size_t prefill_layout(const gw_expert_runner *r, int T, int K, int E, char *base,
+                      PrefillScratch *ps)
+{
+    const size_t N = (size_t)T * K;
+    const size_t tiles = (size_t)gw::prefill_max_tiles(T, K, E);
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        char *p = base ? base + o : nullptr;
+        o += align256(bytes);
+        return p;
+    };
+    PrefillScratch s;
+    s.logits = reinterpret_cast<float *>(take(sizeof(float) * (size_t)T * E));
+    s.ids = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * N));
+    s.weights = reinterpret_cast<float *>(take(sizeof(float) * N));
+    s.offsets = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * (E + 1)));
+    s.order = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * N));
+    s.tiles = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * tiles));
+    s.ntiles = reinterpret_cast<int32_t *>(take(sizeof(int32_t)));
+    s.act = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * N * r->inter));
+    s.y = reinterpret_cast<float *>(take(sizeof(float) * N * r->hidden));
+    if (ps) *ps = s;
+    return o;
+}
+}  // namespace
+
+extern "C" int gw_expert_runner_reserve_prefill(gw_expert_runner *r, int32_t max_tokens,
+                                                int32_t top_k, int32_t expert_count)
+{
+    GW_CHECK(r, GW_ERR_ARG, "runner is null");
+    GW_CHECK(max_tokens >= 1 && top_k >= 1 && top_k <= gw::kMaxTopK && expert_count >= top_k &&
+                 expert_count <= 256,
+             GW_ERR_SHAPE, "prefill shape out of range (tokens %d, top_k %d, experts %d)",
+             max_tokens, top_k, expert_count);
+    if (r->pf_buf && max_tokens <= r->pf_tokens && top_k <= r->pf_topk &&
+        expert_count <= r->pf_experts)
+        return GW_OK;
+    GW_CHECK(!r->ctx->capturing, GW_ERR_ARG,
+             "prefill scratch must be reserved before graph capture");
+    const int T = max_tokens > r->pf_tokens ? max_tokens : r->pf_tokens;
+    const int K = top_k > r->pf_topk ? top_k : r->pf_topk;
+    const int E = expert_count > r->pf_experts ? expert_count : r->pf_experts;
+    const size_t bytes = prefill_layout(r, T, K, E, nullptr, nullptr);
+    GW_HIP(hipStreamSynchronize(r->ctx->stream));
+    (void)hipFree(r->pf_buf);
+    r->pf_buf = nullptr;
+    r->pf_tokens = r->pf_topk = r->pf_experts = 0;
+    GW_HIP(hipMalloc(&r->pf_buf, bytes));
+    r->pf_tokens = T;
+    r->pf_topk = K;
+    r->pf_experts = E;
+    return GW_OK;
+}
+
+extern "C" int gw_moe_prefill_forward(gw_expert_runner *r, const gw_moe_layer_args *a)
+{
+    GW_CHECK(r && a, GW_ERR_ARG, "null argument");
+    GW_CHECK(a->tokens >= 1, GW_ERR_SHAPE, "tokens must be positive (got %d)", a->tokens);
+    GW_CHECK(a->expert_count >= 1 && a->expert_count <= 256, GW_ERR_SHAPE,
+             "prefill takes 1..256 experts (got %lld)", (long long)a->expert_count);
+    GW_CHECK(a->top_k >= 1 && a->top_k <= gw::kMaxTopK && a->top_k <= a->expert_count,
+             GW_ERR_SHAPE, "top_k %lld out of range", (long long)a->top_k);
+    GW_CHECK(a->experts_base && a->x && a->out, GW_ERR_ARG, "null pointer");
+    GW_CHECK(aligned16(a->experts_base) && a->expert_stride > 0 && a->expert_stride % 16 == 0,
+             GW_ERR_ARG, "experts_base/stride must be 16-byte aligned");
+    GW_CHECK(dtype_ok(a->x_dtype), GW_ERR_ARG, "bad x dtype");
+    GW_CHECK(aligned16(a->x), GW_ERR_ARG, "x must be 16-byte aligned for prefill");
+    GW_CHECK(a->logits || a->router_weight, GW_ERR_ARG, "need logits or router weights");
+    GW_CHECK(r->hidden % 32 == 0 && r->inter % 32 == 0, GW_ERR_SHAPE, "bad runner shape");
+    const int T = a->tokens, K = (int)a->top_k, E = (int)a->expert_count;
+    int rc = gw_expert_runner_reserve_prefill(r, T, K, E);
+    if (rc) return rc;
+    PrefillScratch ps;
+    prefill_layout(r, r->pf_tokens, r->pf_topk, r->pf_experts, static_cast<char *>(r->pf_buf),
+                   &ps);
+    gw_context *ctx = r->ctx;
+    const gw::Launch L = launch_of(ctx);
+    const float *logits = a->logits;
+    if (!logits) {
+        GW_CHECK(dtype_ok(a->router_weight_dtype), GW_ERR_ARG, "bad router dtype");
+        ProfScope p(ctx, "router");
+        GW_HIP(gw::launch_router(p.launch(L), a->router_weight, a->router_weight_dtype,
+                                 a->router_bias, a->router_bias ? (int)a->router_bias_dtype : -1,
+                                 a->x, a->x_dtype, ps.logits, E, (int)r->hidden, T));
+        logits = ps.logits;
+    }
+    {
+        ProfScope p(ctx, "prefill_route");
+        GW_HIP(gw::launch_prefill_route(p.launch(L), logits, T, E, K, ps.ids, ps.weights));
+    }
+    const int max_tiles = gw::prefill_max_tiles(T, K, E);
+    {
+        ProfScope p(ctx, "prefill_group");
+        GW_HIP(gw::launch_prefill_group(p.launch(L), ps.ids, T * K, E, ps.offsets, ps.order,
+                                        ps.tiles, ps.ntiles, max_tiles));
+    }
+    const gw::Sections sec = sections_of(r->offsets);
+    gw::PrefillGemm g;
+    g.tiles = ps.tiles;
+    g.ntiles = ps.ntiles;
+    g.offsets = ps.offsets;
+    g.order = ps.order;
+    g.experts_base = a->experts_base;
+    g.stride = a->expert_stride;
+    g.bias_dt = r->bias_dt;
+    g.act_kind = r->act;
+    g.limit = r->limit;
+    g.alpha = r->alpha;
+    {
+        g.in = a->x;
+        g.in_row_div = K;
+        g.blocks_off = sec.gu_blocks;
+        g.scales_off = sec.gu_scales;
+        g.bias_off = sec.gu_bias;
+        g.kdim = (int)r->hidden;
+        g.fdim = (int)(2 * r->inter);
+        g.act_out = ps.act;
+        g.y_out = nullptr;
+        ProfScope p(ctx, "prefill_gate_up");
+        GW_HIP(gw::launch_prefill_gemm(p.launch(L), true, a->x_dtype, g, max_tiles));
+    }
+    {
+        g.in = ps.act;
+        g.in_row_div = 1;
+        g.blocks_off = sec.dn_blocks;
+        g.scales_off = sec.dn_scales;
+        g.bias_off = sec.dn_bias;
+        g.kdim = (int)r->inter;
+        g.fdim = (int)r->hidden;
+        g.act_out = nullptr;
+        g.y_out = ps.y;
+        ProfScope p(ctx, "prefill_down");
+        GW_HIP(gw::launch_prefill_gemm(p.launch(L), false, GW_F16, g, max_tiles));
+    }
+    {
+        ProfScope p(ctx, "prefill_combine");
+        GW_HIP(gw::launch_prefill_combine(p.launch(L), ps.y, ps.weights, T, K, (int)r->hidden,
+                                          a->out, a->out_bf16));
+    }
+    if (a->routing_ids)
+        GW_HIP(hipMemcpyAsync(a->routing_ids, ps.ids, sizeof(int32_t) * T * K,
+                              hipMemcpyDeviceToDevice, ctx->stream));
+    if (a->routing_weights)
+        GW_HIP(hipMemcpyAsync(a->routing_weights, ps.weights, sizeof(float) * T * K,
+                              hipMemcpyDeviceToDevice, ctx->stream));
     return GW_OK;
 }
 

@@ -69,6 +69,35 @@ hipError_t launch_fused_layer(const Launch &L, int grid, const RouteArgs &route,
                               int x_dt, int hidden, int inter, const Sections &sec, int bias_dt,
                               uint16_t *act, int act_kind, float limit, float alpha, float *out,
                               uint16_t *out_bf16, const SyncArgs &sync);
+// ---- prefill (batched tokens) on the matrix cores
+
+// One grouped GEMM launch (gate_up or down) over the work items of a grouping.
+struct PrefillGemm {
+    const int32_t *tiles, *ntiles, *offsets, *order;
+    const void *in;               // [rows, kdim] activations
+    int in_row_div;               // entry -> input row divisor (top_k for x, 1 for act)
+    const uint8_t *experts_base;
+    int64_t stride;
+    int64_t blocks_off, scales_off, bias_off;
+    int bias_dt;                  // -1: none
+    int kdim, fdim;
+    uint16_t *act_out;            // gate_up: [entries, fdim/2] fp16
+    float *y_out;                 // down: [entries, fdim] fp32
+    int act_kind;
+    float limit, alpha;
+};
+int prefill_max_tiles(int T, int K, int E);
+int prefill_gemm_lds_bytes(int in_dt);
+hipError_t launch_prefill_route(const Launch &L, const float *logits, int T, int E, int K,
+                                int32_t *ids, float *weights);
+hipError_t launch_prefill_group(const Launch &L, const int32_t *ids, int N, int E,
+                                int32_t *offsets, int32_t *order, int32_t *tiles,
+                                int32_t *ntiles, int max_tiles);
+hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int in_dt, const PrefillGemm &g,
+                               int max_tiles);
+hipError_t launch_prefill_combine(const Launch &L, const float *y, const float *w, int T, int K,
+                                  int H, float *out, uint16_t *out_bf16);
+
 hipError_t launch_fill_u8(const Launch &L, void *dst, size_t count, int lo, int hi,
                           uint64_t seed);
 hipError_t launch_fill_normal(const Launch &L, void *dst, int dt, size_t count, float mean,

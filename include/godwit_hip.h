@@ -238,7 +238,7 @@ int gw_expert_apply_assignments_async(gw_expert_runner *runner, const void *inpu
 
 /* ---- MoE block of TransformerLayer.forward (Runtime/TransformerLayer.swift:140-238) */
 
-/* One layer's MoE block for `tokens` (1..8) decode tokens, entirely on the
+/* One layer's MoE block for `tokens` decode tokens, entirely on the
  * device: router (bf16_gemv_bias, or given logits) -> top-k + softmax
  * (Router.select) -> expert-major grouping (the demand map, :175-181) ->
  * fused gate_up + activation -> fused down + weighted combine.
@@ -266,6 +266,21 @@ typedef struct gw_moe_layer_args {
 } gw_moe_layer_args;
 
 int gw_moe_layer_forward(gw_expert_runner *runner, const gw_moe_layer_args *args);
+
+/* Batched prefill of the same MoE block for any number of tokens
+ * (TransformerLayer.forward with T > 1, :140-238), as grouped GEMMs on the
+ * matrix cores: route every token, sort the T*k (token, rank) entries by
+ * expert (the demand map, :175-181), run each expert's gate_up and down over
+ * its whole token group (weights widened exactly to bf16 with the block
+ * scale folded in; activations as exact sums of bf16 parts; fp32
+ * accumulation), then combine each token's experts in router order.  Same
+ * arguments as gw_moe_layer_forward; up to 256 experts.  Scratch grows on
+ * demand (or up front with gw_expert_runner_reserve_prefill, which a caller
+ * about to capture a graph must use).  gw_moe_layer_forward itself sends
+ * batches of more than 8 tokens here.  Enqueue only. */
+int gw_expert_runner_reserve_prefill(gw_expert_runner *runner, int32_t max_tokens, int32_t top_k,
+                                     int32_t expert_count);
+int gw_moe_prefill_forward(gw_expert_runner *runner, const gw_moe_layer_args *args);
 
 /* For one token (the decode step of a single sequence) the layer above can
  * run as ONE kernel whose workgroups exchange the activations through device

@@ -1,0 +1,178 @@
+"""Batched prefill (grouped GEMMs on the matrix cores) against the CPU oracle and
+against the decode path.
+
+The oracle is the reference's layer: route each token (Router.select), run
+every selected expert (referenceMXFP4 GEMVs + activation with fp16 rounding)
+and combine in router order (layer_reference.py).  Tolerance: the reference's
+expert metric max|d|/mean|ref| per token (GodwitCLI/main.swift:518-532), see
+_close_batch; routing ids exact, weights to 1e-6.  Shapes cover one, two and three bf16
+activation planes (bf16, fp16, fp32 x), partial feature tiles, K dimensions
+that are not a multiple of the 256-element staging chunk, experts with no
+tokens and experts with several 32-token tiles.
+"""
+import numpy as np
+import pytest
+
+import godwit_amd as gw
+import oracle
+from helpers import expert_metric, normal_bf16, rng
+from test_gpu_expert import GPTOSS, QWEN3, SMALL, _make_layer
+
+pytestmark = pytest.mark.gpu
+
+
+def _close_batch(got, ref):
+    """Per-token expert metric.  A gate_up sum whose last fp32 bits differ from the
+    oracle's can round its fp16 activation one ulp the other way (the reference
+    rounds the activation to fp16, expert.metal:101), which moves a token's down
+    output by up to ~1e-3 of its mean magnitude; with many (token, expert) pairs a
+    few such flips are expected.  So: every token within the reference's own
+    check-expert tolerance (5e-3, GodwitCLI/main.swift:518-532) and the median
+    token within 1e-4 (the accumulation itself is exact to fp32 rounding)."""
+    m = np.array([expert_metric(got[t], ref[t]) for t in range(len(ref))])
+    assert m.max() < 5e-3, (m.max(), np.argmax(m))
+    assert np.median(m) < 1e-4, np.median(m)
+
+
+def _zipf_logits(r, T, E, K, s=1.1):
+    """Logits whose top-k per token is a Zipf(s)-popular draw of K distinct experts
+    (BASELINE config 4's assignment), ranked by decreasing logit."""
+    p = 1.0 / np.arange(1, E + 1) ** s
+    p /= p.sum()
+    logits = (r.standard_normal((T, E)) - 10.0).astype(np.float32)
+    for t in range(T):
+        chosen = r.choice(E, size=K, replace=False, p=p)
+        logits[t, chosen] = (5.0 - np.arange(K) + r.uniform(0, 0.5, K)).astype(np.float32)
+    return logits
+
+
+def _x(ctx, r, T, H, x_dtype):
+    xbits, xw = normal_bf16(r, T * H)
+    if x_dtype == gw.BF16:
+        return ctx.buffer(xbits), xw
+    if x_dtype == gw.F16:
+        x = xw.astype(np.float16)
+        return ctx.buffer(x), x.astype(np.float32)
+    return ctx.buffer(xw.astype(np.float32)), xw.astype(np.float32)
+
+
+def _run(ctx, runner, layout, buf, E, K, xb, x_dtype, lb, T, H, fn="prefill_forward"):
+    out, out16 = ctx.empty(T * H * 4), ctx.empty(T * H * 2)
+    ids_b, w_b = ctx.empty(T * K * 4), ctx.empty(T * K * 4)
+    getattr(runner, fn)(buf.ptr, layout.stride, E, K, xb.ptr, x_dtype, T, out.ptr,
+                        logits=lb.ptr, out_bf16=out16.ptr, routing_ids=ids_b.ptr,
+                        routing_weights=w_b.ptr)
+    ctx.synchronize()
+    res = (out.download(np.float32, T * H).reshape(T, H), out16.download(np.uint16, T * H),
+           ids_b.download(np.int32, T * K).reshape(T, K),
+           w_b.download(np.float32, T * K).reshape(T, K))
+    for b in (out, out16, ids_b, w_b):
+        b.free()
+    return res
+
+
+@pytest.mark.parametrize("shape,E,K,T,x_dtype,seed", [
+    (SMALL, 16, 4, 72, gw.BF16, 1),      # experts with 2-3 tiles, partial feature tiles
+    (QWEN3, 32, 8, 24, gw.F16, 2),       # two activation planes, no biases, SiLU-GLU
+    (GPTOSS, 12, 4, 20, gw.F32, 3),      # three planes, 2880-wide K (11.25 chunks)
+], ids=["small-bf16", "qwen3-f16", "gptoss-f32"])
+def test_prefill_matches_oracle(ctx, shape, E, K, T, x_dtype, seed):
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _make_layer(ctx, shape, E, 2000 + seed)
+    runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+    r = rng(2100 + seed)
+    xb, xw = _x(ctx, r, T, H, x_dtype)
+    logits = _zipf_logits(r, T, E, K)
+    lb = ctx.buffer(logits)
+    got, got16, ids, wts = _run(ctx, runner, layout, buf, E, K, xb, x_dtype, lb, T, H)
+    ref, rids, rw = oracle.moe_layer([e.oracle_expert() for e in experts], K, logits, xw, H, F,
+                                     shape["oact"])
+    assert np.array_equal(ids, rids)
+    assert np.allclose(wts, rw, rtol=1e-6, atol=1e-7)
+    _close_batch(got, ref)
+    assert np.array_equal(got16, oracle.f32_to_bf16_bits(got.ravel()))
+    for b in (xb, lb, buf):
+        b.free()
+    runner.close()
+
+
+def test_prefill_agrees_with_decode_path(ctx):
+    """The same 8 tokens through the grouped-GEMM prefill and the decode kernels."""
+    shape, E, K, T = GPTOSS, 8, 4, 8
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _make_layer(ctx, shape, E, 2200)
+    runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+    r = rng(2201)
+    xb, xw = _x(ctx, r, T, H, gw.BF16)
+    logits = r.standard_normal((T, E)).astype(np.float32)
+    lb = ctx.buffer(logits)
+    pre = _run(ctx, runner, layout, buf, E, K, xb, gw.BF16, lb, T, H, "prefill_forward")
+    dec = _run(ctx, runner, layout, buf, E, K, xb, gw.BF16, lb, T, H, "layer_forward")
+    assert np.array_equal(pre[2], dec[2])
+    assert np.array_equal(pre[3], dec[3])
+    _close_batch(pre[0], dec[0])
+    for b in (xb, lb, buf):
+        b.free()
+    runner.close()
+
+
+def test_layer_forward_sends_large_batches_to_prefill(ctx):
+    """TransformerLayer.forward's batch entry: more than 8 tokens run the grouped GEMMs."""
+    shape, E, K, T = SMALL, 8, 2, 40
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _make_layer(ctx, shape, E, 2300)
+    runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+    r = rng(2301)
+    xb, xw = _x(ctx, r, T, H, gw.BF16)
+    logits = r.standard_normal((T, E)).astype(np.float32)
+    lb = ctx.buffer(logits)
+    ctx.set_profiling(True)
+    ctx.profile_reset()
+    got = _run(ctx, runner, layout, buf, E, K, xb, gw.BF16, lb, T, H, "layer_forward")
+    n_gemm = ctx.profile("prefill_gate_up")[1] + ctx.profile("prefill_down")[1]
+    ctx.set_profiling(False)
+    assert n_gemm == 2
+    ref, _, _ = oracle.moe_layer([e.oracle_expert() for e in experts], K, logits, xw, H, F,
+                                 shape["oact"])
+    _close_batch(got[0], ref)
+    for b in (xb, lb, buf):
+        b.free()
+    runner.close()
+
+
+def test_prefill_router_and_graph_replay(ctx):
+    """Device router logits feeding prefill, captured once (scratch reserved first) and
+    replayed: every replay equals the eager result."""
+    shape, E, K, T = SMALL, 16, 4, 48
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _make_layer(ctx, shape, E, 2400)
+    runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+    runner.reserve_prefill(T, K, E)
+    r = rng(2401)
+    xb, xw = _x(ctx, r, T, H, gw.BF16)
+    W = (r.standard_normal(E * H) * 0.02).astype(np.float32)
+    wb = ctx.buffer(W)
+    out = ctx.empty(T * H * 4)
+
+    def body():
+        runner.prefill_forward(buf.ptr, layout.stride, E, K, xb.ptr, gw.BF16, T, out.ptr,
+                               router_weight=wb.ptr, router_weight_dtype=gw.F32)
+
+    body()
+    ctx.synchronize()
+    eager = out.download(np.float32, T * H)
+    logits = np.stack([oracle.router_logits(W, None, xw[t * H:(t + 1) * H], E, H)
+                       for t in range(T)])
+    ref, _, _ = oracle.moe_layer([e.oracle_expert() for e in experts], K, logits, xw, H, F,
+                                 shape["oact"])
+    _close_batch(eager.reshape(T, H), ref)
+    graph = gw.Graph.capture(ctx, body)
+    for _ in range(3):
+        out.zero()
+        graph.launch()
+        ctx.synchronize()
+        assert np.array_equal(out.download(np.float32, T * H), eager)
+    graph.destroy()
+    for b in (xb, wb, out, buf):
+        b.free()
+    runner.close()
