@@ -41,7 +41,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-typedef const __attribute__((address_space(1))) u32x2v g_u32x2v;
+typedef const __attribute__((address_space(1))) u32x4v g_u32x4v;
 typedef const __attribute__((address_space(1))) uint8_t g_u8c;
 
 constexpr int kPT = 32;                 // tokens per tile (MFMA columns)
@@ -50,7 +50,7 @@ constexpr int kPThreads = 64 * kPWaves;
 constexpr int kPF = 32 * kPWaves;       // features per workgroup
 constexpr int kKC = 8;                  // 32-element blocks per staged activation chunk
 constexpr int kXPitch = kKC * 32 + 8;   // bf16 per staged token row (16-byte pad: banks)
-constexpr int kWDepth = 8;              // weight blocks prefetched ahead (divides kKC)
+constexpr int kWChunks = 2;             // weight chunks in flight per wave (ring depth)
 constexpr int kPrefillMaxExperts = 256;
 
 // ---------------------------------------------------------------------------
@@ -148,14 +148,6 @@ struct GemmArgs {
     float limit, alpha;
 };
 
-__device__ __forceinline__ float bias_value(const uint8_t *p, int dt, int row)
-{
-    if (dt < 0) return 0.0f;
-    if (dt == DT_F32) return reinterpret_cast<const float *>(p)[row];
-    const uint16_t b = reinterpret_cast<const uint16_t *>(p)[row];
-    return dt == DT_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
-}
-
 // Splits 8 input values into PL bf16 planes whose sum is exact.
 template <int IN_DT, int PL>
 __device__ __forceinline__ void split_planes(const float (&v)[8], uint32_t (&out)[PL][4])
@@ -171,26 +163,6 @@ __device__ __forceinline__ void split_planes(const float (&v)[8], uint32_t (&out
             out[p][i] = (uint32_t)a | ((uint32_t)b << 16);
             r[2 * i] -= bf16_bits_to_f32(a);
             r[2 * i + 1] -= bf16_bits_to_f32(b);
-        }
-    }
-}
-
-template <int IN_DT>
-__device__ __forceinline__ void load8(const void *src, int64_t elem, float (&v)[8])
-{
-    if constexpr (IN_DT == DT_F32) {
-        const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(src) + elem);
-        const float4 a = p[0], b = p[1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
-        const uint4 q = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(src) + elem);
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint16_t lo = (uint16_t)(w[i] & 0xFFFFu), hi = (uint16_t)(w[i] >> 16);
-            v[2 * i] = IN_DT == DT_BF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
-            v[2 * i + 1] = IN_DT == DT_BF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
         }
     }
 }
@@ -218,103 +190,171 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
     const int row = min(fbase + c, a.fdim - 1);       // clamped: rows past fdim are never stored
     const int nb = a.kdim >> 5;
     const uint8_t *ex = a.experts_base + (int64_t)e * a.stride;
-    const uint8_t *wrow = ex + a.blocks_off + (int64_t)row * nb * 16 + 8 * h;
+    const uint8_t *wrow = ex + a.blocks_off + (int64_t)row * nb * 16;
     const uint8_t *srow = ex + a.scales_off + (int64_t)row * nb;
 
-    // Activation staging: unit u = (token, 8-element piece) of a chunk.
+    // Activation staging: unit u = (token, 8-element piece) of a chunk.  A
+    // thread's units keep their token and piece for every chunk, so their row
+    // offsets are computed once.  Loads keep the raw bits in registers until
+    // the store at the chunk's end converts them (a conversion right after
+    // the load would wait for every older load still in flight).
     constexpr int kUnits = kPT * kKC * 4;             // 8-element pieces per chunk
+    constexpr int kPer = kUnits / kPThreads;          // units per thread
+    constexpr int kRawQ = IN_DT == DT_F32 ? 2 : 1;    // 16-byte loads per unit
     const size_t plane_elems = (size_t)kPT * kXPitch;
-    auto stage_load = [&](int q, float (&v)[kUnits / kPThreads][8]) {
+    int64_t urow[kPer];
+    int upiece[kPer];
 #pragma unroll
-        for (int s = 0; s < kUnits / kPThreads; ++s) {
-            const int u = s * kPThreads + (int)threadIdx.x;
-            const int t = u / (kKC * 4), piece = u % (kKC * 4);
-            const int k = min(q * kKC * 32 + piece * 8, a.kdim - 8);
-            const int64_t in_row = ent[t] / a.in_row_div;
-            load8<IN_DT>(a.in, in_row * a.kdim + k, v[s]);
+    for (int s = 0; s < kPer; ++s) {
+        const int u = s * kPThreads + (int)threadIdx.x;
+        const int t = u / (kKC * 4);
+        upiece[s] = u % (kKC * 4);
+        urow[s] = (int64_t)(ent[t] / a.in_row_div) * a.kdim;
+    }
+    uint4 raw[kPer][kRawQ];
+    auto stage_load = [&](int q) {
+#pragma unroll
+        for (int s = 0; s < kPer; ++s) {
+            const int k = min(q * kKC * 32 + upiece[s] * 8, a.kdim - 8);
+#pragma unroll
+            for (int j = 0; j < kRawQ; ++j)
+                raw[s][j] = reinterpret_cast<const uint4 *>(
+                    static_cast<const uint8_t *>(a.in) +
+                    (urow[s] + k) * (IN_DT == DT_F32 ? 4 : 2))[j];
         }
     };
-    auto stage_store = [&](int buf, const float (&v)[kUnits / kPThreads][8]) {
+    // Pieces past kdim (the last chunks' tails) are stored as zeros, so the
+    // unconditional chunk loop below multiplies them by finite weights only.
+    auto stage_store = [&](int buf, int q) {
 #pragma unroll
-        for (int s = 0; s < kUnits / kPThreads; ++s) {
+        for (int s = 0; s < kPer; ++s) {
             const int u = s * kPThreads + (int)threadIdx.x;
-            const int t = u / (kKC * 4), piece = u % (kKC * 4);
+            const int t = u / (kKC * 4);
+            const bool live = q * kKC * 32 + upiece[s] * 8 < a.kdim;
+            float v[8];
+            if constexpr (IN_DT == DT_F32) {
+                const uint32_t w[8] = {raw[s][0].x, raw[s][0].y, raw[s][0].z, raw[s][0].w,
+                                       raw[s][1].x, raw[s][1].y, raw[s][1].z, raw[s][1].w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = live ? __uint_as_float(w[i]) : 0.0f;
+            } else {
+                const uint32_t w[4] = {raw[s][0].x, raw[s][0].y, raw[s][0].z, raw[s][0].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint16_t lo = (uint16_t)(w[i] & 0xFFFFu), hi = (uint16_t)(w[i] >> 16);
+                    const float flo = IN_DT == DT_BF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+                    const float fhi = IN_DT == DT_BF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+                    v[2 * i] = live ? flo : 0.0f;
+                    v[2 * i + 1] = live ? fhi : 0.0f;
+                }
+            }
             uint32_t pl[PL][4];
-            split_planes<IN_DT, PL>(v[s], pl);
+            split_planes<IN_DT, PL>(v, pl);
 #pragma unroll
             for (int p = 0; p < PL; ++p) {
-                uint16_t *dst = xs + ((size_t)buf * PL + p) * plane_elems + t * kXPitch + piece * 8;
+                uint16_t *dst = xs + ((size_t)buf * PL + p) * plane_elems + t * kXPitch + upiece[s] * 8;
                 *reinterpret_cast<uint4 *>(dst) = make_uint4(pl[p][0], pl[p][1], pl[p][2], pl[p][3]);
             }
         }
     };
 
-    // Weight ring: block b's two dwords and its scale byte, kWDepth ahead.
-    u32x2v wq[kWDepth];
-    uint32_t sq[kWDepth];
-    auto wload = [&](int slot, int b) {
-        const int bb = min(b, nb - 1);
-        wq[slot] = __builtin_nontemporal_load((g_u32x2v *)(wrow + (int64_t)bb * 16));
-        sq[slot] = ((g_u8c *)srow)[bb];
-    };
+    // Weight ring, kWChunks chunks deep: per chunk a lane holds its row's
+    // blocks 4h .. 4h+3 of the chunk (64 contiguous bytes, four 16-byte loads
+    // that the wave issues back to back, so each 128-byte line is fetched
+    // once) and their four scale bytes.  Block indices past nb clamp to the
+    // row's last block; their activations are staged as zeros.
+    u32x4v wq[kWChunks][4];
+    uint32_t sq[kWChunks][4];
+    auto wload = [&](int slot, int q) {
 #pragma unroll
-    for (int d = 0; d < kWDepth; ++d) wload(d, d);
+        for (int i = 0; i < 4; ++i) {
+            const int bb = min(q * kKC + 4 * h + i, nb - 1);
+            wq[slot][i] = *(g_u32x4v *)(wrow + (int64_t)bb * 16);
+            sq[slot][i] = ((g_u8c *)srow)[bb];
+        }
+    };
 
     f32x16 acc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 
-    float sv[kUnits / kPThreads][8];
-    const int nq = (nb + kKC - 1) / kKC;
-    stage_load(0, sv);
-    stage_store(0, sv);
-    __syncthreads();
-    for (int q = 0; q < nq; ++q) {
-        const int buf = q & 1;
-        if (q + 1 < nq) stage_load(q + 1, sv);
-        const int nblk = min(kKC, nb - q * kKC);
+    // Chunk q from ring slot s and activation buffer s: MFMA 4i+d takes dword d
+    // of block 4h+i, i.e. elements 128h + 32i + 8d .. +7 of the chunk, from
+    // both the weights (A) and the staged activation row of entry c (B).
+    auto chunk = [&](int q, auto s_const) {
+        constexpr int s = decltype(s_const)::value;
+        stage_load(q + 1);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int bi = 0; bi < kKC; ++bi) {
-            if (bi < nblk) {
-                const int slot = bi % kWDepth;            // kKC is a multiple of kWDepth
-                const float sc = decode_scale(sq[slot]);
-                uint32_t a0[4], a1[4];
-#define GW_CV(word, sel) __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4((word), sc, (sel)))
-                a0[0] = GW_CV(wq[slot].x, 0); a0[1] = GW_CV(wq[slot].x, 1);
-                a0[2] = GW_CV(wq[slot].x, 2); a0[3] = GW_CV(wq[slot].x, 3);
-                a1[0] = GW_CV(wq[slot].y, 0); a1[1] = GW_CV(wq[slot].y, 1);
-                a1[2] = GW_CV(wq[slot].y, 2); a1[3] = GW_CV(wq[slot].y, 3);
-#undef GW_CV
-                wload(slot, q * kKC + bi + kWDepth);
-                const bf16x8 A0 = __builtin_bit_cast(bf16x8, make_uint4(a0[0], a0[1], a0[2], a0[3]));
-                const bf16x8 A1 = __builtin_bit_cast(bf16x8, make_uint4(a1[0], a1[1], a1[2], a1[3]));
+        for (int i = 0; i < 4; ++i) {
+            const float sc = decode_scale(sq[s][i]);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t w = wq[s][i][d];
+                const uint4 au = make_uint4(
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0)),
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1)),
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2)),
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3)));
+                const bf16x8 A = __builtin_bit_cast(bf16x8, au);
 #pragma unroll
                 for (int p = 0; p < PL; ++p) {
-                    const uint16_t *xr = xs + ((size_t)buf * PL + p) * plane_elems + c * kXPitch +
-                                         bi * 32 + 16 * h;
-                    const bf16x8 B0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(xr));
-                    const bf16x8 B1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(xr + 8));
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A0, B0, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A1, B1, acc, 0, 0, 0);
+                    const uint16_t *xr = xs + ((size_t)s * PL + p) * plane_elems + c * kXPitch +
+                                         128 * h + 32 * i + 8 * d;
+                    const bf16x8 B = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(xr));
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, acc, 0, 0, 0);
                 }
             }
         }
-        if (q + 1 < nq) stage_store(buf ^ 1, sv);
+        __builtin_amdgcn_sched_barrier(0);
+        wload(s, q + kWChunks);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_store(s ^ 1, q + 1);
         __syncthreads();
+    };
+
+    // nq rounded up to the ring depth: a padding chunk sees zero activations.
+    const int nq = (nb + kKC - 1) / kKC;
+    const int nq_pad = (nq + kWChunks - 1) / kWChunks * kWChunks;
+#pragma unroll
+    for (int s = 0; s < kWChunks; ++s) wload(s, s);
+    stage_load(0);
+    stage_store(0, 0);
+    __syncthreads();
+    for (int q = 0; q < nq_pad; q += kWChunks) {
+        chunk(q, std::integral_constant<int, 0>{});
+        chunk(q + 1, std::integral_constant<int, 1>{});
     }
 
     // Epilogue: lane holds entry column c, feature rows 8(v/4) + 4h + (v%4).
     const bool col_ok = c < ntok;
     const int entry = ent[c];
     const uint8_t *bias = ex + a.bias_off;
+    // The lane's 16 bias values, loaded together before any is used.
+    float bv[16];
+    {
+        uint32_t raw[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int r = min(fbase + 8 * (v >> 2) + 4 * h + (v & 3), a.fdim - 1);
+            raw[v] = a.bias_dt == DT_F32 ? reinterpret_cast<const uint32_t *>(bias)[r]
+                                         : (uint32_t)reinterpret_cast<const uint16_t *>(bias)[r];
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+            bv[v] = a.bias_dt < 0 ? 0.0f
+                    : a.bias_dt == DT_F32 ? __uint_as_float(raw[v])
+                    : a.bias_dt == DT_BF16 ? bf16_bits_to_f32((uint16_t)raw[v])
+                                           : f16_bits_to_f32((uint16_t)raw[v]);
+    }
     if constexpr (GATE_UP) {
         const int half = a.fdim >> 1;
 #pragma unroll
         for (int v = 0; v < 16; v += 2) {
             const int r = fbase + 8 * (v >> 2) + 4 * h + (v & 3);   // even: gate, r+1: up
             if (col_ok && r + 1 < a.fdim) {
-                const float gate = acc[v] + bias_value(bias, a.bias_dt, r);
-                const float up = acc[v + 1] + bias_value(bias, a.bias_dt, r + 1);
+                const float gate = acc[v] + bv[v];
+                const float up = acc[v + 1] + bv[v + 1];
                 const float y = apply_activation(a.act_kind, gate, up, a.limit, a.alpha);
                 a.act_out[(int64_t)entry * half + (r >> 1)] = f32_to_f16_bits(y);
             }
@@ -324,7 +364,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
         for (int v = 0; v < 16; ++v) {
             const int r = fbase + 8 * (v >> 2) + 4 * h + (v & 3);
             if (col_ok && r < a.fdim)
-                a.y_out[(int64_t)entry * a.fdim + r] = acc[v] + bias_value(bias, a.bias_dt, r);
+                a.y_out[(int64_t)entry * a.fdim + r] = acc[v] + bv[v];
         }
     }
 }
