@@ -199,7 +199,8 @@ def prefill_bench(gw, args) -> int:
     gu = kernels.get("prefill_gate_up", {}).get("avg_us")
     roof = None
     if gu:
-        gu_bytes = touched * gate_up_bytes(lay)
+        gu_bytes = touched * sum(lay.sizes[k] for k in ("gate_up_blocks", "gate_up_scales",
+                                                         "gate_up_bias")) + T * H * 2
         ach = gu_bytes / (gu * 1e-6) / 1e9
         gu_tflops = 2.0 * T * K * 2 * F * H / (gu * 1e-6) / 1e12
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
