@@ -1013,7 +1013,8 @@ struct PrefillScratch {
     int32_t *ids;
     float *weights;
     int32_t *offsets, *order, *tiles, *ntiles;
-    uint16_t *act;
+    uint16_t *xsplit;   // [planes][T, hidden] bf16 planes of a fp16 or fp32 x
+    uint16_t *act;      // [2][N, inter] bf16 planes of the fp16 activations
     float *y;
 };
 
@@ -1039,7 +1040,8 @@ size_t prefill_layout(const gw_expert_runner *r, int T, int K, int E, char *base
     s.order = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * N));
     s.tiles = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * tiles));
     s.ntiles = reinterpret_cast<int32_t *>(take(sizeof(int32_t)));
-    s.act = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * N * r->inter));
+    s.xsplit = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * 3 * (size_t)T * r->hidden));
+    s.act = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * 2 * N * r->inter));
     s.y = reinterpret_cast<float *>(take(sizeof(float) * N * r->hidden));
     if (ps) *ps = s;
     return o;
@@ -1088,7 +1090,9 @@ extern "C" int gw_moe_prefill_forward(gw_expert_runner *r, const gw_moe_layer_ar
     GW_CHECK(dtype_ok(a->x_dtype), GW_ERR_ARG, "bad x dtype");
     GW_CHECK(aligned16(a->x), GW_ERR_ARG, "x must be 16-byte aligned for prefill");
     GW_CHECK(a->logits || a->router_weight, GW_ERR_ARG, "need logits or router weights");
-    GW_CHECK(r->hidden % 32 == 0 && r->inter % 32 == 0, GW_ERR_SHAPE, "bad runner shape");
+    GW_CHECK(r->hidden % 32 == 0 && r->inter % 32 == 0 && r->hidden >= 128 && r->inter >= 128,
+             GW_ERR_SHAPE, "prefill needs hidden and intermediate sizes that are multiples of 32 "
+             "and at least 128 (got %lld, %lld)", (long long)r->hidden, (long long)r->inter);
     const int T = a->tokens, K = (int)a->top_k, E = (int)a->expert_count;
     int rc = gw_expert_runner_reserve_prefill(r, T, K, E);
     if (rc) return rc;
@@ -1129,7 +1133,15 @@ extern "C" int gw_moe_prefill_forward(gw_expert_runner *r, const gw_moe_layer_ar
     g.limit = r->limit;
     g.alpha = r->alpha;
     {
-        g.in = a->x;
+        const int planes = gw::prefill_planes(a->x_dtype);
+        const int64_t nx = (int64_t)T * r->hidden;
+        g.in = static_cast<const uint16_t *>(a->x);
+        g.in_plane = nx;
+        if (planes > 1) {
+            ProfScope p(ctx, "prefill_split");
+            GW_HIP(gw::launch_prefill_split(p.launch(L), a->x, a->x_dtype, nx, ps.xsplit));
+            g.in = ps.xsplit;
+        }
         g.in_row_div = K;
         g.blocks_off = sec.gu_blocks;
         g.scales_off = sec.gu_scales;
@@ -1137,12 +1149,14 @@ extern "C" int gw_moe_prefill_forward(gw_expert_runner *r, const gw_moe_layer_ar
         g.kdim = (int)r->hidden;
         g.fdim = (int)(2 * r->inter);
         g.act_out = ps.act;
+        g.act_plane = (int64_t)T * K * r->inter;
         g.y_out = nullptr;
         ProfScope p(ctx, "prefill_gate_up");
-        GW_HIP(gw::launch_prefill_gemm(p.launch(L), true, a->x_dtype, g, max_tiles));
+        GW_HIP(gw::launch_prefill_gemm(p.launch(L), true, planes, g, max_tiles));
     }
     {
         g.in = ps.act;
+        g.in_plane = (int64_t)T * K * r->inter;
         g.in_row_div = 1;
         g.blocks_off = sec.dn_blocks;
         g.scales_off = sec.dn_scales;
@@ -1150,9 +1164,10 @@ extern "C" int gw_moe_prefill_forward(gw_expert_runner *r, const gw_moe_layer_ar
         g.kdim = (int)r->inter;
         g.fdim = (int)r->hidden;
         g.act_out = nullptr;
+        g.act_plane = 0;
         g.y_out = ps.y;
         ProfScope p(ctx, "prefill_down");
-        GW_HIP(gw::launch_prefill_gemm(p.launch(L), false, GW_F16, g, max_tiles));
+        GW_HIP(gw::launch_prefill_gemm(p.launch(L), false, 2, g, max_tiles));
     }
     {
         ProfScope p(ctx, "prefill_combine");

@@ -74,26 +74,31 @@ hipError_t launch_fused_layer(const Launch &L, int grid, const RouteArgs &route,
 // One grouped GEMM launch (gate_up or down) over the work items of a grouping.
 struct PrefillGemm {
     const int32_t *tiles, *ntiles, *offsets, *order;
-    const void *in;               // [rows, kdim] activations
+    const uint16_t *in;           // bf16 planes of [rows, kdim] activations
+    int64_t in_plane;             // elements between planes
     int in_row_div;               // entry -> input row divisor (top_k for x, 1 for act)
     const uint8_t *experts_base;
     int64_t stride;
     int64_t blocks_off, scales_off, bias_off;
     int bias_dt;                  // -1: none
     int kdim, fdim;
-    uint16_t *act_out;            // gate_up: [entries, fdim/2] fp16
+    uint16_t *act_out;            // gate_up: two bf16 planes of [entries, fdim/2]
+    int64_t act_plane;            // elements between those planes
     float *y_out;                 // down: [entries, fdim] fp32
     int act_kind;
     float limit, alpha;
 };
 int prefill_max_tiles(int T, int K, int E);
-int prefill_gemm_lds_bytes(int in_dt);
+int prefill_planes(int in_dt);        // bf16 planes that hold a dtype exactly: 1, 2 or 3
+int prefill_gemm_lds_bytes(int planes);
 hipError_t launch_prefill_route(const Launch &L, const float *logits, int T, int E, int K,
                                 int32_t *ids, float *weights);
 hipError_t launch_prefill_group(const Launch &L, const int32_t *ids, int N, int E,
                                 int32_t *offsets, int32_t *order, int32_t *tiles,
                                 int32_t *ntiles, int max_tiles);
-hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int in_dt, const PrefillGemm &g,
+hipError_t launch_prefill_split(const Launch &L, const void *in, int in_dt, int64_t n,
+                                uint16_t *out);
+hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const PrefillGemm &g,
                                int max_tiles);
 hipError_t launch_prefill_combine(const Launch &L, const float *y, const float *w, int T, int K,
                                   int H, float *out, uint16_t *out_bf16);

@@ -22,6 +22,8 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_ext.h>
 
+#include <algorithm>
+
 #include "gw_device.h"
 #include "gw_launch.h"
 #include "gw_route.h"
@@ -49,8 +51,6 @@ constexpr int kPWaves = 8;              // waves per workgroup, 32 features each
 constexpr int kPThreads = 64 * kPWaves;
 constexpr int kPF = 32 * kPWaves;       // features per workgroup
 constexpr int kKC = 8;                  // 32-element blocks per staged activation chunk
-constexpr int kXPitch = kKC * 32 + 8;   // bf16 per staged token row (16-byte pad: banks)
-constexpr int kWChunks = 2;             // weight chunks in flight per wave (ring depth)
 constexpr int kPrefillMaxExperts = 256;
 
 // ---------------------------------------------------------------------------
@@ -121,13 +121,26 @@ __global__ __launch_bounds__(1024) void prefill_group_kernel(const int32_t *__re
 // ---------------------------------------------------------------------------
 // 3./4. Grouped GEMM: workgroup (feature tile f, work item) computes
 // C[256 features x 32 entries] = W_e[f-tile, :] . X[entries, :]^T over K, one
-// 32x32 block per wave.  Per 32-element K block a lane (row r = lane & 31,
-// half h = lane >> 5) holds dwords 2h, 2h+1 of row r's 16-byte block, i.e.
-// elements 16h .. 16h+15, widened with the scale folded in; MFMA j (0, 1)
-// takes elements 16h + 8j .. +7 from both A (weights) and B (the staged
-// activation row of entry r' = lane & 31), so A and B share one K order.
-// C element v of a lane is feature row 8(v/4) + 4h + (v%4), entry column
-// lane & 31.
+// 32x32 block per wave, in chunks of kKC 32-element blocks (256 K elements).
+//
+// Operands.  The activations arrive as PL bf16 planes whose sum is exact
+// (bf16 x: the input itself; fp16 or fp32 x: split beforehand; the fp16
+// gate_up activation: written as two planes by the gate_up epilogue).  Per
+// chunk a lane (row r = lane & 31, half h = lane >> 5) holds its row's blocks
+// 4h .. 4h+3 (64 contiguous bytes), widened to bf16 with the block scale
+// folded in; MFMA 4i+d takes dword d of block 4h+i, i.e. chunk elements
+// 128h + 32i + 8d .. +7, from A (weights) and from B (the staged activation
+// row of entry r), so A and B share one K order.  C element v of a lane is
+// feature row 8(v/4) + 4h + (v%4), entry column lane & 31.
+//
+// Pipeline.  A chunk's activations are staged by LDS-DMA (16 bytes per lane
+// straight into LDS, no registers) and its weights are loaded into a
+// register ring; both are issued together kDepth-1 chunks ahead, activation
+// first.  The vector-memory counter completes in issue order, so waiting for
+// a chunk's activations leaves every younger load in flight: kDepth-1 chunks
+// of weights stream while one chunk is multiplied.  Staged rows are 512
+// bytes (32 pieces of 16 bytes); piece j of row t sits in slot j ^ (t & 15),
+// which keeps the B reads of 16 consecutive rows on distinct LDS banks.
 // ---------------------------------------------------------------------------
 
 struct GemmArgs {
@@ -135,46 +148,72 @@ struct GemmArgs {
     const int32_t *ntiles;
     const int32_t *offsets;
     const int32_t *order;
-    const void *in;               // activations: [rows, kdim] of in_dt
+    const uint16_t *in;           // PL bf16 planes of [rows, kdim]
+    int64_t in_plane;             // elements between planes
+    uint32_t in_bytes;            // bytes of all planes (below 2^31)
     int in_row_div;               // entry -> input row: entry / in_row_div (K for x, 1 for act)
     const uint8_t *experts_base;
     int64_t stride;
     int64_t blocks_off, scales_off, bias_off;   // section offsets within an expert
     int bias_dt;                  // -1: no bias
     int kdim, fdim;               // K (input width) and weight rows
-    uint16_t *act_out;            // gate_up: [N, fdim/2] fp16
+    uint16_t *act_out;            // gate_up: two bf16 planes of [N, fdim/2] (fp16 value = hi + lo)
+    int64_t act_plane;            // elements between the two planes
     float *y_out;                 // down: [N, fdim] fp32
     int act_kind;
     float limit, alpha;
 };
 
-// Splits 8 input values into PL bf16 planes whose sum is exact.
-template <int IN_DT, int PL>
-__device__ __forceinline__ void split_planes(const float (&v)[8], uint32_t (&out)[PL][4])
+template <int PL> struct PrefillDepth { static constexpr int value = PL == 3 ? 3 : 4; };
+
+constexpr int kRowBytes = kKC * 32 * 2;       // one staged chunk row: 256 bf16
+constexpr int kPlaneBytes = kPT * kRowBytes;  // one staged plane of a chunk
+
+typedef __attribute__((address_space(3))) void l_void;
+
+// s_waitcnt with only the vector-memory count limited (gfx9 encoding: vmcnt
+// in bits 3:0 and 15:14; expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+template <int N> __device__ __forceinline__ void wait_vmcnt()
 {
-    float r[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = v[i];
-#pragma unroll
-    for (int p = 0; p < PL; ++p) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint16_t a = f32_to_bf16_bits(r[2 * i]), b = f32_to_bf16_bits(r[2 * i + 1]);
-            out[p][i] = (uint32_t)a | ((uint32_t)b << 16);
-            r[2 * i] -= bf16_bits_to_f32(a);
-            r[2 * i + 1] -= bf16_bits_to_f32(b);
-        }
-    }
+    static_assert(N >= 0 && N < 64, "vmcnt out of range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int IN_DT, int PL, bool GATE_UP>
+// The staged activations are read with ds_read_b128 written out here: the
+// compiler's own wait insertion treats any LDS read after an LDS-DMA as
+// possibly dependent on the newest DMA and would drain the whole pipeline;
+// the kernel orders DMA and reads itself (a counted vmcnt wait and a barrier
+// per chunk), and lds_settle waits for the reads before their values are used.
+__device__ __forceinline__ uint32_t lds_address(const void *p)
+{
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+__device__ __forceinline__ bf16x8 lds_read16(uint32_t addr)
+{
+    bf16x8 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+
+__device__ __forceinline__ void lds_settle(bf16x8 &a, bf16x8 &b, bf16x8 &c, bf16x8 &d)
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+
+template <int PL, bool GATE_UP>
 __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
 {
+    constexpr int D = PrefillDepth<PL>::value;
+    constexpr int kNW = 5;                    // weight-ring loads per chunk (4 x 16 B + scales)
+    constexpr int kNX = 2 * PL;               // LDS-DMA loads per chunk per wave
+    // Loads a wave issues after a chunk's DMA until it waits for that DMA.
+    constexpr int kYounger = kNW + (D - 2) * (kNX + kNW);
     // Dynamic LDS only (a static __shared__ variable would shift the dynamic
-    // area off its 16-byte alignment): [kPT] entries, then [2][PL][kPT][kXPitch].
+    // area off its alignment): [kPT] entries, then the [D][PL] staged chunks.
     extern __shared__ __align__(16) uint32_t plds[];
     int *ent = reinterpret_cast<int *>(plds);
-    uint16_t *xs = reinterpret_cast<uint16_t *>(plds + kPT);
+    uint8_t *xring = reinterpret_cast<uint8_t *>(plds + kPT);
     const int item = blockIdx.y;
     if (item >= *a.ntiles) return;                    // uniform: the workgroup leaves
     const int te = a.tiles[item];
@@ -184,7 +223,8 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
     if (threadIdx.x < kPT) ent[threadIdx.x] = a.order[g0 + min((int)threadIdx.x, ntok - 1)];
     __syncthreads();
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
     const int h = lane >> 5, c = lane & 31;
     const int fbase = blockIdx.x * kPF + wave * 32;
     const int row = min(fbase + c, a.fdim - 1);       // clamped: rows past fdim are never stored
@@ -193,138 +233,150 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
     const uint8_t *wrow = ex + a.blocks_off + (int64_t)row * nb * 16;
     const uint8_t *srow = ex + a.scales_off + (int64_t)row * nb;
 
-    // Activation staging: unit u = (token, 8-element piece) of a chunk.  A
-    // thread's units keep their token and piece for every chunk, so their row
-    // offsets are computed once.  Loads keep the raw bits in registers until
-    // the store at the chunk's end converts them (a conversion right after
-    // the load would wait for every older load still in flight).
-    constexpr int kUnits = kPT * kKC * 4;             // 8-element pieces per chunk
-    constexpr int kPer = kUnits / kPThreads;          // units per thread
-    constexpr int kRawQ = IN_DT == DT_F32 ? 2 : 1;    // 16-byte loads per unit
-    const size_t plane_elems = (size_t)kPT * kXPitch;
-    int64_t urow[kPer];
-    int upiece[kPer];
+    // Staging: wave w copies rows 4w .. 4w+3 of each plane, two rows per DMA
+    // (lanes 0-31 row 4w+2n, lanes 32-63 the next); a lane's slot is lane & 31.
+    int64_t xrow[2];
+    int xpiece[2];
 #pragma unroll
-    for (int s = 0; s < kPer; ++s) {
-        const int u = s * kPThreads + (int)threadIdx.x;
-        const int t = u / (kKC * 4);
-        upiece[s] = u % (kKC * 4);
-        urow[s] = (int64_t)(ent[t] / a.in_row_div) * a.kdim;
+    for (int n = 0; n < 2; ++n) {
+        const int t = 4 * wave + 2 * n + h;
+        xpiece[n] = (lane & 31) ^ (t & 15);
+        xrow[n] = (int64_t)(ent[t] / a.in_row_div) * a.kdim;
     }
-    uint4 raw[kPer][kRawQ];
-    auto stage_load = [&](int q) {
+    // Pieces past kdim read the row's last piece instead; the weights of the
+    // blocks there are zeroed, so they add exact zeros (for finite inputs).
+    // The buffer form of the LDS-DMA (not the global one) keeps the
+    // compiler's own waits for the weight ring exact.
+    const __amdgpu_buffer_rsrc_t xres =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.in), (short)0,
+                                          (int)a.in_bytes, 0x00020000);
+    auto xload = [&](int buf, int q) {
 #pragma unroll
-        for (int s = 0; s < kPer; ++s) {
-            const int k = min(q * kKC * 32 + upiece[s] * 8, a.kdim - 8);
+        for (int p = 0; p < PL; ++p) {
 #pragma unroll
-            for (int j = 0; j < kRawQ; ++j)
-                raw[s][j] = reinterpret_cast<const uint4 *>(
-                    static_cast<const uint8_t *>(a.in) +
-                    (urow[s] + k) * (IN_DT == DT_F32 ? 4 : 2))[j];
-        }
-    };
-    // Pieces past kdim (the last chunks' tails) are stored as zeros, so the
-    // unconditional chunk loop below multiplies them by finite weights only.
-    auto stage_store = [&](int buf, int q) {
-#pragma unroll
-        for (int s = 0; s < kPer; ++s) {
-            const int u = s * kPThreads + (int)threadIdx.x;
-            const int t = u / (kKC * 4);
-            const bool live = q * kKC * 32 + upiece[s] * 8 < a.kdim;
-            float v[8];
-            if constexpr (IN_DT == DT_F32) {
-                const uint32_t w[8] = {raw[s][0].x, raw[s][0].y, raw[s][0].z, raw[s][0].w,
-                                       raw[s][1].x, raw[s][1].y, raw[s][1].z, raw[s][1].w};
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = live ? __uint_as_float(w[i]) : 0.0f;
-            } else {
-                const uint32_t w[4] = {raw[s][0].x, raw[s][0].y, raw[s][0].z, raw[s][0].w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint16_t lo = (uint16_t)(w[i] & 0xFFFFu), hi = (uint16_t)(w[i] >> 16);
-                    const float flo = IN_DT == DT_BF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
-                    const float fhi = IN_DT == DT_BF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
-                    v[2 * i] = live ? flo : 0.0f;
-                    v[2 * i + 1] = live ? fhi : 0.0f;
-                }
-            }
-            uint32_t pl[PL][4];
-            split_planes<IN_DT, PL>(v, pl);
-#pragma unroll
-            for (int p = 0; p < PL; ++p) {
-                uint16_t *dst = xs + ((size_t)buf * PL + p) * plane_elems + t * kXPitch + upiece[s] * 8;
-                *reinterpret_cast<uint4 *>(dst) = make_uint4(pl[p][0], pl[p][1], pl[p][2], pl[p][3]);
+            for (int n = 0; n < 2; ++n) {
+                const int k = min(q * (kKC * 32) + xpiece[n] * 8, a.kdim - 8);
+                const uint32_t voff = (uint32_t)((p * a.in_plane + xrow[n] + k) * 2);
+                uint8_t *dst = xring + (size_t)(buf * PL + p) * kPlaneBytes +
+                               (4 * wave + 2 * n) * kRowBytes;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (l_void *)dst, 16, voff, 0, 0, 0);
             }
         }
     };
 
-    // Weight ring, kWChunks chunks deep: per chunk a lane holds its row's
-    // blocks 4h .. 4h+3 of the chunk (64 contiguous bytes, four 16-byte loads
-    // that the wave issues back to back, so each 128-byte line is fetched
-    // once) and their four scale bytes.  Block indices past nb clamp to the
-    // row's last block; their activations are staged as zeros.
-    u32x4v wq[kWChunks][4];
-    uint32_t sq[kWChunks][4];
+    // Weight ring: per chunk a lane's four 16-byte blocks (issued back to
+    // back, so each 128-byte line is fetched once) and their four scale bytes
+    // in one 4-byte load.  Block indices past nb clamp to the row's last
+    // block; the scale load stays inside the row (shifted so byte i is block
+    // base+i's scale while that block exists).
+    // The loaded words are used only when their chunk is multiplied (any
+    // arithmetic on them here would wait for the load just issued).
+    u32x4v wq[D][4];
+    uint32_t sq[D], sshift[D];
     auto wload = [&](int slot, int q) {
+        const int base = q * kKC + 4 * h;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int bb = min(q * kKC + 4 * h + i, nb - 1);
+            const int bb = min(base + i, nb - 1);
             wq[slot][i] = *(g_u32x4v *)(wrow + (int64_t)bb * 16);
-            sq[slot][i] = ((g_u8c *)srow)[bb];
         }
+        const int off = min(base, nb - 4);
+        __builtin_memcpy(&sq[slot], srow + off, 4);
+        sshift[slot] = 8 * min(base - off, 3);
     };
 
     f32x16 acc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 
-    // Chunk q from ring slot s and activation buffer s: MFMA 4i+d takes dword d
-    // of block 4h+i, i.e. elements 128h + 32i + 8d .. +7 of the chunk, from
-    // both the weights (A) and the staged activation row of entry c (B).
-    auto chunk = [&](int q, auto s_const) {
+    // B read address of piece 16h + j for entry c: row c, slot (j ^ (c & 15)).
+    const uint32_t rb = (uint32_t)(c * kRowBytes + 256 * h + ((c & 15) << 4));
+    const uint32_t xbase = lds_address(xring);
+
+    // Chunk q from ring slot / staging buffer s.  A block past nb is widened
+    // from a zero word with scale 1: exact zeros.
+    auto multiply = [&](int q, auto s_const) {
         constexpr int s = decltype(s_const)::value;
-        stage_load(q + 1);
-        __builtin_amdgcn_sched_barrier(0);
+        // Recomputed per chunk rather than kept in 16 registers per plane.
+        uint32_t rbs = rb;
+        asm volatile("" : "+v"(rbs));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float sc = decode_scale(sq[s][i]);
+            bf16x8 B[4][PL];
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-                const uint32_t w = wq[s][i][d];
+                const uint32_t off = rbs ^ (uint32_t)((4 * i + d) << 4);
+#pragma unroll
+                for (int p = 0; p < PL; ++p)
+                    B[d][p] = lds_read16(xbase + (uint32_t)((s * PL + p) * kPlaneBytes) + off);
+            }
+            // Bit masks rather than selects, so no branch separates a load
+            // from its use.
+            const uint32_t keep = q * kKC + 4 * h + i < nb ? 0xFFFFFFFFu : 0u;
+            const uint32_t sb = (sq[s] >> (sshift[s] + 8 * i)) & 0xFFu;
+            const float sc = decode_scale(sb ^ ((sb ^ 127u) & ~keep));
+            bf16x8 A[4];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t w = wq[s][i][d] & keep;
                 const uint4 au = make_uint4(
                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0)),
                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1)),
                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2)),
                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3)));
-                const bf16x8 A = __builtin_bit_cast(bf16x8, au);
-#pragma unroll
-                for (int p = 0; p < PL; ++p) {
-                    const uint16_t *xr = xs + ((size_t)s * PL + p) * plane_elems + c * kXPitch +
-                                         128 * h + 32 * i + 8 * d;
-                    const bf16x8 B = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(xr));
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, acc, 0, 0, 0);
-                }
+                A[d] = __builtin_bit_cast(bf16x8, au);
             }
+#pragma unroll
+            for (int p = 0; p < PL; ++p) lds_settle(B[0][p], B[1][p], B[2][p], B[3][p]);
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int p = 0; p < PL; ++p)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[d], B[d][p], acc, 0, 0, 0);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        wload(s, q + kWChunks);
-        __builtin_amdgcn_sched_barrier(0);
-        stage_store(s ^ 1, q + 1);
-        __syncthreads();
     };
 
-    // nq rounded up to the ring depth: a padding chunk sees zero activations.
+    // One step: issue chunk q+D-1 into the slot chunk q-1 left, multiply
+    // chunk q, then wait for this wave's DMA of chunk q+1 and meet the other
+    // waves (after which every row of chunk q+1 is in LDS and nobody reads
+    // chunk q's buffer any more).
+    auto step = [&](int q, auto s_const) {
+        constexpr int s = decltype(s_const)::value;
+        constexpr int sn = (s + D - 1) % D;
+        xload(sn, q + D - 1);
+        wload(sn, q + D - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(q, s_const);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<kYounger>();
+        // A bare barrier: a fenced one would also wait for every LDS-DMA in
+        // flight.  Ordering is explicit here: the counted wait above for the
+        // DMA, and lds_settle for this wave's reads.
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // nq rounded up to the ring depth: a padding chunk multiplies zero weights.
     const int nq = (nb + kKC - 1) / kKC;
-    const int nq_pad = (nq + kWChunks - 1) / kWChunks * kWChunks;
+    const int nq_pad = (nq + D - 1) / D * D;
 #pragma unroll
-    for (int s = 0; s < kWChunks; ++s) wload(s, s);
-    stage_load(0);
-    stage_store(0, 0);
-    __syncthreads();
-    for (int q = 0; q < nq_pad; q += kWChunks) {
-        chunk(q, std::integral_constant<int, 0>{});
-        chunk(q + 1, std::integral_constant<int, 1>{});
+    for (int s = 0; s < D - 1; ++s) {
+        xload(s, s);
+        wload(s, s);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<kYounger>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    for (int q = 0; q < nq_pad; q += D) {
+        step(q, std::integral_constant<int, 0>{});
+        step(q + 1, std::integral_constant<int, 1>{});
+        step(q + 2, std::integral_constant<int, 2>{});
+        if constexpr (D == 4) step(q + 3, std::integral_constant<int, 3>{});
+    }
+    // The DMAs of the padding chunks past nq_pad land before the workgroup's
+    // LDS is released.
+    wait_vmcnt<0>();
 
     // Epilogue: lane holds entry column c, feature rows 8(v/4) + 4h + (v%4).
     const bool col_ok = c < ntok;
@@ -356,7 +408,14 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
                 const float gate = acc[v] + bv[v];
                 const float up = acc[v + 1] + bv[v + 1];
                 const float y = apply_activation(a.act_kind, gate, up, a.limit, a.alpha);
-                a.act_out[(int64_t)entry * half + (r >> 1)] = f32_to_f16_bits(y);
+                // The reference rounds the activation to fp16; it is kept as
+                // the exact sum of two bf16 planes for the down GEMM.
+                const float y16 = f16_bits_to_f32(f32_to_f16_bits(y));
+                const uint16_t hi = f32_to_bf16_bits(y16);
+                const uint16_t lo = f32_to_bf16_bits(y16 - bf16_bits_to_f32(hi));
+                const int64_t o = (int64_t)entry * half + (r >> 1);
+                a.act_out[o] = hi;
+                a.act_out[a.act_plane + o] = lo;
             }
         }
     } else {
@@ -365,6 +424,25 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
             const int r = fbase + 8 * (v >> 2) + 4 * h + (v & 3);
             if (col_ok && r < a.fdim)
                 a.y_out[(int64_t)entry * a.fdim + r] = acc[v] + bv[v];
+        }
+    }
+}
+
+// Splits n fp16 or fp32 values into PL bf16 planes whose sum is exact.
+template <int IN_DT, int PL>
+__global__ __launch_bounds__(256) void prefill_split_kernel(const void *__restrict__ in,
+                                                            int64_t n,
+                                                            uint16_t *__restrict__ out)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        float r = IN_DT == DT_F32 ? static_cast<const float *>(in)[i]
+                                  : f16_bits_to_f32(static_cast<const uint16_t *>(in)[i]);
+#pragma unroll
+        for (int p = 0; p < PL; ++p) {
+            const uint16_t b = f32_to_bf16_bits(r);
+            out[p * n + i] = b;
+            r -= bf16_bits_to_f32(b);
         }
     }
 }
@@ -417,23 +495,46 @@ hipError_t launch_prefill_group(const Launch &L, const int32_t *ids, int N, int 
     return hipGetLastError();
 }
 
-int prefill_gemm_lds_bytes(int in_dt)
+int prefill_planes(int in_dt) { return in_dt == DT_BF16 ? 1 : in_dt == DT_F16 ? 2 : 3; }
+
+int prefill_gemm_lds_bytes(int planes)
 {
-    const int pl = in_dt == DT_BF16 ? 1 : in_dt == DT_F16 ? 2 : 3;
-    return kPT * 4 + 2 * pl * kPT * kXPitch * 2;
+    const int depth = planes == 3 ? PrefillDepth<3>::value : PrefillDepth<1>::value;
+    return kPT * 4 + depth * planes * kPlaneBytes;
 }
 
-hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int in_dt, const PrefillGemm &g,
+hipError_t launch_prefill_split(const Launch &L, const void *in, int in_dt, int64_t n,
+                                uint16_t *out)
+{
+    if (n <= 0) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)std::min<int64_t>(pdiv_up(n, 256), 4096));
+    if (in_dt == DT_F16)
+        GW_LAUNCH((prefill_split_kernel<DT_F16, 2>), grid, dim3(256), 0, L, in, n, out);
+    else if (in_dt == DT_F32)
+        GW_LAUNCH((prefill_split_kernel<DT_F32, 3>), grid, dim3(256), 0, L, in, n, out);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const PrefillGemm &g,
                                int max_tiles)
 {
-    if (g.kdim % 32 != 0 || g.kdim < 32 || g.fdim <= 0 || max_tiles <= 0)
+    // The staged rows are read 16 bytes at a time and the scale word 4 bytes
+    // back from a row's end: K must be a multiple of 32 and at least 128.
+    if (g.kdim % 32 != 0 || g.kdim < 128 || g.fdim <= 0 || max_tiles <= 0)
         return hipErrorInvalidValue;
+    if (planes < 1 || planes > 3 || (!gate_up && planes != 2)) return hipErrorInvalidValue;
     GemmArgs a;
     a.tiles = g.tiles;
     a.ntiles = g.ntiles;
     a.offsets = g.offsets;
     a.order = g.order;
     a.in = g.in;
+    a.in_plane = g.in_plane;
+    if (g.in_plane <= 0 || (int64_t)planes * g.in_plane * 2 >= ((int64_t)1 << 31))
+        return hipErrorInvalidValue;     // staged through 32-bit buffer offsets
+    a.in_bytes = (uint32_t)(planes * g.in_plane * 2);
     a.in_row_div = g.in_row_div;
     a.experts_base = g.experts_base;
     a.stride = g.stride;
@@ -444,42 +545,39 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int in_dt, const P
     a.kdim = g.kdim;
     a.fdim = g.fdim;
     a.act_out = g.act_out;
+    a.act_plane = g.act_plane;
     a.y_out = g.y_out;
     a.act_kind = g.act_kind;
     a.limit = g.limit;
     a.alpha = g.alpha;
     const dim3 grid(pdiv_up(g.fdim, kPF), max_tiles);
-    const size_t lds = (size_t)prefill_gemm_lds_bytes(in_dt);
+    const size_t lds = (size_t)prefill_gemm_lds_bytes(planes);
     hipError_t err = hipSuccess;
-    auto go = [&](auto dt, auto pl, auto gu) {
-        constexpr int DT = decltype(dt)::value, PL = decltype(pl)::value;
+    auto go = [&](auto pl, auto gu) {
+        constexpr int PL = decltype(pl)::value;
         constexpr bool GU = decltype(gu)::value;
-        // More than 64 KiB of dynamic LDS (two or three planes) must be allowed
-        // explicitly, once per instantiation.
+        // More than 64 KiB of dynamic LDS must be allowed explicitly, once per
+        // instantiation.
         static bool lds_ok = false;
         if (!lds_ok) {
-            err = hipFuncSetAttribute(reinterpret_cast<const void *>(&prefill_gemm_kernel<DT, PL, GU>),
+            err = hipFuncSetAttribute(reinterpret_cast<const void *>(&prefill_gemm_kernel<PL, GU>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
             if (err != hipSuccess) return;
             lds_ok = true;
         }
-        GW_LAUNCH((prefill_gemm_kernel<DT, PL, GU>), grid, dim3(kPThreads), lds, L, a);
+        GW_LAUNCH((prefill_gemm_kernel<PL, GU>), grid, dim3(kPThreads), lds, L, a);
     };
-    using B1 = std::integral_constant<int, DT_BF16>;
-    using H2 = std::integral_constant<int, DT_F16>;
-    using F3 = std::integral_constant<int, DT_F32>;
     using P1 = std::integral_constant<int, 1>;
     using P2 = std::integral_constant<int, 2>;
     using P3 = std::integral_constant<int, 3>;
     using Y = std::true_type;
     using N = std::false_type;
     if (gate_up) {
-        if (in_dt == DT_BF16) go(B1{}, P1{}, Y{});
-        else if (in_dt == DT_F16) go(H2{}, P2{}, Y{});
-        else go(F3{}, P3{}, Y{});
+        if (planes == 1) go(P1{}, Y{});
+        else if (planes == 2) go(P2{}, Y{});
+        else go(P3{}, Y{});
     } else {
-        if (in_dt != DT_F16) return hipErrorInvalidValue;   // the activation is fp16
-        go(H2{}, P2{}, N{});
+        go(P2{}, N{});
     }
     if (err != hipSuccess) return err;
     return hipGetLastError();
