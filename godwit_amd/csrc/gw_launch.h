@@ -90,7 +90,7 @@ struct PrefillGemm {
 };
 int prefill_max_tiles(int T, int K, int E);
 int prefill_planes(int in_dt);        // bf16 planes that hold a dtype exactly: 1, 2 or 3
-int prefill_gemm_lds_bytes(int planes);
+int prefill_gemm_lds_bytes(int planes, int kdim);
 hipError_t launch_prefill_route(const Launch &L, const float *logits, int T, int E, int K,
                                 int32_t *ids, float *weights);
 hipError_t launch_prefill_group(const Launch &L, const int32_t *ids, int N, int E,

@@ -164,10 +164,39 @@ struct GemmArgs {
     float limit, alpha;
 };
 
-template <int PL> struct PrefillDepth { static constexpr int value = PL == 3 ? 3 : 4; };
+template <int PL> struct PrefillDepth { static constexpr int value = PL == 3 ? 2 : 4; };
+
+// Calls f(integral_constant<int, S>) for S = B .. E-1 in order.
+template <int B, int E> struct Unroll {
+    template <class F> __device__ __forceinline__ static void run(F &&f)
+    {
+        f(std::integral_constant<int, B>{});
+        Unroll<B + 1, E>::run(f);
+    }
+};
+template <int E> struct Unroll<E, E> {
+    template <class F> __device__ __forceinline__ static void run(F &&) {}
+};
 
 constexpr int kRowBytes = kKC * 32 * 2;       // one staged chunk row: 256 bf16
 constexpr int kPlaneBytes = kPT * kRowBytes;  // one staged plane of a chunk
+constexpr int kPrefillLdsMax = 160 * 1024;
+
+// LDS layout of one GEMM workgroup (byte offsets): the kPT entry ids, the
+// [depth][planes] staged activation chunks (also the output tile at the end),
+// a copy of the workgroup's kPF rows of scale bytes (whole 1 KiB DMA pieces
+// from a 16-byte aligned start, plus room for reads one dword past the last
+// byte), and the bias tile.
+struct PrefillLds { int ring, scales, bias, total; };
+__host__ __device__ inline PrefillLds prefill_lds(int planes, int depth, int nb)
+{
+    PrefillLds l;
+    l.ring = kPT * 4;
+    l.scales = l.ring + depth * planes * kPlaneBytes;
+    l.bias = l.scales + ((kPF * nb + 32 + 1023) & ~1023);
+    l.total = l.bias + 1024;
+    return l;
+}
 
 typedef __attribute__((address_space(3))) void l_void;
 
@@ -183,10 +212,17 @@ template <int N> __device__ __forceinline__ void wait_vmcnt()
 // compiler's own wait insertion treats any LDS read after an LDS-DMA as
 // possibly dependent on the newest DMA and would drain the whole pipeline;
 // the kernel orders DMA and reads itself (a counted vmcnt wait and a barrier
-// per chunk), and lds_settle waits for the reads before their values are used.
+// per chunk), and lds_wait for the reads before their values are used.
 __device__ __forceinline__ uint32_t lds_address(const void *p)
 {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+__device__ __forceinline__ uint32_t lds_read4(uint32_t addr)
+{
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
 }
 
 __device__ __forceinline__ bf16x8 lds_read16(uint32_t addr)
@@ -196,24 +232,35 @@ __device__ __forceinline__ bf16x8 lds_read16(uint32_t addr)
     return v;
 }
 
-__device__ __forceinline__ void lds_settle(bf16x8 &a, bf16x8 &b, bf16x8 &c, bf16x8 &d)
+// Waits until at most N of this wave's LDS reads are outstanding (they
+// complete in order); the caller then passes each register it reads through
+// an empty asm so that no use is scheduled above the wait.
+template <int N> __device__ __forceinline__ void lds_wait()
 {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+    static_assert(N >= 0 && N < 16, "lgkmcnt out of range");
+    if constexpr (N == 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    else if constexpr (N == 2) asm volatile("s_waitcnt lgkmcnt(2)" ::: "memory");
+    else if constexpr (N == 3) asm volatile("s_waitcnt lgkmcnt(3)" ::: "memory");
+    else if constexpr (N == 4) asm volatile("s_waitcnt lgkmcnt(4)" ::: "memory");
+    else static_assert(N == 0 || N == 2 || N == 3 || N == 4, "unsupported count");
 }
 
 template <int PL, bool GATE_UP>
 __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
 {
     constexpr int D = PrefillDepth<PL>::value;
-    constexpr int kNW = 5;                    // weight-ring loads per chunk (4 x 16 B + scales)
+    constexpr int kNW = 4;                    // weight-ring loads per chunk (4 x 16 B)
     constexpr int kNX = 2 * PL;               // LDS-DMA loads per chunk per wave
     // Loads a wave issues after a chunk's DMA until it waits for that DMA.
     constexpr int kYounger = kNW + (D - 2) * (kNX + kNW);
     // Dynamic LDS only (a static __shared__ variable would shift the dynamic
-    // area off its alignment): [kPT] entries, then the [D][PL] staged chunks.
+    // area off its alignment); layout in prefill_lds.
     extern __shared__ __align__(16) uint32_t plds[];
+    uint8_t *lds8 = reinterpret_cast<uint8_t *>(plds);
     int *ent = reinterpret_cast<int *>(plds);
-    uint8_t *xring = reinterpret_cast<uint8_t *>(plds + kPT);
+    const int nb = a.kdim >> 5;
+    const PrefillLds lay = prefill_lds(PL, D, nb);
+    uint8_t *xring = lds8 + lay.ring;
     const int item = blockIdx.y;
     if (item >= *a.ntiles) return;                    // uniform: the workgroup leaves
     const int te = a.tiles[item];
@@ -221,17 +268,39 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
     const int g0 = a.offsets[e] + m * kPT;
     const int ntok = min(kPT, a.offsets[e + 1] - g0);
     if (threadIdx.x < kPT) ent[threadIdx.x] = a.order[g0 + min((int)threadIdx.x, ntok - 1)];
-    __syncthreads();
 
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int h = lane >> 5, c = lane & 31;
-    const int fbase = blockIdx.x * kPF + wave * 32;
+    const int f0 = blockIdx.x * kPF;
+    const int fbase = f0 + wave * 32;
     const int row = min(fbase + c, a.fdim - 1);       // clamped: rows past fdim are never stored
-    const int nb = a.kdim >> 5;
     const uint8_t *ex = a.experts_base + (int64_t)e * a.stride;
     const uint8_t *wrow = ex + a.blocks_off + (int64_t)row * nb * 16;
-    const uint8_t *srow = ex + a.scales_off + (int64_t)row * nb;
+
+    __syncthreads();                                  // ent[] is written
+
+    // The workgroup's scale bytes (rows f0 .. f0+255 are contiguous in the
+    // scales section) and its bias tile, copied once by LDS-DMA in 1 KiB
+    // pieces from a 16-byte aligned start; reads past a section's end
+    // return zeros (buffer bounds).
+    const uint32_t s0 = (uint32_t)(f0 * nb) & ~15u;
+    const int sshift = f0 * nb - (int)s0;
+    {
+        const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(ex + a.scales_off), (short)0, a.fdim * nb, 0x00020000);
+        const int ninst = (sshift + kPF * nb + 1023) >> 10;
+        for (int k = wave; k < ninst; k += kPWaves)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(sres, (l_void *)(lds8 + lay.scales + k * 1024),
+                                                     16, s0 + k * 1024 + lane * 16, 0, 0, 0);
+        if (a.bias_dt >= 0 && wave == 0) {
+            const int esz = a.bias_dt == DT_F32 ? 4 : 2;
+            const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint8_t *>(ex + a.bias_off), (short)0, a.fdim * esz, 0x00020000);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (l_void *)(lds8 + lay.bias), 16,
+                                                     f0 * esz + lane * 16, 0, 0, 0);
+        }
+    }
 
     // Staging: wave w copies rows 4w .. 4w+3 of each plane, two rows per DMA
     // (lanes 0-31 row 4w+2n, lanes 32-63 the next); a lane's slot is lane & 31.
@@ -264,15 +333,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
         }
     };
 
-    // Weight ring: per chunk a lane's four 16-byte blocks (issued back to
-    // back, so each 128-byte line is fetched once) and their four scale bytes
-    // in one 4-byte load.  Block indices past nb clamp to the row's last
-    // block; the scale load stays inside the row (shifted so byte i is block
-    // base+i's scale while that block exists).
-    // The loaded words are used only when their chunk is multiplied (any
-    // arithmetic on them here would wait for the load just issued).
+    // Weight ring: per chunk a lane's four 16-byte blocks 4h .. 4h+3 (64
+    // contiguous bytes of its row).  Block indices past nb clamp to the row's
+    // last block.  The loaded words are used only when their chunk is
+    // multiplied (arithmetic on them here would wait for the load just issued).
     u32x4v wq[D][4];
-    uint32_t sq[D], sshift[D];
     auto wload = [&](int slot, int q) {
         const int base = q * kKC + 4 * h;
 #pragma unroll
@@ -280,59 +345,92 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
             const int bb = min(base + i, nb - 1);
             wq[slot][i] = *(g_u32x4v *)(wrow + (int64_t)bb * 16);
         }
-        const int off = min(base, nb - 4);
-        __builtin_memcpy(&sq[slot], srow + off, 4);
-        sshift[slot] = 8 * min(base - off, 3);
     };
 
-    f32x16 acc;
+    f32x16 acc, acc1;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    for (int i = 0; i < 16; ++i) {
+        acc[i] = 0.0f;
+        acc1[i] = 0.0f;
+    }
 
     // B read address of piece 16h + j for entry c: row c, slot (j ^ (c & 15)).
     const uint32_t rb = (uint32_t)(c * kRowBytes + 256 * h + ((c & 15) << 4));
     const uint32_t xbase = lds_address(xring);
+    // The lane's scale bytes for chunk q start at byte srel + 8q of the copy.
+    const uint32_t sbase = lds_address(lds8 + lay.scales);
+    const int srel = sshift + (row - f0) * nb + 4 * h;
 
     // Chunk q from ring slot / staging buffer s.  A block past nb is widened
-    // from a zero word with scale 1: exact zeros.
+    // from a zero word with scale 1: exact zeros.  The 16 MFMAs (m = 4i + d)
+    // run in groups of G whose B reads are issued one group ahead, and
+    // alternate between two accumulators so consecutive MFMAs are independent.
+    constexpr int G = PL == 1 ? 4 : PL == 2 ? 2 : 1;
+    constexpr int NG = 16 / G;
     auto multiply = [&](int q, auto s_const) {
         constexpr int s = decltype(s_const)::value;
         // Recomputed per chunk rather than kept in 16 registers per plane.
         uint32_t rbs = rb;
         asm volatile("" : "+v"(rbs));
+        bf16x8 B[2][G][PL];
+        auto read_group = [&](int g, bf16x8 (&dst)[G][PL]) {
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+                const uint32_t off = rbs ^ (uint32_t)((g * G + j) << 4);
+#pragma unroll
+                for (int p = 0; p < PL; ++p)
+                    dst[j][p] = lds_read16(xbase + (uint32_t)((s * PL + p) * kPlaneBytes) + off);
+            }
+        };
+        // The four scale bytes (blocks 4h .. 4h+3): two aligned dwords and a
+        // byte shift, read ahead of the first B group.
+        const uint32_t sb0 = sbase + (uint32_t)(srel + 8 * q);
+        uint32_t slo = lds_read4(sb0 & ~3u), shi = lds_read4((sb0 & ~3u) + 4);
+        read_group(0, B[0]);
+        lds_wait<G * PL>();
+        asm volatile("" : "+v"(slo), "+v"(shi));
+        const uint32_t sword = __builtin_amdgcn_alignbyte(shi, slo, sb0 & 3u);
+        // Bit masks rather than selects, so no branch separates a load from
+        // its use.
+        uint32_t keep[4];
+        float sc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            bf16x8 B[4][PL];
+            keep[i] = q * kKC + 4 * h + i < nb ? 0xFFFFFFFFu : 0u;
+            const uint32_t sb = (sword >> (8 * i)) & 0xFFu;
+            sc[i] = decode_scale(sb ^ ((sb ^ 127u) & ~keep[i]));
+        }
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                const uint32_t off = rbs ^ (uint32_t)((4 * i + d) << 4);
+        for (int g = 0; g < NG; ++g) {
+            if (g + 1 < NG) read_group(g + 1, B[(g + 1) & 1]);
+            bf16x8 A[G];
 #pragma unroll
-                for (int p = 0; p < PL; ++p)
-                    B[d][p] = lds_read16(xbase + (uint32_t)((s * PL + p) * kPlaneBytes) + off);
-            }
-            // Bit masks rather than selects, so no branch separates a load
-            // from its use.
-            const uint32_t keep = q * kKC + 4 * h + i < nb ? 0xFFFFFFFFu : 0u;
-            const uint32_t sb = (sq[s] >> (sshift[s] + 8 * i)) & 0xFFu;
-            const float sc = decode_scale(sb ^ ((sb ^ 127u) & ~keep));
-            bf16x8 A[4];
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                const uint32_t w = wq[s][i][d] & keep;
+            for (int j = 0; j < G; ++j) {
+                const int mm = g * G + j, i = mm >> 2, d = mm & 3;
+                const uint32_t w = wq[s][i][d] & keep[i];
                 const uint4 au = make_uint4(
-                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0)),
-                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1)),
-                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2)),
-                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3)));
-                A[d] = __builtin_bit_cast(bf16x8, au);
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 0)),
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 1)),
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 2)),
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 3)));
+                A[j] = __builtin_bit_cast(bf16x8, au);
             }
+            if (g + 1 < NG) lds_wait<G * PL>();
+            else lds_wait<0>();
 #pragma unroll
-            for (int p = 0; p < PL; ++p) lds_settle(B[0][p], B[1][p], B[2][p], B[3][p]);
+            for (int j = 0; j < G; ++j)
 #pragma unroll
-            for (int d = 0; d < 4; ++d)
+                for (int p = 0; p < PL; ++p) asm volatile("" : "+v"(B[g & 1][j][p]));
 #pragma unroll
-                for (int p = 0; p < PL; ++p)
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[d], B[d][p], acc, 0, 0, 0);
+            for (int j = 0; j < G; ++j) {
+#pragma unroll
+                for (int p = 0; p < PL; ++p) {
+                    if ((j * PL + p) & 1)
+                        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[j], B[g & 1][j][p], acc1, 0, 0, 0);
+                    else
+                        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[j], B[g & 1][j][p], acc, 0, 0, 0);
+                }
+            }
         }
     };
 
@@ -351,12 +449,14 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
         wait_vmcnt<kYounger>();
         // A bare barrier: a fenced one would also wait for every LDS-DMA in
         // flight.  Ordering is explicit here: the counted wait above for the
-        // DMA, and lds_settle for this wave's reads.
+        // DMA, and lds_wait for this wave's reads.
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
     };
 
     // nq rounded up to the ring depth: a padding chunk multiplies zero weights.
+    // The scale and bias copies are older than chunk 0's DMA, so the first
+    // counted wait covers them too.
     const int nq = (nb + kKC - 1) / kKC;
     const int nq_pad = (nq + D - 1) / D * D;
 #pragma unroll
@@ -368,62 +468,74 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
     wait_vmcnt<kYounger>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    for (int q = 0; q < nq_pad; q += D) {
-        step(q, std::integral_constant<int, 0>{});
-        step(q + 1, std::integral_constant<int, 1>{});
-        step(q + 2, std::integral_constant<int, 2>{});
-        if constexpr (D == 4) step(q + 3, std::integral_constant<int, 3>{});
-    }
-    // The DMAs of the padding chunks past nq_pad land before the workgroup's
-    // LDS is released.
+    for (int q = 0; q < nq_pad; q += D)
+        Unroll<0, D>::run([&](auto s_const) { step(q + decltype(s_const)::value, s_const); });
+    // Every DMA has landed (the padding chunks' too) and, after the barrier,
+    // no wave reads the staging ring any more: it holds the output tile next.
     wait_vmcnt<0>();
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] += acc1[i];
 
-    // Epilogue: lane holds entry column c, feature rows 8(v/4) + 4h + (v%4).
-    const bool col_ok = c < ntok;
-    const int entry = ent[c];
-    const uint8_t *bias = ex + a.bias_off;
-    // The lane's 16 bias values, loaded together before any is used.
+    // Epilogue: lane holds entry column c, feature rows 8(v/4) + 4h + (v%4)
+    // of the wave's 32; bias from the LDS tile.  The tile is written to LDS,
+    // then stored as 16-byte rows per entry.
     float bv[16];
-    {
-        uint32_t raw[16];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int r = min(fbase + 8 * (v >> 2) + 4 * h + (v & 3), a.fdim - 1);
-            raw[v] = a.bias_dt == DT_F32 ? reinterpret_cast<const uint32_t *>(bias)[r]
-                                         : (uint32_t)reinterpret_cast<const uint16_t *>(bias)[r];
-        }
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-            bv[v] = a.bias_dt < 0 ? 0.0f
-                    : a.bias_dt == DT_F32 ? __uint_as_float(raw[v])
-                    : a.bias_dt == DT_BF16 ? bf16_bits_to_f32((uint16_t)raw[v])
-                                           : f16_bits_to_f32((uint16_t)raw[v]);
+    for (int v = 0; v < 16; ++v) {
+        const int rl = wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        bv[v] = a.bias_dt < 0 ? 0.0f
+                : a.bias_dt == DT_F32 ? reinterpret_cast<const float *>(lds8 + lay.bias)[rl]
+                : a.bias_dt == DT_BF16
+                    ? bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(lds8 + lay.bias)[rl])
+                    : f16_bits_to_f32(reinterpret_cast<const uint16_t *>(lds8 + lay.bias)[rl]);
     }
     if constexpr (GATE_UP) {
-        const int half = a.fdim >> 1;
+        // [2 planes][kPT entries][kPF/2 activations] bf16
+        uint16_t *tile = reinterpret_cast<uint16_t *>(xring);
+        constexpr int kCols = kPF / 2;
 #pragma unroll
         for (int v = 0; v < 16; v += 2) {
-            const int r = fbase + 8 * (v >> 2) + 4 * h + (v & 3);   // even: gate, r+1: up
-            if (col_ok && r + 1 < a.fdim) {
-                const float gate = acc[v] + bv[v];
-                const float up = acc[v + 1] + bv[v + 1];
-                const float y = apply_activation(a.act_kind, gate, up, a.limit, a.alpha);
-                // The reference rounds the activation to fp16; it is kept as
-                // the exact sum of two bf16 planes for the down GEMM.
-                const float y16 = f16_bits_to_f32(f32_to_f16_bits(y));
-                const uint16_t hi = f32_to_bf16_bits(y16);
-                const uint16_t lo = f32_to_bf16_bits(y16 - bf16_bits_to_f32(hi));
-                const int64_t o = (int64_t)entry * half + (r >> 1);
-                a.act_out[o] = hi;
-                a.act_out[a.act_plane + o] = lo;
+            const int rl = wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3);   // even: gate, +1: up
+            const float y = apply_activation(a.act_kind, acc[v] + bv[v], acc[v + 1] + bv[v + 1],
+                                             a.limit, a.alpha);
+            // The reference rounds the activation to fp16; it is kept as the
+            // exact sum of two bf16 planes for the down GEMM.
+            const float y16 = f16_bits_to_f32(f32_to_f16_bits(y));
+            const uint16_t hi = f32_to_bf16_bits(y16);
+            tile[c * kCols + (rl >> 1)] = hi;
+            tile[(kPT + c) * kCols + (rl >> 1)] = f32_to_bf16_bits(y16 - bf16_bits_to_f32(hi));
+        }
+        __syncthreads();
+        const int half = a.fdim >> 1;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int idx = (int)threadIdx.x + k * kPThreads;
+            const int p = idx >> 9, t = (idx >> 4) & 31, piece = idx & 15;
+            const int col0 = (f0 >> 1) + piece * 8;
+            if (t < ntok && col0 + 8 <= half) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(tile + (p * kPT + t) * kCols + piece * 8);
+                *reinterpret_cast<uint4 *>(a.act_out + p * a.act_plane + (int64_t)ent[t] * half + col0) = v;
             }
         }
     } else {
+        // [kPT entries][kPF rows] fp32
+        float *tile = reinterpret_cast<float *>(xring);
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const int r = fbase + 8 * (v >> 2) + 4 * h + (v & 3);
-            if (col_ok && r < a.fdim)
-                a.y_out[(int64_t)entry * a.fdim + r] = acc[v] + bv[v];
+            const int rl = wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            tile[c * kPF + rl] = acc[v] + bv[v];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int idx = (int)threadIdx.x + k * kPThreads;
+            const int t = idx >> 6, piece = idx & 63;
+            const int row0 = f0 + piece * 4;
+            if (t < ntok && row0 + 4 <= a.fdim) {
+                const float4 v = *reinterpret_cast<const float4 *>(tile + t * kPF + piece * 4);
+                *reinterpret_cast<float4 *>(a.y_out + (int64_t)ent[t] * a.fdim + row0) = v;
+            }
         }
     }
 }
@@ -497,10 +609,12 @@ hipError_t launch_prefill_group(const Launch &L, const int32_t *ids, int N, int 
 
 int prefill_planes(int in_dt) { return in_dt == DT_BF16 ? 1 : in_dt == DT_F16 ? 2 : 3; }
 
-int prefill_gemm_lds_bytes(int planes)
+int prefill_gemm_lds_bytes(int planes, int kdim)
 {
-    const int depth = planes == 3 ? PrefillDepth<3>::value : PrefillDepth<1>::value;
-    return kPT * 4 + depth * planes * kPlaneBytes;
+    const int depth = planes == 1   ? PrefillDepth<1>::value
+                      : planes == 2 ? PrefillDepth<2>::value
+                                    : PrefillDepth<3>::value;
+    return prefill_lds(planes, depth, kdim / 32).total;
 }
 
 hipError_t launch_prefill_split(const Launch &L, const void *in, int in_dt, int64_t n,
@@ -525,6 +639,8 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
     if (g.kdim % 32 != 0 || g.kdim < 128 || g.fdim <= 0 || max_tiles <= 0)
         return hipErrorInvalidValue;
     if (planes < 1 || planes > 3 || (!gate_up && planes != 2)) return hipErrorInvalidValue;
+    // The output tile is stored 8 activations or 4 outputs at a time.
+    if ((gate_up && g.fdim % 16 != 0) || (!gate_up && g.fdim % 4 != 0)) return hipErrorInvalidValue;
     GemmArgs a;
     a.tiles = g.tiles;
     a.ntiles = g.ntiles;
@@ -551,7 +667,9 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
     a.limit = g.limit;
     a.alpha = g.alpha;
     const dim3 grid(pdiv_up(g.fdim, kPF), max_tiles);
-    const size_t lds = (size_t)prefill_gemm_lds_bytes(planes);
+    const int lds_bytes = prefill_gemm_lds_bytes(planes, g.kdim);
+    if (lds_bytes > kPrefillLdsMax) return hipErrorInvalidValue;   // K too wide for the staging
+    const size_t lds = (size_t)lds_bytes;
     hipError_t err = hipSuccess;
     auto go = [&](auto pl, auto gu) {
         constexpr int PL = decltype(pl)::value;
@@ -561,7 +679,7 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
         static bool lds_ok = false;
         if (!lds_ok) {
             err = hipFuncSetAttribute(reinterpret_cast<const void *>(&prefill_gemm_kernel<PL, GU>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kPrefillLdsMax);
             if (err != hipSuccess) return;
             lds_ok = true;
         }
