@@ -24,7 +24,7 @@ from typing import Dict, List, Optional, Sequence, Tuple, Union
 import numpy as np
 
 from ._lib import (ACT_GPTOSS_CLAMPED_GLU, ACT_SILU, BF16, F16, F32, SECTION_COUNT,
-                   AssignmentC, ExpertLayoutC, ExpertWeightsC, GodwitError, MoeLayerArgsC,
+                   AssignmentC, ExpertLayoutC, ExpertWeightsC, GodwitError, MoeBlockArgsC, MoeLayerArgsC,
                    check, lib)
 
 __all__ = [
@@ -395,6 +395,27 @@ class ExpertRunner:
                              router_bias, router_bias_dtype, out_bf16, routing_ids,
                              routing_weights)
         check(lib.gw_moe_prefill_forward(self.handle, ctypes.byref(a)))
+
+    def block_forward(self, experts_base: int, expert_stride: int, expert_count: int,
+                      top_k: int, tokens: int, stream: int, norm_weight: int,
+                      epsilon: float, norm_weight_dtype: int = BF16, logits: int = 0,
+                      router_weight: int = 0, router_weight_dtype: int = BF16,
+                      router_bias: int = 0, router_bias_dtype: int = BF16,
+                      out_bf16: int = 0, routing_ids: int = 0,
+                      routing_weights: int = 0) -> None:
+        """The MoE block with its surroundings (TransformerLayer.swift:140-143 and
+        232-238): stream += MoE(RMSNorm(stream)), stream fp32 [tokens, hidden] updated in
+        place; the router (when logits is 0) sees the normalised rows.  Enqueue only."""
+        b = MoeBlockArgsC()
+        b.layer = self._layer_args(experts_base, expert_stride, expert_count, top_k, 0, F16,
+                                   tokens, 0, logits, router_weight, router_weight_dtype,
+                                   router_bias, router_bias_dtype, out_bf16, routing_ids,
+                                   routing_weights)
+        b.stream = stream
+        b.norm_weight = norm_weight
+        b.norm_weight_dtype = norm_weight_dtype
+        b.epsilon = epsilon
+        check(lib.gw_moe_block_forward(self.handle, ctypes.byref(b)))
 
     def reserve_prefill(self, max_tokens: int, top_k: int, expert_count: int) -> None:
         """Sizes the prefill scratch up front (required before capturing a graph)."""

@@ -47,6 +47,11 @@ class MoeLayerArgsC(ctypes.Structure):
                 ("routing_ids", _P), ("routing_weights", _P)]
 
 
+class MoeBlockArgsC(ctypes.Structure):
+    _fields_ = [("layer", MoeLayerArgsC), ("stream", _P), ("norm_weight", _P),
+                ("norm_weight_dtype", _I), ("epsilon", ctypes.c_float)]
+
+
 # name -> (restype, argtypes).  This table is also the list of exported
 # symbols the CPU tests check against include/godwit_hip.h.
 SIGNATURES = {
@@ -91,6 +96,7 @@ SIGNATURES = {
     "gw_expert_apply_assignments_async": (_I, [_P, _P, _I, _P, _I32, _P]),
     "gw_moe_layer_forward": (_I, [_P, ctypes.POINTER(MoeLayerArgsC)]),
     "gw_moe_prefill_forward": (_I, [_P, ctypes.POINTER(MoeLayerArgsC)]),
+    "gw_moe_block_forward": (_I, [_P, ctypes.POINTER(MoeBlockArgsC)]),
     "gw_graph_begin_capture": (_I, [_P]),
     "gw_graph_end_capture": (_I, [_P, ctypes.POINTER(_P)]),
     "gw_graph_launch": (_I, [_P]),

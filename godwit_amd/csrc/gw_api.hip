@@ -551,6 +551,7 @@ struct gw_expert_runner {
     Plan *plans = nullptr;           // [kPlanRing] host-built plans
     Plan *route_plan = nullptr;      // device-built plan of gw_moe_layer_forward
     uint16_t *act_buf = nullptr;     // [kMaxSlots, inter] fp16 activations
+    uint16_t *normed_buf = nullptr;  // [kMaxTokens, hidden] fp16 RMSNorm output
     float *logits = nullptr;         // [kMaxTokens, kMaxExperts]
     Plan *staging = nullptr;         // pinned host mirror of `plans`
     unsigned *sync_buf = nullptr;    // fused layer exchange: counters | epochs | error word
@@ -580,6 +581,7 @@ extern "C" int gw_expert_runner_destroy(gw_expert_runner *r)
     (void)hipFree(r->plans);
     (void)hipFree(r->route_plan);
     (void)hipFree(r->act_buf);
+    (void)hipFree(r->normed_buf);
     (void)hipFree(r->logits);
     (void)hipHostFree(r->staging);
     (void)hipFree(r->sync_buf);
@@ -617,6 +619,8 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     if (e == hipSuccess) e = hipMalloc((void **)&r->route_plan, sizeof(Plan));
     if (e == hipSuccess)
         e = hipMalloc((void **)&r->act_buf, sizeof(uint16_t) * gw::kMaxSlots * intermediate_size);
+    if (e == hipSuccess)
+        e = hipMalloc((void **)&r->normed_buf, sizeof(uint16_t) * gw::kMaxTokens * hidden_size);
     if (e == hipSuccess)
         e = hipMalloc((void **)&r->logits, sizeof(float) * gw::kMaxTokens * kMaxExperts);
     if (e == hipSuccess) e = hipHostMalloc((void **)&r->staging, sizeof(Plan) * kPlanRing);
@@ -928,10 +932,13 @@ extern "C" int gw_expert_apply_assignments(gw_expert_runner *r, const void *inpu
 // MoE layer (device-routed)
 // ---------------------------------------------------------------------------
 
-extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args *a)
+// out_mode 0: out = MoE output; 2: out += MoE output (the residual add).
+static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int out_mode);
+
+static int moe_layer_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int out_mode)
 {
     GW_CHECK(r && a, GW_ERR_ARG, "null argument");
-    if (a->tokens > gw::kMaxTokens) return gw_moe_prefill_forward(r, a);
+    if (a->tokens > gw::kMaxTokens) return moe_prefill_impl(r, a, out_mode);
     GW_CHECK(a->tokens >= 1, GW_ERR_SHAPE, "tokens must be positive (got %d)", a->tokens);
     GW_CHECK(a->expert_count >= 1 && a->expert_count <= kMaxExperts, GW_ERR_SHAPE,
              "expert_count %lld out of range", (long long)a->expert_count);
@@ -970,7 +977,7 @@ extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args
     const gw::Sections sec = sections_of(r->offsets);
     // One token: the whole layer in one kernel when the shape and the
     // occupancy allow it.
-    if (a->tokens == 1 && r->fused_enabled) {
+    if (a->tokens == 1 && r->fused_enabled && out_mode == 0) {
         const int grid = gw::fused_layer_grid(L, (int)r->hidden, (int)r->inter, a->x_dtype,
                                               (int)a->top_k, (int)a->expert_count);
         if (grid > 0 && grid <= kSyncEpochWords) {
@@ -998,9 +1005,14 @@ extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args
         ProfScope ps(ctx, "down");
         GW_HIP(gw::launch_down(ps.launch(L), r->route_plan, a->tokens, (int)(a->tokens * a->top_k), r->act_buf,
                                (int)r->hidden, (int)r->inter, sec, r->bias_dt, a->out,
-                               a->out_bf16, 0));
+                               a->out_bf16, out_mode));
     }
     return GW_OK;
+}
+
+extern "C" int gw_moe_layer_forward(gw_expert_runner *r, const gw_moe_layer_args *a)
+{
+    return moe_layer_impl(r, a, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1013,6 +1025,7 @@ struct PrefillScratch {
     int32_t *ids;
     float *weights;
     int32_t *offsets, *order, *tiles, *ntiles;
+    uint16_t *normed;   // [T, hidden] fp16 RMSNorm output (gw_moe_block_forward)
     uint16_t *xsplit;   // [planes][T, hidden] bf16 planes of a fp16 or fp32 x
     uint16_t *act;      // [2][N, inter] bf16 planes of the fp16 activations
     float *y;
@@ -1040,6 +1053,7 @@ size_t prefill_layout(const gw_expert_runner *r, int T, int K, int E, char *base
     s.order = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * N));
     s.tiles = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * tiles));
     s.ntiles = reinterpret_cast<int32_t *>(take(sizeof(int32_t)));
+    s.normed = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * (size_t)T * r->hidden));
     s.xsplit = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * 3 * (size_t)T * r->hidden));
     s.act = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * 2 * N * r->inter));
     s.y = reinterpret_cast<float *>(take(sizeof(float) * N * r->hidden));
@@ -1076,7 +1090,7 @@ extern "C" int gw_expert_runner_reserve_prefill(gw_expert_runner *r, int32_t max
     return GW_OK;
 }
 
-extern "C" int gw_moe_prefill_forward(gw_expert_runner *r, const gw_moe_layer_args *a)
+static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int out_mode)
 {
     GW_CHECK(r && a, GW_ERR_ARG, "null argument");
     GW_CHECK(a->tokens >= 1, GW_ERR_SHAPE, "tokens must be positive (got %d)", a->tokens);
@@ -1172,7 +1186,7 @@ extern "C" int gw_moe_prefill_forward(gw_expert_runner *r, const gw_moe_layer_ar
     {
         ProfScope p(ctx, "prefill_combine");
         GW_HIP(gw::launch_prefill_combine(p.launch(L), ps.y, ps.weights, T, K, (int)r->hidden,
-                                          a->out, a->out_bf16));
+                                          a->out, a->out_bf16, out_mode == 2 ? 1 : 0));
     }
     if (a->routing_ids)
         GW_HIP(hipMemcpyAsync(a->routing_ids, ps.ids, sizeof(int32_t) * T * K,
@@ -1181,6 +1195,49 @@ extern "C" int gw_moe_prefill_forward(gw_expert_runner *r, const gw_moe_layer_ar
         GW_HIP(hipMemcpyAsync(a->routing_weights, ps.weights, sizeof(float) * T * K,
                               hipMemcpyDeviceToDevice, ctx->stream));
     return GW_OK;
+}
+
+extern "C" int gw_moe_prefill_forward(gw_expert_runner *r, const gw_moe_layer_args *a)
+{
+    return moe_prefill_impl(r, a, 0);
+}
+
+// ---------------------------------------------------------------------------
+// the MoE block with its surroundings: RMSNorm before, residual add after
+// ---------------------------------------------------------------------------
+
+extern "C" int gw_moe_block_forward(gw_expert_runner *r, const gw_moe_block_args *b)
+{
+    GW_CHECK(r && b, GW_ERR_ARG, "null argument");
+    GW_CHECK(b->stream && b->norm_weight, GW_ERR_ARG, "null stream or norm weight");
+    GW_CHECK(b->norm_weight_dtype == GW_BF16 || b->norm_weight_dtype == GW_F32, GW_ERR_ARG,
+             "norm weight must be bf16 or fp32");
+    GW_CHECK(b->epsilon >= 0.0f, GW_ERR_ARG, "epsilon must be non-negative");
+    const int T = b->layer.tokens;
+    GW_CHECK(T >= 1, GW_ERR_SHAPE, "tokens must be positive (got %d)", T);
+    gw_context *ctx = r->ctx;
+    uint16_t *normed = r->normed_buf;
+    if (T > gw::kMaxTokens) {
+        // The batched path: normalised rows live in the prefill scratch.
+        int rc = gw_expert_runner_reserve_prefill(r, T, (int)b->layer.top_k,
+                                                  (int)b->layer.expert_count);
+        if (rc) return rc;
+        PrefillScratch ps;
+        prefill_layout(r, r->pf_tokens, r->pf_topk, r->pf_experts,
+                       static_cast<char *>(r->pf_buf), &ps);
+        normed = ps.normed;
+    }
+    const gw::Launch L = launch_of(ctx);
+    {
+        ProfScope ps(ctx, "rmsnorm");
+        GW_HIP(gw::launch_rmsnorm(ps.launch(L), b->stream, b->norm_weight, b->norm_weight_dtype,
+                                  T, (int)r->hidden, b->epsilon, normed));
+    }
+    gw_moe_layer_args a = b->layer;
+    a.x = normed;
+    a.x_dtype = GW_F16;
+    a.out = b->stream;
+    return moe_layer_impl(r, &a, 2);
 }
 
 // ---------------------------------------------------------------------------

@@ -586,11 +586,15 @@ __global__ __launch_bounds__(kNT) void down_kernel(
         const int t = p / n;
         const int q = p - t * n;
         const int64_t o = (int64_t)plan->tok_global[t] * hidden + r0 + q;
-        float dst = accumulate ? out[o] : 0.0f;
+        // accumulate: 0 overwrite; 1 continue the sum from out (applyAssignments);
+        // 2 the residual add after the block, out += finished sum
+        // (TransformerLayer.swift:232-238).
+        float dst = accumulate == 1 ? out[o] : 0.0f;
         for (int k = 0; k < plan->tok_nslots[t]; ++k) {
             const int s = plan->tok_slots[t][k];
             dst = add_scaled_rn(dst, vals[s * nmax + q], plan->slot_weight[s]);
         }
+        if (accumulate == 2) dst = out[o] + dst;
         out[o] = dst;
         if (out_bf16) out_bf16[o] = f32_to_bf16_bits(dst);
     }
@@ -899,6 +903,31 @@ __global__ __launch_bounds__(256) void activation_kernel(int kind,
                                               limit, alpha));
 }
 
+// Post-attention RMSNorm of fp32 residual-stream rows to the fp16 MoE input
+// (TransformerLayer.normalise, TransformerLayer.swift:265-285; rmsnorm,
+// router.metal:36-60): one workgroup per row, the sum of squares as a
+// workgroup tree in fp32, inverse = 1 / sqrt(sum / width + eps) (correctly
+// rounded), out = fp16((x * inverse) * weight).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x,
+                                                      const void *__restrict__ weight, int w_dt,
+                                                      int width, float eps,
+                                                      uint16_t *__restrict__ out)
+{
+    __shared__ float partial[4];
+    const float *row = x + (int64_t)blockIdx.x * width;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < width; i += 256) ss += row[i] * row[i];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    const float inverse = 1.0f / sqrtf(total / (float)width + eps);
+    uint16_t *dst = out + (int64_t)blockIdx.x * width;
+    for (int i = threadIdx.x; i < width; i += 256)
+        dst[i] = f32_to_f16_bits((row[i] * inverse) * load_as_f32(weight, w_dt, i));
+}
+
 __global__ __launch_bounds__(256) void accumulate_kernel(const float *__restrict__ src,
                                                          float *__restrict__ dst, float w,
                                                          int64_t width)
@@ -1201,6 +1230,14 @@ hipError_t launch_activation(const Launch &L, int kind, const float *gate_up, ui
     if (width == 0) return hipSuccess;
     GW_LAUNCH(activation_kernel, dim3(div_up(width, 256)), dim3(256), 0, L, kind, gate_up, out,
               width, limit, alpha);
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const Launch &L, const float *x, const void *weight, int w_dt,
+                          int rows, int width, float eps, uint16_t *out)
+{
+    if (rows <= 0 || width <= 0) return hipErrorInvalidValue;
+    GW_LAUNCH(rmsnorm_kernel, dim3(rows), dim3(256), 0, L, x, weight, w_dt, width, eps, out);
     return hipGetLastError();
 }
 

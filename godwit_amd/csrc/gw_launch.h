@@ -47,6 +47,8 @@ hipError_t launch_gemv(const Launch &L, const uint8_t *packed, const uint8_t *sc
                        int rows, int cols);
 hipError_t launch_activation(const Launch &L, int kind, const float *gate_up, uint16_t *out,
                              int64_t width, float limit, float alpha);
+hipError_t launch_rmsnorm(const Launch &L, const float *x, const void *weight, int w_dt,
+                          int rows, int width, float eps, uint16_t *out);
 hipError_t launch_accumulate(const Launch &L, const float *src, float *dst, float w,
                              int64_t width);
 hipError_t launch_router(const Launch &L, const void *W, int w_dt, const void *b, int b_dt,
@@ -101,7 +103,7 @@ hipError_t launch_prefill_split(const Launch &L, const void *in, int in_dt, int6
 hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const PrefillGemm &g,
                                int max_tiles);
 hipError_t launch_prefill_combine(const Launch &L, const float *y, const float *w, int T, int K,
-                                  int H, float *out, uint16_t *out_bf16);
+                                  int H, float *out, uint16_t *out_bf16, int residual);
 
 hipError_t launch_fill_u8(const Launch &L, void *dst, size_t count, int lo, int hi,
                           uint64_t seed);

@@ -561,14 +561,17 @@ __global__ __launch_bounds__(256) void prefill_split_kernel(const void *__restri
 
 // ---------------------------------------------------------------------------
 // 5. Combine: out[t] = sum_k w[t,k] * y[t*K+k], product and sum rounded
-// separately in router order (expert_accumulate), starting from zero.
+// separately in router order (expert_accumulate), starting from zero; with
+// `residual` the finished sum is added to out (the residual add after the
+// block, TransformerLayer.swift:232-238).
 // ---------------------------------------------------------------------------
 
 __global__ __launch_bounds__(256) void prefill_combine_kernel(const float *__restrict__ y,
                                                               const float *__restrict__ w,
                                                               int T, int K, int H,
                                                               float *__restrict__ out,
-                                                              uint16_t *__restrict__ out_bf16)
+                                                              uint16_t *__restrict__ out_bf16,
+                                                              int residual)
 {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)T * H) return;
@@ -576,6 +579,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const float *__res
     float dst = 0.0f;
     for (int k = 0; k < K; ++k)
         dst = add_scaled_rn(dst, y[((int64_t)t * K + k) * H + col], w[(int64_t)t * K + k]);
+    if (residual) dst = out[i] + dst;
     out[i] = dst;
     if (out_bf16) out_bf16[i] = f32_to_bf16_bits(dst);
 }
@@ -702,10 +706,10 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
 }
 
 hipError_t launch_prefill_combine(const Launch &L, const float *y, const float *w, int T, int K,
-                                  int H, float *out, uint16_t *out_bf16)
+                                  int H, float *out, uint16_t *out_bf16, int residual)
 {
     GW_LAUNCH(prefill_combine_kernel, dim3(pdiv_up((int64_t)T * H, 256)), dim3(256), 0, L, y, w,
-              T, K, H, out, out_bf16);
+              T, K, H, out, out_bf16, residual);
     return hipGetLastError();
 }
 

@@ -282,6 +282,26 @@ int gw_expert_runner_reserve_prefill(gw_expert_runner *runner, int32_t max_token
                                      int32_t expert_count);
 int gw_moe_prefill_forward(gw_expert_runner *runner, const gw_moe_layer_args *args);
 
+/* The MoE block with the steps either side of it (TransformerLayer.forward,
+ * TransformerLayer.swift:140-143 and 232-238): normed = RMSNorm(stream) in fp16
+ * (TransformerLayer.normalise, :265-285; rmsnorm, router.metal:36-60: the sum
+ * of squares in fp32, x * rsqrt(mean + eps) * weight), then the block of
+ * gw_moe_layer_forward on `normed` (the router, when logits is NULL, sees it
+ * too), then stream += the combined expert output, in fp32, the sum finished
+ * before it is added.  `layer.x`, `layer.x_dtype` and `layer.out` are ignored;
+ * `layer.out_bf16`, when set, receives a bf16 copy of the updated stream.
+ * Batches above 8 tokens take the prefill path (reserve it before capture).
+ * Enqueue only. */
+typedef struct gw_moe_block_args {
+    gw_moe_layer_args layer;
+    float *stream;                    /* [tokens, hidden] fp32 residual stream, in place */
+    const void *norm_weight;          /* [hidden] post-attention norm weight */
+    gw_dtype norm_weight_dtype;       /* GW_BF16 (the .gwt trunk) or GW_F32 */
+    float epsilon;                    /* ArchitectureSpec.rmsNormEpsilon (1e-5 GPT-OSS) */
+} gw_moe_block_args;
+
+int gw_moe_block_forward(gw_expert_runner *runner, const gw_moe_block_args *args);
+
 /* For one token (the decode step of a single sequence) the layer above can
  * run as ONE kernel whose workgroups exchange the activations through device
  * memory (enabled by GODWIT_FUSED_LAYER=1 in the environment when the runner

@@ -57,6 +57,8 @@ def _load() -> ctypes.CDLL:
         "gwo_swiglu_f32": (_F, [_F, _F]),
         "gwo_activation": (None, [ctypes.c_int, _P, _P, _I64, _F, _F]),
         "gwo_accumulate": (None, [_P, _P, _F, _I64]),
+        "gwo_rmsnorm_f16": (None, [_P, _P, _I64, _F, _P]),
+        "gwo_residual_add": (None, [_P, _P, _I64]),
         "gwo_router_logits": (None, [_P, _P, _P, _P, _I64, _I64]),
         "gwo_router_select": (None, [_P, _I64, _I64, _P, _P]),
         "gwo_expert_apply": (None, [_P, _P, _P, _I64, _I64, ctypes.c_int, _F, _F]),
@@ -181,6 +183,22 @@ def accumulate(expert_out, dst, weight: float) -> np.ndarray:
     o, d = _c(expert_out, np.float32), _c(dst, np.float32).copy()
     _lib.gwo_accumulate(_ptr(o), _ptr(d), weight, o.size)
     return d
+
+
+def rmsnorm_f16(x, weight_bf16, eps: float) -> np.ndarray:
+    """fp16 bits of RMSNorm(x) per row of a [T, width] fp32 array (bf16 weight bits)."""
+    x = _c(np.atleast_2d(x), np.float32)
+    w = _c(weight_bf16, np.uint16)
+    out = np.empty(x.shape, np.uint16)
+    for t in range(x.shape[0]):
+        _lib.gwo_rmsnorm_f16(_ptr(x[t]), _ptr(w), x.shape[1], eps, _ptr(out[t]))
+    return out
+
+
+def residual_add(stream, combined) -> np.ndarray:
+    s, c = _c(stream, np.float32).copy(), _c(combined, np.float32)
+    _lib.gwo_residual_add(_ptr(s), _ptr(c), s.size)
+    return s
 
 
 def router_logits(weight, bias, x, experts: int, hidden: int) -> np.ndarray:

@@ -262,6 +262,33 @@ void gwo_accumulate(const float *expert_out, float *dst, float weight, int64_t w
     for (int64_t i = 0; i < width; ++i) dst[i] += expert_out[i] * weight;
 }
 
+/* ---- around the MoE block ------------------------------------------------ */
+
+/* Post-attention RMSNorm of one token's fp32 residual-stream row to the fp16
+ * MoE input — TransformerLayer.normalise, TransformerLayer.swift:265-285: the
+ * sum of squares in element order, inverse = 1 / sqrt(sum / width + eps), then
+ * out[i] = Float16(value * inverse * weight) with the bf16 weight widened and
+ * the two products taken left to right (router.metal:36-60 is the same formula
+ * on the GPU, with a SIMD-tree sum). */
+void gwo_rmsnorm_f16(const float *x, const uint16_t *weight_bf16, int64_t width, float eps,
+                     uint16_t *out_f16)
+{
+    float sum_squares = 0.0f;
+    for (int64_t i = 0; i < width; ++i) sum_squares += x[i] * x[i];
+    const float inverse = 1.0f / sqrtf(sum_squares / (float)width + eps);
+    for (int64_t i = 0; i < width; ++i) {
+        const float v = x[i] * inverse;
+        out_f16[i] = gwo_f32_to_f16(v * gwo_bf16_to_f32(weight_bf16[i]));
+    }
+}
+
+/* The residual add after the block — TransformerLayer.swift:232-238:
+ * stream[i] += combined[i] in fp32. */
+void gwo_residual_add(float *stream, const float *combined, int64_t count)
+{
+    for (int64_t i = 0; i < count; ++i) stream[i] += combined[i];
+}
+
 /* ---- router ------------------------------------------------------------ */
 
 /* bf16_gemv_bias — Sources/Godwit/Metal/MoE/router.metal:18-34 (weights and

@@ -53,6 +53,11 @@ void  gwo_activation(int kind, const float *gate_up, uint16_t *out_f16, int64_t 
 void  gwo_accumulate(const float *expert_out, float *dst, float weight, int64_t width);
 
 /* ---- router ------------------------------------------------------------ */
+/* around the MoE block */
+void gwo_rmsnorm_f16(const float *x, const uint16_t *weight_bf16, int64_t width, float eps,
+                     uint16_t *out_f16);
+void gwo_residual_add(float *stream, const float *combined, int64_t count);
+
 void gwo_router_logits(const float *weight, const float *bias, const float *x, float *logits,
                        int64_t experts, int64_t hidden);
 void gwo_router_select(const float *logits, int64_t experts, int64_t top_k,

@@ -375,3 +375,62 @@ def test_moe_layer_composition():
     acc = oracle.apply_assignments(es, assigns, x, np.zeros((T, hidden), np.float32), hidden,
                                    inter)
     assert np.array_equal(acc, out)
+
+
+# ---- around the MoE block: RMSNorm and the residual add --------------------
+
+def _f16_ulp_diff(a_bits, b_bits):
+    """Distance in fp16 ulps between finite fp16 bit patterns (sign-aware)."""
+    def key(b):
+        b = np.asarray(b, np.int32)
+        return np.where(b & 0x8000, -(b & 0x7FFF), b & 0x7FFF)
+    return np.abs(key(a_bits) - key(b_bits))
+
+
+def test_rmsnorm_against_float64_closed_form():
+    """x / sqrt(mean(x^2) + eps) * w (layer_reference.py's rms_norm), in fp64, rounded
+    once to fp16: the oracle's fp32 evaluation differs by at most one fp16 ulp.  A
+    dropped mean (sum instead), eps outside the root or a missing weight all miss."""
+    r = rng(41)
+    for width, eps in ((2880, 1e-5), (2048, 1e-6), (64, 1e-5)):
+        x = (r.standard_normal((3, width)) * np.array([[0.5], [2.0], [30.0]])).astype(np.float32)
+        wbits = oracle.f32_to_bf16_bits((1.0 + 0.1 * r.standard_normal(width)).astype(np.float32))
+        w = oracle.bf16_bits_to_f32(wbits).astype(np.float64)
+        got = oracle.rmsnorm_f16(x, wbits, eps)
+        x64 = x.astype(np.float64)
+        ref = x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + eps) * w
+        assert _f16_ulp_diff(got, oracle.f32_to_f16_bits(ref.astype(np.float32)).reshape(got.shape)).max() <= 1
+
+
+def test_rmsnorm_invariants_and_known_answers():
+    # constant row c: every output is fp16(c / sqrt(c^2 + eps)) times the weight
+    width = 2880
+    ones = oracle.f32_to_bf16_bits(np.ones(width, np.float32))
+    out = oracle.rmsnorm_f16(np.full((1, width), 3.0, np.float32), ones, 0.0)
+    assert np.all(out == oracle.f32_to_f16_bits(np.float32(1.0)))
+    # scale invariance (eps negligible): c * x normalises like x
+    r = rng(42)
+    x = r.standard_normal((1, width)).astype(np.float32)
+    a = oracle.rmsnorm_f16(x, ones, 1e-30)
+    b = oracle.rmsnorm_f16(np.float32(8.0) * x, ones, 1e-30)
+    assert np.array_equal(a, b)                      # a power of two scales exactly
+    # eps dominates for a tiny row, and a zero row stays zero (no NaN)
+    tiny = np.full((1, width), 1e-6, np.float32)
+    t = oracle.rmsnorm_f16(tiny, ones, 1e-2)
+    expect = np.float32(1e-6) / np.sqrt(np.float32(1e-12) + np.float32(1e-2))
+    assert _f16_ulp_diff(t[0], oracle.f32_to_f16_bits(np.full(width, expect, np.float32))).max() <= 1
+    assert np.all(oracle.rmsnorm_f16(np.zeros((1, width), np.float32), ones, 1e-5) == 0)
+    # the weight applies per element: a one-hot weight keeps only that element
+    for i in (0, 17, width - 1):
+        w = np.zeros(width, np.float32)
+        w[i] = 1.0
+        o = oracle.rmsnorm_f16(x, oracle.f32_to_bf16_bits(w), 1e-5)[0]
+        nz = np.nonzero(o & 0x7FFF)[0]
+        assert list(nz) == [i]
+
+
+def test_residual_add_is_fp32_elementwise():
+    r = rng(43)
+    s = r.standard_normal(1000).astype(np.float32)
+    c = r.standard_normal(1000).astype(np.float32)
+    assert np.array_equal(oracle.residual_add(s, c), s + c)
