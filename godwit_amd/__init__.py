@@ -18,13 +18,14 @@ package fails when the library has not been built.
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence, Tuple, Union
 
 import numpy as np
 
 from ._lib import (ACT_GPTOSS_CLAMPED_GLU, ACT_SILU, BF16, F16, F32, SECTION_COUNT,
-                   AssignmentC, ExpertLayoutC, ExpertWeightsC, GodwitError, MoeBlockArgsC, MoeLayerArgsC,
+                   AssignmentC, ExpertLayoutC, ExpertWeightsC, GodwitError, ModelInfoC, MoeBlockArgsC, MoeLayerArgsC,
                    check, lib)
 
 __all__ = [
@@ -237,6 +238,64 @@ class ExpertLayout:
 
     def offsets_array(self):
         return [self.offsets[s] for s in SECTIONS]
+
+
+SECTION_NAMES = ("gate_up_blocks", "gate_up_scales", "down_blocks", "down_scales",
+                 "gate_up_bias", "down_bias")
+
+
+class ModelReader:
+    """A .gwt installation (ModelReader, Runtime/ModelReader.swift:11-111): the manifest's
+    counts, stride, sections and the MoE spec fields, and its expert layer files read
+    into device memory with unchanged bytes."""
+
+    def __init__(self, directory: str):
+        h = ctypes.c_void_p()
+        check(lib.gw_model_open(os.fsencode(directory), ctypes.byref(h)))
+        self.handle = h.value
+        info = ModelInfoC()
+        check(lib.gw_model_info_get(self.handle, ctypes.byref(info)))
+        self.format_version = info.format_version
+        self.layer_count = info.layer_count
+        self.expert_count = info.expert_count
+        self.expert_stride = info.expert_stride
+        self.sections = {n: (info.section_offset[i], info.section_length[i])
+                         for i, n in enumerate(SECTION_NAMES)}
+        self.hidden_size = info.hidden_size
+        self.intermediate_size = info.intermediate_size
+        self.experts_per_token = info.experts_per_token
+        self.rms_norm_epsilon = info.rms_norm_epsilon
+        self.activation = ("gptOssClampedGLU", "silu")[info.activation]
+        self.activation_limit = info.activation_limit
+        self.activation_alpha = info.activation_alpha
+        self.expert_bias = bool(info.expert_bias)
+        self.router_bias = bool(info.router_bias)
+
+    @property
+    def layer_file_size(self) -> int:
+        return self.expert_stride * self.expert_count
+
+    def validate(self) -> None:
+        """GodwitManifest.validate: every layer file has the size the manifest implies."""
+        check(lib.gw_model_validate(self.handle))
+
+    def load_layer(self, ctx: "Context", layer: int) -> "DeviceBuffer":
+        """Layer `layer`'s expert file, resident on the device (the experts_base of
+        layer_forward)."""
+        buf = ctx.empty(self.layer_file_size)
+        check(lib.gw_model_load_layer(ctx.handle, self.handle, layer, buf.ptr, buf.nbytes))
+        return buf
+
+    def load_expert(self, ctx: "Context", layer: int, expert: int) -> "DeviceBuffer":
+        """One expert stride, all six sections (ModelReader.loadExpertStride)."""
+        buf = ctx.empty(self.expert_stride)
+        check(lib.gw_model_load_expert(ctx.handle, self.handle, layer, expert, buf.ptr))
+        return buf
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib.gw_model_close(self.handle))
+            self.handle = None
 
 
 @dataclass

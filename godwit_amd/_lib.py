@@ -47,6 +47,16 @@ class MoeLayerArgsC(ctypes.Structure):
                 ("routing_ids", _P), ("routing_weights", _P)]
 
 
+class ModelInfoC(ctypes.Structure):
+    _fields_ = [("format_version", _I64), ("layer_count", _I64), ("expert_count", _I64),
+                ("expert_stride", _I64), ("section_offset", _I64 * 6),
+                ("section_length", _I64 * 6), ("hidden_size", _I64),
+                ("intermediate_size", _I64), ("experts_per_token", _I64),
+                ("rms_norm_epsilon", ctypes.c_float), ("activation_limit", ctypes.c_float),
+                ("activation_alpha", ctypes.c_float), ("activation", _I),
+                ("expert_bias", _I32), ("router_bias", _I32)]
+
+
 class MoeBlockArgsC(ctypes.Structure):
     _fields_ = [("layer", MoeLayerArgsC), ("stream", _P), ("norm_weight", _P),
                 ("norm_weight_dtype", _I), ("epsilon", ctypes.c_float)]
@@ -97,6 +107,12 @@ SIGNATURES = {
     "gw_moe_layer_forward": (_I, [_P, ctypes.POINTER(MoeLayerArgsC)]),
     "gw_moe_prefill_forward": (_I, [_P, ctypes.POINTER(MoeLayerArgsC)]),
     "gw_moe_block_forward": (_I, [_P, ctypes.POINTER(MoeBlockArgsC)]),
+    "gw_model_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "gw_model_close": (_I, [_P]),
+    "gw_model_info_get": (_I, [_P, ctypes.POINTER(ModelInfoC)]),
+    "gw_model_validate": (_I, [_P]),
+    "gw_model_load_layer": (_I, [_P, _P, _I32, _P, ctypes.c_size_t]),
+    "gw_model_load_expert": (_I, [_P, _P, _I32, _I32, _P]),
     "gw_graph_begin_capture": (_I, [_P]),
     "gw_graph_end_capture": (_I, [_P, ctypes.POINTER(_P)]),
     "gw_graph_launch": (_I, [_P]),

@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "../../include/godwit_hip.h"
+#include "gw_error.h"
 #include "gw_launch.h"
 #include "gw_plan.h"
 
@@ -27,7 +28,7 @@ using gw::Plan;
 
 static thread_local std::string g_error;
 
-static int fail(int code, const char *fmt, ...)
+int gw::set_error(int code, const char *fmt, ...)
 {
     char buf[512];
     va_list ap;
@@ -37,6 +38,8 @@ static int fail(int code, const char *fmt, ...)
     g_error = buf;
     return code;
 }
+
+#define fail gw::set_error
 
 #define GW_HIP(call)                                                                     \
     do {                                                                                 \

@@ -282,6 +282,48 @@ int gw_expert_runner_reserve_prefill(gw_expert_runner *runner, int32_t max_token
                                      int32_t expert_count);
 int gw_moe_prefill_forward(gw_expert_runner *runner, const gw_moe_layer_args *args);
 
+/* ---- .gwt installations ---------------------------------------------------
+ * A .gwt install is a directory with manifest.json (GodwitManifest,
+ * Install/GodwitManifest.swift:8-105) and experts/layer_NN.bin, each
+ * expertCount strides of expertStride bytes in ExpertLayout section order
+ * (Install/InstallLayout.swift:14-121).  gw_model_open replaces ModelReader.init
+ * (Runtime/ModelReader.swift:17-37: manifest required, format version 2);
+ * gw_model_validate is GodwitManifest.validate (:79-104, layer file sizes);
+ * gw_model_load_layer / _load_expert replace ModelReader.loadExpertStride and
+ * read (:72-110): pread into pinned staging, copied to HBM by the context's
+ * stream; they return when the bytes are on the device.  The loaded layer is
+ * the experts_base of gw_moe_layer_forward, unchanged bytes. */
+#define GW_GWT_FORMAT_VERSION 2
+
+typedef struct gw_model gw_model;
+
+typedef struct gw_model_info {
+    int64_t format_version;
+    int64_t layer_count;              /* installed layers */
+    int64_t expert_count;
+    int64_t expert_stride;            /* bytes per expert within a layer file */
+    int64_t section_offset[GW_SECTION_COUNT];   /* ExpertLayout.Section order */
+    int64_t section_length[GW_SECTION_COUNT];
+    int64_t hidden_size;
+    int64_t intermediate_size;
+    int64_t experts_per_token;        /* largest spec.layers[].expertsPerToken */
+    float rms_norm_epsilon;
+    float activation_limit;           /* spec.activationLimit (default 7.0) */
+    float activation_alpha;           /* spec.activationAlpha (default 1.702) */
+    gw_activation activation;         /* spec.activation */
+    int32_t expert_bias;              /* spec.expertBias (default false) */
+    int32_t router_bias;              /* spec.routerBias (default false) */
+} gw_model_info;
+
+int gw_model_open(const char *directory, gw_model **out);
+int gw_model_close(gw_model *model);
+int gw_model_info_get(const gw_model *model, gw_model_info *info);
+int gw_model_validate(const gw_model *model);
+int gw_model_load_layer(gw_context *ctx, gw_model *model, int32_t layer, void *device_dst,
+                        size_t capacity);
+int gw_model_load_expert(gw_context *ctx, gw_model *model, int32_t layer, int32_t expert,
+                         void *device_dst);
+
 /* The MoE block with the steps either side of it (TransformerLayer.forward,
  * TransformerLayer.swift:140-143 and 232-238): normed = RMSNorm(stream) in fp16
  * (TransformerLayer.normalise, :265-285; rmsnorm, router.metal:36-60: the sum
