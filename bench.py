@@ -228,6 +228,132 @@ def prefill_bench(gw, args) -> int:
     return 0
 
 
+QWEN3 = dict(H=2048, F=768, E=128, K=8, L=48)
+
+
+def qwen3_bench(gw, args, batch: int) -> int:
+    """Qwen3 MoE stack, 48 layers x 128 experts (hidden 2048,
+    expert intermediate 768, gate/up interleaved row-wise, zero bias sections as
+    the reference's install writes them, SiLU-GLU), top-8, bf16 x; `batch` tokens
+    per step (1 or 8) with independent N(0,1) logits per token and layer.  Bytes per
+    step: every distinct selected expert of every layer once (the packed nibbles,
+    scales and zero bias sections), plus logits, activations and outputs."""
+    q = QWEN3
+    Hq, Fq, Eq, Kq, Lq = q["H"], q["F"], q["E"], q["K"], q["L"]
+    ctx = gw.Context(0)
+    lay = gw.ExpertLayout(Hq, Fq, Eq)
+    runner = gw.ExpertRunner(ctx, Hq, Fq, "silu")
+    # A batch may take the grouped GEMMs (GODWIT_PREFILL_ABOVE below the
+    # batch): their scratch has to exist before the step is captured.
+    runner.reserve_prefill(batch, Kq, Eq)
+    o, sz = lay.offsets, lay.sizes
+    layers = []
+    for l in range(Lq):
+        buf = ctx.empty(lay.layer_file_size)
+        s = args.seed * 1000003 + l * 7919
+        ctx.fill_uniform_u8(buf, 0, 255, s)
+        for e in range(Eq):
+            base = e * lay.stride
+            ctx.fill_uniform_u8(buf, 119, 127, s * 131 + 4 * e + 1,
+                                offset=base + o["gate_up_scales"], count=sz["gate_up_scales"])
+            ctx.fill_uniform_u8(buf, 119, 127, s * 131 + 4 * e + 2,
+                                offset=base + o["down_scales"], count=sz["down_scales"])
+            for sec in ("gate_up_bias", "down_bias"):
+                ctx.fill_uniform_u8(buf, 0, 0, 0, offset=base + o[sec], count=sz[sec])
+        layers.append(buf)
+    ctx.synchronize()
+    log(f"resident experts: {Lq} x {Eq} x {lay.stride} B = {Lq * lay.layer_file_size / 1e9:.2f} GB")
+    total = args.warmup + args.steps
+    step_logits = Lq * batch * Eq * 4
+    logits_all = ctx.empty(total * step_logits)
+    ctx.fill_normal(logits_all, gw.F32, total * Lq * batch * Eq, 0.0, 1.0, args.seed * 31 + 7)
+    cur = ctx.empty(step_logits)
+    xs = [ctx.empty(batch * Hq * 2) for _ in range(Lq + 1)]
+    ctx.fill_normal(xs[0], gw.BF16, batch * Hq, 0.0, 1.0, args.seed * 31 + 9)
+    outs = [ctx.empty(batch * Hq * 4) for _ in range(Lq)]
+    ids = ctx.empty(Lq * batch * Kq * 4)
+    ctx.synchronize()
+
+    def token():
+        for l in range(Lq):
+            runner.layer_forward(layers[l].ptr, lay.stride, Eq, Kq, xs[l].ptr, gw.BF16, batch,
+                                 outs[l].ptr, logits=cur.address(l * batch * Eq * 4),
+                                 out_bf16=xs[l + 1].ptr,
+                                 routing_ids=ids.address(l * batch * Kq * 4))
+
+    graph = gw.Graph.capture(ctx, token)
+
+    def step(i):
+        ctx.copy_async(cur.ptr, logits_all.address(i * step_logits), step_logits)
+        graph.launch()
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.synchronize()
+    uniq = []
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i)
+    ctx.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    # distinct experts per layer, from the routing of the steps just timed
+    lg = logits_all.download(np.float32, total * Lq * batch * Eq).reshape(total, Lq, batch, Eq)
+    for i in range(args.warmup, total):
+        top = np.argsort(-lg[i], axis=-1)[..., :Kq]
+        uniq.append(sum(len(set(top[l].ravel().tolist())) for l in range(Lq)))
+    per_expert = sum(lay.sizes[k] for k in lay.sizes)
+    nbytes = float(np.mean(uniq)) * per_expert + Lq * batch * (Eq * 4 + Hq * 2 + Hq * 4 + Hq * 2)
+    value = nbytes / dt / 1e9
+    log(f"qwen3 batch {batch}: {dt * 1e6:.1f} us/step ({dt * 1e6 / batch:.1f} us/token), "
+        f"{value:.0f} GB/s ({value / PEAK_HBM_GBS * 100:.1f}% of {PEAK_HBM_GBS:.0f}), "
+        f"{np.mean(uniq) / Lq:.1f} distinct experts per layer")
+    kernels = {}
+    if not args.no_profile_pass:
+        ctx.set_profiling(True)
+        ctx.profile_reset()
+        for i in range(args.steps):
+            ctx.copy_async(cur.ptr, logits_all.address((args.warmup + i) * step_logits),
+                           step_logits)
+            token()
+        ctx.synchronize()
+        for name in ("gate_up", "down", "prefill_route", "prefill_group", "prefill_gate_up",
+                     "prefill_down", "prefill_combine"):
+            ms, n = ctx.profile(name)
+            if n:
+                kernels[name] = {"launches": n, "avg_us": ms / n * 1e3}
+        ctx.set_profiling(False)
+        log("kernels: " + ", ".join(f"{k} {v['avg_us']:.2f} us x{v['launches']}"
+                                    for k, v in kernels.items()))
+    roof = None
+    gu = "gate_up" if "gate_up" in kernels else "prefill_gate_up"
+    if gu in kernels:
+        gu_bytes = (float(np.mean(uniq)) / Lq) * (lay.sizes["gate_up_blocks"] +
+                                                  lay.sizes["gate_up_scales"] +
+                                                  lay.sizes["gate_up_bias"])
+        ach = gu_bytes / (kernels[gu]["avg_us"] * 1e-6) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": ("gate_up_kernel (fused MXFP4 gate_up GEMV + SiLU-GLU)" if gu == "gate_up"
+                           else "prefill_gemm_kernel gate_up (grouped MXFP4 GEMM + SiLU-GLU)"),
+                "bytes_per_launch": int(gu_bytes),
+                "avg_launch_us": round(kernels[gu]["avg_us"], 3)}
+    print(json.dumps({
+        "metric": f"HBM GB/s (% of peak) + µs/token, Qwen3 MXFP4 MoE stack, batch {batch}",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
+        "us_per_token": round(dt * 1e6 / batch, 2), "hbm_frac_of_peak": round(value / PEAK_HBM_GBS, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4",
+        "compute": "e2m1 weights x bf16 activations, fp32 accumulation",
+        "data": "synthetic (seeded MXFP4, zero bias sections, logits N(0,1) per token and layer)",
+        "config": {"workload": f"qwen3-moe-stack-decode-b{batch}", "layers": Lq, "experts": Eq,
+                   "top_k": Kq, "hidden": Hq, "intermediate": Fq, "batch": batch,
+                   "parallelism": "single-gpu"},
+        "kernels": kernels, "roofline": roof, "cpu_baseline": None}), flush=True)
+    runner.close()
+    ctx.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -237,9 +363,13 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bounded CPU-baseline sample (0 disables it)")
     ap.add_argument("--no-profile-pass", action="store_true")
-    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
+    ap.add_argument("--batch", type=int, default=None,
+                    help="tokens per step for the qwen3 workloads (default 1, or 8 for qwen3-b8)")
+    ap.add_argument("--workload", choices=["decode", "prefill", "qwen3", "qwen3-b8"],
+                    default="decode",
                     help="decode: BASELINE config 2 (the headline line, default); prefill: "
-                         "config 4, one GPT-OSS-120B layer, 512 Zipf-routed tokens")
+                         "config 4, one GPT-OSS-120B layer, 512 Zipf-routed tokens; qwen3 / "
+                         "qwen3-b8: config 3, the Qwen3 stack at batch 1 / 8")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -252,6 +382,9 @@ def main() -> int:
 
     if args.workload == "prefill":
         return prefill_bench(gw, args)
+    if args.workload in ("qwen3", "qwen3-b8"):
+        batch = args.batch or (8 if args.workload == "qwen3-b8" else 1)
+        return qwen3_bench(gw, args, batch)
 
     ctx = gw.Context(0)
     lay = gw.ExpertLayout(H, F, E)

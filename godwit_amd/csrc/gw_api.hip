@@ -562,6 +562,7 @@ struct gw_expert_runner {
     int pf_tokens = 0, pf_topk = 0, pf_experts = 0;
     void *pf_buf = nullptr;
     bool fused_enabled = false;      // GODWIT_FUSED_LAYER=1 at creation turns it on
+    int prefill_above = 2;           // batches larger than this run the grouped GEMMs
     int ring_next = 0;
     int ring_used = 0;
 };
@@ -637,6 +638,8 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     }
     const char *env = getenv("GODWIT_FUSED_LAYER");
     r->fused_enabled = env && env[0] == '1';
+    const int pa = get_env_int("GODWIT_PREFILL_ABOVE", 2);
+    r->prefill_above = pa < 1 ? 1 : pa > gw::kMaxTokens ? gw::kMaxTokens : pa;
     *out = r;
     return GW_OK;
 }
@@ -938,10 +941,32 @@ extern "C" int gw_expert_apply_assignments(gw_expert_runner *r, const void *inpu
 // out_mode 0: out = MoE output; 2: out += MoE output (the residual add).
 static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int out_mode);
 
+// A batch of up to kMaxTokens tokens runs either the streaming decode kernels,
+// which read each selected expert once per token group of a workgroup, or the
+// grouped GEMMs, which read each distinct expert once for the whole batch but
+// pay for routing, grouping and combining in kernels of their own.  Above
+// prefill_above tokens (GODWIT_PREFILL_ABOVE at creation, default 2) the
+// grouped GEMMs win; they are taken when the shape is one they accept and,
+// under graph capture, when their scratch is already large enough.
+static bool batch_takes_grouped_gemm(const gw_expert_runner *r, const gw_moe_layer_args *a)
+{
+    if (a->tokens <= r->prefill_above) return false;
+    if (r->hidden % 32 || r->inter % 32 || r->hidden < 128 || r->inter < 128) return false;
+    if (a->expert_count < 1 || a->expert_count > 256 || !aligned16(a->x) ||
+        !aligned16(a->experts_base) || a->expert_stride % 16)
+        return false;
+    if (r->ctx->capturing &&
+        !(r->pf_buf && a->tokens <= r->pf_tokens && a->top_k <= r->pf_topk &&
+          a->expert_count <= r->pf_experts))
+        return false;
+    return true;
+}
+
 static int moe_layer_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int out_mode)
 {
     GW_CHECK(r && a, GW_ERR_ARG, "null argument");
-    if (a->tokens > gw::kMaxTokens) return moe_prefill_impl(r, a, out_mode);
+    if (a->tokens > gw::kMaxTokens || batch_takes_grouped_gemm(r, a))
+        return moe_prefill_impl(r, a, out_mode);
     GW_CHECK(a->tokens >= 1, GW_ERR_SHAPE, "tokens must be positive (got %d)", a->tokens);
     GW_CHECK(a->expert_count >= 1 && a->expert_count <= kMaxExperts, GW_ERR_SHAPE,
              "expert_count %lld out of range", (long long)a->expert_count);
@@ -1127,15 +1152,17 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
                                  a->x, a->x_dtype, ps.logits, E, (int)r->hidden, T));
         logits = ps.logits;
     }
-    {
+    const bool route_in_group = gw::prefill_routes_in_group(T, K);
+    if (!route_in_group) {
         ProfScope p(ctx, "prefill_route");
         GW_HIP(gw::launch_prefill_route(p.launch(L), logits, T, E, K, ps.ids, ps.weights));
     }
     const int max_tiles = gw::prefill_max_tiles(T, K, E);
     {
         ProfScope p(ctx, "prefill_group");
-        GW_HIP(gw::launch_prefill_group(p.launch(L), ps.ids, T * K, E, ps.offsets, ps.order,
-                                        ps.tiles, ps.ntiles, max_tiles));
+        GW_HIP(gw::launch_prefill_group(p.launch(L), route_in_group ? logits : nullptr, T, K,
+                                        ps.weights, ps.ids, E, ps.offsets, ps.order, ps.tiles,
+                                        ps.ntiles, max_tiles));
     }
     const gw::Sections sec = sections_of(r->offsets);
     gw::PrefillGemm g;

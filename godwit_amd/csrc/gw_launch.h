@@ -95,9 +95,14 @@ int prefill_planes(int in_dt);        // bf16 planes that hold a dtype exactly: 
 int prefill_gemm_lds_bytes(int planes, int kdim);
 hipError_t launch_prefill_route(const Launch &L, const float *logits, int T, int E, int K,
                                 int32_t *ids, float *weights);
-hipError_t launch_prefill_group(const Launch &L, const int32_t *ids, int N, int E,
-                                int32_t *offsets, int32_t *order, int32_t *tiles,
-                                int32_t *ntiles, int max_tiles);
+// True when launch_prefill_group can route the batch itself (logits given).
+bool prefill_routes_in_group(int T, int K);
+// Groups entries t*K+k by expert.  With logits non-null it first routes the
+// batch (writing ids and weights), which needs prefill_routes_in_group(T, K);
+// with logits null it reads ids written by launch_prefill_route.
+hipError_t launch_prefill_group(const Launch &L, const float *logits, int T, int K, float *weights,
+                                int32_t *ids, int E, int32_t *offsets, int32_t *order,
+                                int32_t *tiles, int32_t *ntiles, int max_tiles);
 hipError_t launch_prefill_split(const Launch &L, const void *in, int in_dt, int64_t n,
                                 uint16_t *out);
 hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const PrefillGemm &g,

@@ -79,41 +79,87 @@ __global__ __launch_bounds__(256) void prefill_route_kernel(const float *__restr
 // index `order`, which lists expert e's entries; a work item is one 32-entry
 // tile of one expert, encoded (e << 16) | m.  Positions inside a group come
 // from LDS atomics: each entry's results depend only on its own token row, so
-// the order inside a group never changes a value.
+// the order inside a group never changes a value.  The expert offsets and the
+// tile list come from one exclusive scan over the experts (waves 0..3 hold
+// one expert per lane).  Small batches (T <= kRouteGroupTokens) are routed in
+// the same workgroup first, one wave per token, and skip the route kernel.
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(1024) void prefill_group_kernel(const int32_t *__restrict__ ids, int N,
-                                                             int E, int32_t *__restrict__ offsets,
-                                                             int32_t *__restrict__ order,
-                                                             int32_t *__restrict__ tiles,
-                                                             int32_t *__restrict__ ntiles,
-                                                             int max_tiles)
+constexpr int kGroupThreads = 1024;
+constexpr int kRouteGroupTokens = 32;
+constexpr int kRouteGroupEntries = kRouteGroupTokens * kMaxTopK;
+
+__global__ __launch_bounds__(kGroupThreads) void prefill_group_kernel(
+    const float *__restrict__ logits, int T, int K, float *__restrict__ weights,
+    int32_t *__restrict__ ids, int E, int32_t *__restrict__ offsets,
+    int32_t *__restrict__ order, int32_t *__restrict__ tiles, int32_t *__restrict__ ntiles,
+    int max_tiles)
 {
     __shared__ int cnt[kPrefillMaxExperts];
     __shared__ int cur[kPrefillMaxExperts];
     __shared__ int off[kPrefillMaxExperts + 1];
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    __shared__ int wtot[2][kPrefillMaxExperts / 64];
+    __shared__ int sids[kRouteGroupEntries];
+    const int tid = (int)threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int N = T * K;
+    for (int e = tid; e < E; e += kGroupThreads) {
         cnt[e] = 0;
         cur[e] = 0;
     }
-    __syncthreads();
-    for (int j = threadIdx.x; j < N; j += blockDim.x) atomicAdd(&cnt[ids[j]], 1);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int o = 0, nt = 0;
-        for (int e = 0; e < E; ++e) {
-            off[e] = o;
-            o += cnt[e];
-            for (int m = 0; m * kPT < cnt[e]; ++m)
-                if (nt < max_tiles) tiles[nt++] = (e << 16) | m;
+    if (logits) {
+        // routing fused in: the launcher only passes logits for N <= kRouteGroupEntries
+        for (int t = wv; t < T; t += kGroupThreads / 64) {
+            int sid;
+            float w;
+            select_one<4>(logits + (int64_t)t * E, E, K, sid, w);
+            if (lane < K) {
+                ids[t * K + lane] = sid;
+                weights[t * K + lane] = w;
+                sids[t * K + lane] = sid;
+            }
         }
-        off[E] = o;
-        *ntiles = nt;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e <= E; e += blockDim.x) offsets[e] = off[e];
-    for (int j = threadIdx.x; j < N; j += blockDim.x) {
-        const int e = ids[j];
+    for (int j = tid; j < N; j += kGroupThreads) atomicAdd(&cnt[logits ? sids[j] : ids[j]], 1);
+    __syncthreads();
+    // inclusive wave scans of (entries, tiles) per expert, then wave totals
+    int c = 0, n = 0;
+    if (tid < kPrefillMaxExperts && tid < E) {
+        c = cnt[tid];
+        n = (c + kPT - 1) / kPT;
+    }
+    int ic = c, in = n;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int uc = __shfl_up(ic, d, 64), un = __shfl_up(in, d, 64);
+        if (lane >= d) {
+            ic += uc;
+            in += un;
+        }
+    }
+    if (tid < kPrefillMaxExperts && lane == 63) {
+        wtot[0][wv] = ic;
+        wtot[1][wv] = in;
+    }
+    __syncthreads();
+    if (tid < E) {
+        int bc = 0, bn = 0;
+        for (int w = 0; w < wv; ++w) {
+            bc += wtot[0][w];
+            bn += wtot[1][w];
+        }
+        const int ec = bc + ic - c, en = bn + in - n;   // exclusive prefix of expert tid
+        off[tid] = ec;
+        for (int m = 0; m < n && en + m < max_tiles; ++m) tiles[en + m] = (tid << 16) | m;
+        if (tid == E - 1) {
+            off[E] = ec + c;
+            *ntiles = min(en + n, max_tiles);
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e <= E; e += kGroupThreads) offsets[e] = off[e];
+    for (int j = tid; j < N; j += kGroupThreads) {
+        const int e = logits ? sids[j] : ids[j];
         order[off[e] + atomicAdd(&cur[e], 1)] = j;
     }
 }
@@ -601,13 +647,16 @@ hipError_t launch_prefill_route(const Launch &L, const float *logits, int T, int
 
 int prefill_max_tiles(int T, int K, int E) { return pdiv_up((int64_t)T * K, kPT) + E; }
 
-hipError_t launch_prefill_group(const Launch &L, const int32_t *ids, int N, int E,
-                                int32_t *offsets, int32_t *order, int32_t *tiles,
-                                int32_t *ntiles, int max_tiles)
+bool prefill_routes_in_group(int T, int K) { return T <= kRouteGroupTokens && K <= kMaxTopK; }
+
+hipError_t launch_prefill_group(const Launch &L, const float *logits, int T, int K, float *weights,
+                                int32_t *ids, int E, int32_t *offsets, int32_t *order,
+                                int32_t *tiles, int32_t *ntiles, int max_tiles)
 {
-    if (E > kPrefillMaxExperts) return hipErrorInvalidValue;
-    GW_LAUNCH(prefill_group_kernel, dim3(1), dim3(1024), 0, L, ids, N, E, offsets, order, tiles,
-              ntiles, max_tiles);
+    if (E > kPrefillMaxExperts || T <= 0 || K <= 0 || K > kMaxTopK) return hipErrorInvalidValue;
+    if (logits && !prefill_routes_in_group(T, K)) return hipErrorInvalidValue;
+    GW_LAUNCH(prefill_group_kernel, dim3(1), dim3(kGroupThreads), 0, L, logits, T, K, weights,
+              ids, E, offsets, order, tiles, ntiles, max_tiles);
     return hipGetLastError();
 }
 

@@ -265,9 +265,13 @@ def test_layer_given_logits_128_experts(ctx):
     _close(got[0], ref[0])
 
 
-@pytest.mark.parametrize("tokens", [1, 8])
-def test_layer_qwen3_decode(ctx, tokens):
-    """BASELINE config 3 layer: Qwen3 shape, top-8 of 128, no biases, SiLU-GLU, batch 1/8."""
+@pytest.mark.parametrize("tokens,path", [(1, "stream"), (3, "stream"), (8, "stream"),
+                                         (3, "grouped"), (8, "grouped")])
+def test_layer_qwen3_decode(ctx, monkeypatch, tokens, path):
+    """BASELINE config 3 layer: Qwen3 shape, top-8 of 128, no biases, SiLU-GLU, batch 1/8.
+    A batch of 3..8 tokens takes the grouped GEMMs by default; GODWIT_PREFILL_ABOVE=8
+    at runner creation keeps it on the streaming decode kernels."""
+    monkeypatch.setenv("GODWIT_PREFILL_ABOVE", "8" if path == "stream" else "2")
     got, _, ids, wts, ref, rids, rw = _layer_case(ctx, QWEN3, 128, 8, tokens, 800 + tokens,
                                                   router=False)
     assert np.array_equal(ids, rids)
@@ -275,12 +279,16 @@ def test_layer_qwen3_decode(ctx, tokens):
         _close(got[t], ref[t])
 
 
-@pytest.mark.parametrize("experts,top_k,tokens", [(128, 8, 8), (64, 4, 3), (300, 4, 2)])
-def test_layer_routing_ties_exact(ctx, experts, top_k, tokens):
+@pytest.mark.parametrize("experts,top_k,tokens,path", [(128, 8, 8, "stream"), (64, 4, 3, "stream"),
+                                                        (300, 4, 2, "stream"),
+                                                        (128, 8, 8, "grouped")])
+def test_layer_routing_ties_exact(ctx, monkeypatch, experts, top_k, tokens, path):
     """Device routing reproduces Router.select's partial selection sort exactly, ties
     included: logits drawn from 6 distinct values, so most top-k picks are ties
     broken by the sort's swap history.  300 experts exercises the standalone route
-    kernel, the others the routing fused into the gate_up kernel."""
+    kernel, the other streaming cases the routing fused into the gate_up kernel, the
+    grouped case the grouped GEMMs' route kernel."""
+    monkeypatch.setenv("GODWIT_PREFILL_ABOVE", "8" if path == "stream" else "2")
     shape = SMALL
     H = shape["hidden"]
     layout, experts_d, buf = _make_layer(ctx, shape, experts, 1000 + experts)

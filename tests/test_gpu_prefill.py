@@ -75,7 +75,9 @@ def _run(ctx, runner, layout, buf, E, K, xb, x_dtype, lb, T, H, fn="prefill_forw
     (SMALL, 16, 4, 72, gw.BF16, 1),      # experts with 2-3 tiles, partial feature tiles
     (QWEN3, 32, 8, 24, gw.F16, 2),       # two activation planes, no biases, SiLU-GLU
     (GPTOSS, 12, 4, 20, gw.F32, 3),      # three planes, 2880-wide K (11.25 chunks)
-], ids=["small-bf16", "qwen3-f16", "gptoss-f32"])
+    (SMALL, 200, 4, 32, gw.BF16, 4),     # routed inside the group kernel, 4-wave expert scan
+    (SMALL, 256, 8, 40, gw.BF16, 5),     # route kernel, then a scan over 256 experts
+], ids=["small-bf16", "qwen3-f16", "gptoss-f32", "small-e200-t32", "small-e256-t40"])
 def test_prefill_matches_oracle(ctx, shape, E, K, T, x_dtype, seed):
     H, F = shape["hidden"], shape["inter"]
     layout, experts, buf = _make_layer(ctx, shape, E, 2000 + seed)
@@ -96,11 +98,13 @@ def test_prefill_matches_oracle(ctx, shape, E, K, T, x_dtype, seed):
     runner.close()
 
 
-def test_prefill_agrees_with_decode_path(ctx):
-    """The same 8 tokens through the grouped-GEMM prefill and the decode kernels."""
+def test_prefill_agrees_with_decode_path(ctx, monkeypatch):
+    """The same 8 tokens through the grouped-GEMM prefill and the decode kernels
+    (GODWIT_PREFILL_ABOVE=8 keeps layer_forward's 8-token batch on the latter)."""
     shape, E, K, T = GPTOSS, 8, 4, 8
     H, F = shape["hidden"], shape["inter"]
     layout, experts, buf = _make_layer(ctx, shape, E, 2200)
+    monkeypatch.setenv("GODWIT_PREFILL_ABOVE", "8")
     runner = gw.ExpertRunner(ctx, H, F, shape["act"])
     r = rng(2201)
     xb, xw = _x(ctx, r, T, H, gw.BF16)
