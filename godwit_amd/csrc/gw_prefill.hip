@@ -484,9 +484,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
     // chunk q, then wait for this wave's DMA of chunk q+1 and meet the other
     // waves (after which every row of chunk q+1 is in LDS and nobody reads
     // chunk q's buffer any more).
+    const int nq = (nb + kKC - 1) / kKC;
     auto step = [&](int q, auto s_const) {
         constexpr int s = decltype(s_const)::value;
         constexpr int sn = (s + D - 1) % D;
+        if (q >= nq) return;                          // uniform: past the last chunk
         xload(sn, q + D - 1);
         wload(sn, q + D - 1);
         __builtin_amdgcn_sched_barrier(0);
@@ -500,10 +502,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    // nq rounded up to the ring depth: a padding chunk multiplies zero weights.
-    // The scale and bias copies are older than chunk 0's DMA, so the first
+    // The loop runs over nq rounded up to the ring depth (the slot of a step
+    // is a constant); steps past nq do nothing, and the chunks the last real
+    // steps issued past nq are clamped reads that are never multiplied.  The
+    // scale and bias copies are older than chunk 0's DMA, so the first
     // counted wait covers them too.
-    const int nq = (nb + kKC - 1) / kKC;
     const int nq_pad = (nq + D - 1) / D * D;
 #pragma unroll
     for (int s = 0; s < D - 1; ++s) {

@@ -245,7 +245,12 @@ int gw_expert_apply_assignments_async(gw_expert_runner *runner, const void *inpu
  * Experts are HBM-resident at experts_base + e * expert_stride with the
  * runner's section offsets (the .gwt layer file, ExpertLayout).
  * out [tokens, hidden] fp32 is overwritten with the combined expert output
- * (the residual add stays with the caller, :232-238).  Enqueue only. */
+ * (the residual add stays with the caller, :232-238).  Batches of more than
+ * 8 tokens run the grouped GEMMs of gw_moe_prefill_forward; so do batches of
+ * 3..8 tokens (more than GODWIT_PREFILL_ABOVE at runner creation, default 2)
+ * when hidden and intermediate sizes are multiples of 32 and >= 128, x is
+ * 16-byte aligned, there are at most 256 experts and, during graph capture,
+ * the prefill scratch is already reserved.  Enqueue only. */
 typedef struct gw_moe_layer_args {
     const uint8_t *experts_base;
     int64_t expert_stride;
@@ -277,7 +282,8 @@ int gw_moe_layer_forward(gw_expert_runner *runner, const gw_moe_layer_args *args
  * arguments as gw_moe_layer_forward; up to 256 experts.  Scratch grows on
  * demand (or up front with gw_expert_runner_reserve_prefill, which a caller
  * about to capture a graph must use).  gw_moe_layer_forward itself sends
- * batches of more than 8 tokens here.  Enqueue only. */
+ * batches of more than 8 tokens here, and smaller batches as it describes.
+ * Enqueue only. */
 int gw_expert_runner_reserve_prefill(gw_expert_runner *runner, int32_t max_tokens, int32_t top_k,
                                      int32_t expert_count);
 int gw_moe_prefill_forward(gw_expert_runner *runner, const gw_moe_layer_args *args);
@@ -332,8 +338,8 @@ int gw_model_load_expert(gw_context *ctx, gw_model *model, int32_t layer, int32_
  * too), then stream += the combined expert output, in fp32, the sum finished
  * before it is added.  `layer.x`, `layer.x_dtype` and `layer.out` are ignored;
  * `layer.out_bf16`, when set, receives a bf16 copy of the updated stream.
- * Batches above 8 tokens take the prefill path (reserve it before capture).
- * Enqueue only. */
+ * Batches take the prefill path as in gw_moe_layer_forward (reserve it
+ * before capture).  Enqueue only. */
 typedef struct gw_moe_block_args {
     gw_moe_layer_args layer;
     float *stream;                    /* [tokens, hidden] fp32 residual stream, in place */
