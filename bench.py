@@ -59,6 +59,18 @@ def gate_up_bytes(lay) -> int:
     return K * per + H * 2 + K * F * 2
 
 
+COUNTER_LAYERS = 4
+# HBM bytes per gate_up_kernel launch (GPT-OSS-120B layer, batch 1): rocprofv3
+# FETCH_SIZE + WRITE_SIZE per dispatch from `bench.py --counter-pass 256`, each
+# scaled by what the counter reads for a 256 MiB device-to-device copy
+# (profiles/decode_gate_up_down_traffic.md).
+GATE_UP_TRAFFIC_BYTES = 35_944_526
+# The same for the prefill gate_up GEMM launch (512 tokens, seed 1):
+# `bench.py --workload prefill` under rocprofv3 --pmc, the copy scale of the
+# decode run (profiles/prefill_gemm_gptoss_512.md).
+PREFILL_GATE_UP_TRAFFIC_BYTES = 1_241_689_122
+
+
 def build_model(ctx, gw, lay, seed: int):
     """36 layer files of 128 expert strides each, filled on the device."""
     return build_model_layers(ctx, gw, lay, seed, L)
@@ -84,6 +96,43 @@ def build_model_layers(ctx, gw, lay, seed: int, n_layers: int):
         bufs.append(buf)
     ctx.synchronize()
     return bufs
+
+
+def counter_pass(gw, args) -> int:
+    """The run rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE profiles for the decode
+    kernels: COUNTER_LAYERS GPT-OSS-120B layers resident (fewer than the stack:
+    the profiler does not survive the 36 x 128 x 4 fill dispatches of the full
+    model; per-launch traffic does not depend on how many layers are resident,
+    as no expert is re-read within the L2), --warmup + --steps tokens through
+    them eagerly with fresh N(0,1) logits per layer and token, then three
+    device-to-device copies of --counter-pass MiB, whose known bytes scale the
+    counters."""
+    ctx = gw.Context(0)
+    lay = gw.ExpertLayout(H, F, E)
+    runner = gw.ExpertRunner(ctx, H, F, "gptOssClampedGLU", 7.0, 1.702)
+    layers = build_model_layers(ctx, gw, lay, args.seed, COUNTER_LAYERS)
+    n_tok = args.warmup + args.steps
+    logits = ctx.empty(n_tok * COUNTER_LAYERS * E * 4)
+    ctx.fill_normal(logits, gw.F32, n_tok * COUNTER_LAYERS * E, 0.0, 1.0, args.seed * 31 + 7)
+    xs = [ctx.empty(H * 2) for _ in range(COUNTER_LAYERS + 1)]
+    ctx.fill_normal(xs[0], gw.BF16, H, 0.0, 1.0, args.seed * 31 + 9)
+    out = ctx.empty(H * 4)
+    for i in range(n_tok):
+        for l in range(COUNTER_LAYERS):
+            runner.layer_forward(layers[l].ptr, lay.stride, E, K, xs[l].ptr, gw.BF16, 1, out.ptr,
+                                 logits=logits.address(((i * COUNTER_LAYERS) + l) * E * 4),
+                                 out_bf16=xs[l + 1].ptr)
+    nb = args.counter_pass << 20
+    src, dst = ctx.empty(nb), ctx.empty(nb)
+    ctx.fill_uniform_u8(src, 0, 255, 3)
+    for _ in range(3):
+        ctx.copy_async(dst.ptr, src.ptr, nb)
+    ctx.synchronize()
+    log(f"counter pass: {n_tok} eager tokens x {COUNTER_LAYERS} layers, then 3 copies of "
+        f"{nb} B (__amd_rocclr_copyBuffer: {nb} B read + {nb} B written each)")
+    runner.close()
+    ctx.close()
+    return 0
 
 
 def cpu_baseline(seconds: float) -> dict:
@@ -204,7 +253,7 @@ def prefill_bench(gw, args) -> int:
         ach = gu_bytes / (gu * 1e-6) / 1e9
         gu_tflops = 2.0 * T * K * 2 * F * H / (gu * 1e-6) / 1e12
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": PREFILL_GATE_UP_TRAFFIC_BYTES,
                 "kernel": "prefill_gemm_kernel (gate_up grouped GEMM)",
                 "avg_launch_us": round(gu, 3), "algorithmic_bytes": gu_bytes,
                 "mfma_tflops": round(gu_tflops, 1),
@@ -363,6 +412,11 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bounded CPU-baseline sample (0 disables it)")
     ap.add_argument("--no-profile-pass", action="store_true")
+    ap.add_argument("--counter-pass", type=int, default=0, metavar="MIB",
+                    help="decode only: run --steps tokens eagerly (no graph, no events), then a "
+                         "device-to-device copy of MIB MiB three times, and exit; the run "
+                         "that rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE profiles (the copy "
+                         "scales the counters to bytes)")
     ap.add_argument("--batch", type=int, default=None,
                     help="tokens per step for the qwen3 workloads (default 1, or 8 for qwen3-b8)")
     ap.add_argument("--workload", choices=["decode", "prefill", "qwen3", "qwen3-b8"],
@@ -380,6 +434,8 @@ def main() -> int:
 
     import godwit_amd as gw
 
+    if args.counter_pass:
+        return counter_pass(gw, args)
     if args.workload == "prefill":
         return prefill_bench(gw, args)
     if args.workload in ("qwen3", "qwen3-b8"):
@@ -410,8 +466,8 @@ def main() -> int:
                                  outs[l].ptr, logits=cur_logits.address(l * E * 4),
                                  out_bf16=xs[l + 1].ptr, routing_ids=ids.address(l * K * 4))
 
-    graph = gw.Graph.capture(ctx, token)
     step_logits = L * E * 4
+    graph = gw.Graph.capture(ctx, token)
 
     def step(i: int):
         ctx.copy_async(cur_logits.ptr, logits_all.address(i * step_logits), step_logits)
@@ -462,7 +518,8 @@ def main() -> int:
         k_us = kernels[dom]["avg_us"]
         achieved = nbytes / (k_us * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                    "traffic": GATE_UP_TRAFFIC_BYTES if dom == "gate_up" else None,
                     "kernel": desc, "bytes_per_launch": nbytes, "avg_launch_us": round(k_us, 3)}
         log("kernels: " + ", ".join(f"{k} {v['avg_us']:.2f} us x{v['launches']}"
                                     for k, v in kernels.items()))

@@ -307,10 +307,26 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
     const int nb = a.kdim >> 5;
     const PrefillLds lay = prefill_lds(PL, D, nb);
     uint8_t *xring = lds8 + lay.ring;
-    const int item = blockIdx.y;
-    if (item >= *a.ntiles) return;                    // uniform: the workgroup leaves
-    const int te = a.tiles[item];
-    const int e = te >> 16, m = te & 0xFFFF;
+    // Work unit -> (expert e, feature tile, entry tile m).  Units run expert by
+    // expert, feature tile by feature tile, with the entry tiles of one
+    // (expert, feature tile) adjacent, so the workgroups that read the same
+    // weights run together; and each XCD (workgroup ids congruent mod 8) takes
+    // one contiguous eighth of the units, so those workgroups share one L2.
+    // floor(unit / nft) is always one of the unit's expert's tiles.
+    const int nft = (a.fdim + kPF - 1) / kPF;
+    const int units = *a.ntiles * nft;
+    const int per = (units + 7) >> 3;
+    const int jx = (int)(blockIdx.x >> 3);
+    const int unit = (int)(blockIdx.x & 7) * per + jx;
+    if (jx >= per || unit >= units) return;           // uniform: the workgroup leaves
+    const int tq = unit / nft;
+    const int te = a.tiles[tq];
+    const int e = te >> 16;
+    const int t0 = tq - (te & 0xFFFF);
+    const int ecnt = a.offsets[e + 1] - a.offsets[e];
+    const int ne = (ecnt + kPT - 1) / kPT;
+    const int local = unit - t0 * nft;
+    const int fidx = local / ne, m = local - fidx * ne;
     const int g0 = a.offsets[e] + m * kPT;
     const int ntok = min(kPT, a.offsets[e + 1] - g0);
     if (threadIdx.x < kPT) ent[threadIdx.x] = a.order[g0 + min((int)threadIdx.x, ntok - 1)];
@@ -318,7 +334,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int h = lane >> 5, c = lane & 31;
-    const int f0 = blockIdx.x * kPF;
+    const int f0 = fidx * kPF;
     const int fbase = f0 + wave * 32;
     const int row = min(fbase + c, a.fdim - 1);       // clamped: rows past fdim are never stored
     const uint8_t *ex = a.experts_base + (int64_t)e * a.stride;
@@ -722,7 +738,9 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
     a.act_kind = g.act_kind;
     a.limit = g.limit;
     a.alpha = g.alpha;
-    const dim3 grid(pdiv_up(g.fdim, kPF), max_tiles);
+    // One workgroup per (feature tile, tile) unit, rounded up to whole XCD
+    // rounds; the kernel maps ids to units and retires the spare ones.
+    const dim3 grid((pdiv_up(g.fdim, kPF) * max_tiles + 7) / 8 * 8);
     const int lds_bytes = prefill_gemm_lds_bytes(planes, g.kdim);
     if (lds_bytes > kPrefillLdsMax) return hipErrorInvalidValue;   // K too wide for the staging
     const size_t lds = (size_t)lds_bytes;
