@@ -501,7 +501,7 @@ template <int MT, class SH>
 __global__ __launch_bounds__(kNT) void down_kernel(
     const Plan *__restrict__ gplan, const uint16_t *__restrict__ act, int hidden, int inter,
     Sections sec, int bias_dt, float *__restrict__ out, uint16_t *__restrict__ out_bf16,
-    int accumulate, int smax, int nmax, int chunks, int prestage)
+    int accumulate, int smax, int nmax, int chunks)
 {
     constexpr int TPR = SH::TPR;
     extern __shared__ __align__(16) uint32_t lds[];
@@ -511,12 +511,10 @@ __global__ __launch_bounds__(kNT) void down_kernel(
     const int astride = bpr * BD;
     uint32_t *as = lds + sizeof(Plan) / 4;                          // [smax][astride]
     float *vals = reinterpret_cast<float *>(as + smax * astride);   // [kMaxSlots][nmax]
-    // Activations are stored slot-major, so the first `prestage` slots (the
-    // whole first chunk when it holds every slot) are staged without waiting
-    // for the plan; both copies are in flight together.
+    // The plan comes first: the weights' addresses depend on it.  Each chunk
+    // of groups below issues its first weight stages before it stages its
+    // activations, so those two round trips overlap.
     copy_plan(plan, gplan);
-    for (int s = 0; s < prestage; ++s)
-        stage_vector<DT_F16>(as + s * astride, act + (int64_t)s * inter, inter);
     __syncthreads();
 
     int r0, r1;
@@ -536,12 +534,6 @@ __global__ __launch_bounds__(kNT) void down_kernel(
             ++g1;
         }
         if (g1 == g) break;   // a group wider than the staging area (the host prevents it)
-        const int staged = s0 == 0 ? prestage : 0;      // slots already in LDS
-        if (s1 > s0 + staged) {
-            for (int s = s0 + staged; s < s1; ++s)
-                stage_vector<DT_F16>(as + (s - s0) * astride, act + (int64_t)s * inter, inter);
-            __syncthreads();
-        }
         const int gbase = g;
         const float inv_n = 1.0f / (float)n;
         auto split = [&](int item, int &gl, int &q) { divmod_small(item, n, inv_n, gl, q); };
@@ -573,8 +565,15 @@ __global__ __launch_bounds__(kNT) void down_kernel(
                     if (t < ntok) vals[(sg + t) * nmax + q] = acc[t] + b;
             }
         };
-        row_engine<(MT == 1 ? kDownDepth : 2), DT_F16, MT, SH, false>((g1 - g) * n, chunks, bpr,
-                                                                    as, rowfn, epi);
+        // Weights first, then this chunk's activations (slot-major in act);
+        // the barrier publishes the staged activations before any consume.
+        constexpr int DD = MT == 1 ? kDownDepth : 2;
+        EngineRing<DD, MT, SH> E;
+        engine_prime<DD, MT, SH>(E, (g1 - g) * n, chunks, bpr, rowfn);
+        for (int s = s0; s < s1; ++s)
+            stage_vector<DT_F16>(as + (s - s0) * astride, act + (int64_t)s * inter, inter);
+        __syncthreads();
+        engine_run<DD, DT_F16, MT, SH, false>(E, (g1 - g) * n, chunks, bpr, as, rowfn, epi);
         __syncthreads();
         g = g1;
     }
@@ -1092,13 +1091,13 @@ template <int MT>
 static void down_dispatch(const Launch &L, const RowShape &s, int grid, size_t lds,
                           const Plan *plan, const uint16_t *act, int hidden, int inter,
                           const Sections &sec, int bias_dt, float *out, uint16_t *out_bf16,
-                          int accumulate, int smax, int nmax, int prestage)
+                          int accumulate, int smax, int nmax)
 {
     with_shape(s, [&](auto sh) {
         using SH = decltype(sh);
         GW_LAUNCH((down_kernel<MT, SH>), dim3(grid), dim3(kNT), lds, L, plan,
                            act, hidden, inter, sec, bias_dt, out, out_bf16, accumulate, smax,
-                           nmax, s.chunks, prestage);
+                           nmax, s.chunks);
     });
 }
 
@@ -1214,13 +1213,12 @@ hipError_t launch_down(const Launch &L, const Plan *plan, int max_tokens, int ma
     if (smax < need) return hipErrorInvalidValue;
     const int nmax = (hidden + grid - 1) / grid;
     const size_t lds = (size_t)down_lds_bytes(hidden, inter, grid, smax);
-    const int prestage = max_slots < smax ? max_slots : smax;
     if (max_tokens == 1)
         down_dispatch<1>(L, s, grid, lds, plan, act, hidden, inter, sec, bias_dt, out, out_bf16,
-                         accumulate, smax, nmax, prestage);
+                         accumulate, smax, nmax);
     else
         down_dispatch<kMaxTokens>(L, s, grid, lds, plan, act, hidden, inter, sec, bias_dt, out,
-                                  out_bf16, accumulate, smax, nmax, prestage);
+                                  out_bf16, accumulate, smax, nmax);
     return hipGetLastError();
 }
 
