@@ -404,12 +404,23 @@ __global__ __launch_bounds__(kNT) void gate_up_kernel(
         // Wave 0 routes (every workgroup, redundantly: 4 x 128 logits) while the
         // other waves stage the inputs, which are rows 0..T-1 of x.
         if (threadIdx.x < 64) {
-            if (route.tokens == 1)
-                route_one<kFusedRouteR>(route.logits, route.experts, route.top_k,
-                                        route.experts_base, route.stride, plan,
-                                        blockIdx.x == 0 ? route.ids_out : nullptr,
-                                        blockIdx.x == 0 ? route.w_out : nullptr);
-            else
+            if constexpr (MT == 1) {
+                // This workgroup streams rows of the experts of rank < need
+                // only; workgroup 0 routes in full for the down kernel's plan.
+                // 128 experts or fewer fit two logits per lane.
+                int q0, q1;
+                slice_of(route.top_k * inter, q0, q1);
+                const int need = blockIdx.x == 0 ? route.top_k : q1 > q0 ? (q1 - 1) / inter + 1 : 0;
+                int32_t *ids = blockIdx.x == 0 ? route.ids_out : nullptr;
+                float *ws = blockIdx.x == 0 ? route.w_out : nullptr;
+                if (route.experts <= 128)
+                    route_one<2>(route.logits, route.experts, route.top_k, route.experts_base,
+                                 route.stride, plan, ids, ws, need);
+                else
+                    route_one<kFusedRouteR>(route.logits, route.experts, route.top_k,
+                                            route.experts_base, route.stride, plan, ids, ws,
+                                            need);
+            } else
                 route_wave<kFusedRouteR>(route.logits, route.experts, route.top_k, route.tokens,
                                          route.experts_base, route.stride, plan,
                                          blockIdx.x == 0 ? route.ids_out : nullptr,

@@ -66,7 +66,8 @@ __global__ __launch_bounds__(256) void prefill_route_kernel(const float *__restr
     if (t >= T) return;   // whole waves leave together
     int sid;
     float w;
-    select_one<4>(logits + (int64_t)t * E, E, K, sid, w);
+    if (E <= 128) select_one<2>(logits + (int64_t)t * E, E, K, sid, w);
+    else select_one<4>(logits + (int64_t)t * E, E, K, sid, w);
     const int lane = threadIdx.x & 63;
     if (lane < K) {
         ids[(int64_t)t * K + lane] = sid;
@@ -111,7 +112,8 @@ __global__ __launch_bounds__(kGroupThreads) void prefill_group_kernel(
         for (int t = wv; t < T; t += kGroupThreads / 64) {
             int sid;
             float w;
-            select_one<4>(logits + (int64_t)t * E, E, K, sid, w);
+            if (E <= 128) select_one<2>(logits + (int64_t)t * E, E, K, sid, w);
+            else select_one<4>(logits + (int64_t)t * E, E, K, sid, w);
             if (lane < K) {
                 ids[t * K + lane] = sid;
                 weights[t * K + lane] = w;

@@ -14,42 +14,15 @@ namespace gw {
 // Routing by one wave (Router.select, Router.swift:78-98, plus the demand map
 // of TransformerLayer.swift:175-181), register resident.
 //
-// The selection sort's permutation lives in registers: lane l holds positions
-// l, l+64, ... (R per lane) as (expert id, logit) pairs.  At position p the
-// reference keeps the first position >= p holding the largest logit (strict
-// `>` scan), or p itself when logits[order[p]] is NaN; positions are swapped
-// exactly as `order.swapAt(p, best)` does, so ties resolve as in the reference.
+// select_exact follows the selection sort's permutation in registers: lane l
+// holds elements l, l+64, ... (R per lane) with their current positions.  At
+// position p the reference keeps the first position >= p holding the largest
+// logit (strict `>` scan), or p itself when logits[order[p]] is NaN; positions
+// are swapped exactly as `order.swapAt(p, best)` does, so ties resolve as in
+// the reference.  select_fast gives the same result in far fewer instructions
+// when there is no NaN and no tie among the ranks it picks, and hands over to
+// select_exact otherwise.
 // ---------------------------------------------------------------------------
-
-// Wave-wide unsigned max / min: DPP within each 16-lane row (quad swaps, half
-// mirror, mirror), then the four rows through v_readlane.  ALU latency only;
-// the whole wave must be active.
-#define GW_DPP(x, ctrl) ((uint32_t)__builtin_amdgcn_update_dpp((int)(x), (int)(x), (ctrl), 0xF, 0xF, false))
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x)
-{
-    x = max(x, GW_DPP(x, 0xB1));    // quad_perm [1,0,3,2]
-    x = max(x, GW_DPP(x, 0x4E));    // quad_perm [2,3,0,1]
-    x = max(x, GW_DPP(x, 0x141));   // row_half_mirror
-    x = max(x, GW_DPP(x, 0x140));   // row_mirror
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0);
-    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
-    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32);
-    const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
-    return max(max(a, b), max(c, d));
-}
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x)
-{
-    x = min(x, GW_DPP(x, 0xB1));
-    x = min(x, GW_DPP(x, 0x4E));
-    x = min(x, GW_DPP(x, 0x141));
-    x = min(x, GW_DPP(x, 0x140));
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0);
-    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
-    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32);
-    const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
-    return min(min(a, b), min(c, d));
-}
-#undef GW_DPP
 
 // Float -> unsigned key with the same order; 0 is reserved for "no candidate"
 // (NaN and out-of-range positions never win, as `>` never picks them).
@@ -92,151 +65,6 @@ __device__ __forceinline__ float lane_value(float v, int lane)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-template <int R>
-__device__ __forceinline__ void route_wave(const float *__restrict__ logits, int E, int K,
-                                           int T, const uint8_t *experts_base, int64_t stride,
-                                           Plan *plan, int32_t *ids_out, float *w_out)
-{
-    const int lane = threadIdx.x & 63;
-    int my_e = -1;
-    float my_w = 0.0f;
-    for (int t = 0; t < T; ++t) {
-        int ord[R];
-        float ov[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int i = lane + 64 * r;
-            ord[r] = i;
-            ov[r] = i < E ? logits[(int64_t)t * E + i] : 0.0f;
-        }
-        for (int pos = 0; pos < K; ++pos) {
-            // Largest logit among positions >= pos, then the smallest position
-            // holding it: the first one the reference's strict `>` scan keeps.
-            uint32_t km = 0;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int i = lane + 64 * r;
-                const uint32_t k = (i >= pos && i < E && !__builtin_isnan(ov[r])) ? order_key(ov[r]) : 0u;
-                km = max(km, k);
-            }
-            const uint32_t kmax = wave_max_u32(km);
-            uint32_t pmin = 0xFFFFFFFFu;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int i = lane + 64 * r;
-                const bool hit = kmax != 0u && i >= pos && i < E && !__builtin_isnan(ov[r]) &&
-                                 order_key(ov[r]) == kmax;
-                pmin = hit ? min(pmin, (uint32_t)i) : pmin;
-            }
-            const uint32_t bp = wave_min_u32(pmin);
-            const int pr = pos >> 6, pl = pos & 63;
-            float v_pos = 0.0f;
-            int o_pos = 0;
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (r == pr) {
-                    v_pos = lane_value(ov[r], pl);
-                    o_pos = __builtin_amdgcn_readlane(ord[r], pl);
-                }
-            const int best = (bp == 0xFFFFFFFFu || __builtin_isnan(v_pos)) ? pos : (int)bp;
-            const int br = best >> 6, bl = best & 63;
-            float v_b = 0.0f;
-            int o_b = 0;
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (r == br) {
-                    v_b = lane_value(ov[r], bl);
-                    o_b = __builtin_amdgcn_readlane(ord[r], bl);
-                }
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (r == pr && lane == pl) {
-                    ord[r] = o_b;
-                    ov[r] = v_b;
-                }
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (r == br && lane == bl) {
-                    ord[r] = o_pos;
-                    ov[r] = v_pos;
-                }
-        }
-        // Positions 0..K-1 are lanes 0..K-1, register 0.  Softmax over the K
-        // selected logits with the maximum subtracted, summed in order.
-        const int sid = ord[0];
-        const float sv = ov[0];
-        float peak = lane_value(sv, 0);
-        for (int i = 1; i < K; ++i) {
-            const float v = lane_value(sv, i);
-            if (v > peak) peak = v;
-        }
-        const float ex = expf(sv - peak);
-        float total = 0.0f;
-        for (int i = 0; i < K; ++i) total += lane_value(ex, i);
-        const float w = ex / total;
-        const int src = lane - t * K;
-        const bool mine = src >= 0 && src < K;
-        int e_src = 0;
-        float w_src = 0.0f;
-        for (int i = 0; i < K; ++i) {   // entry (t, i) moves to lane t*K + i
-            const int ei = __builtin_amdgcn_readlane(sid, i);
-            const float wi = lane_value(w, i);
-            if (src == i) {
-                e_src = ei;
-                w_src = wi;
-            }
-        }
-        if (mine) {
-            my_e = e_src;
-            my_w = w_src;
-        }
-        if (ids_out && lane < K) ids_out[(int64_t)t * K + lane] = sid;
-        if (w_out && lane < K) w_out[(int64_t)t * K + lane] = w;
-    }
-
-    // Expert-major grouping of the T*K (token, rank) entries by first appearance.
-    const int n = T * K;
-    int first = -1, before = 0, same = 0;
-    for (int j = 0; j < n; ++j) {
-        const int ej = __builtin_amdgcn_readlane(my_e, j);
-        if (lane < n && ej == my_e) {
-            if (first < 0) first = j;
-            if (j < lane) ++before;
-            ++same;
-        }
-    }
-    const bool leader = lane < n && first == lane;
-    const unsigned long long leaders = __ballot(leader);
-    int slot0 = 0;
-    for (int j = 0; j < n; ++j) {
-        const int fj = __builtin_amdgcn_readlane(first, j);
-        if (lane < n && fj < first) ++slot0;
-    }
-    if (lane < n) {
-        const int gi = __popcll(leaders & ((1ull << first) - 1ull));
-        const int slot = slot0 + before;
-        const int t = lane / K, r = lane - (lane / K) * K;
-        plan->slot_token[slot] = t;
-        plan->slot_group[slot] = gi;
-        plan->slot_weight[slot] = my_w;
-        plan->tok_slots[t][r] = slot;
-        if (leader) {
-            plan->group_base[gi] = experts_base + (int64_t)my_e * stride;
-            plan->group_slot0[gi] = slot0;
-            plan->group_ntok[gi] = same;
-        }
-    }
-    if (lane < T) {
-        plan->tok_global[lane] = lane;
-        plan->tok_nslots[lane] = K;
-    }
-    if (lane == 0) {
-        plan->ngroups = __popcll(leaders);
-        plan->nslots = n;
-        plan->ntokens = T;
-        plan->pad0 = 0;
-    }
-}
 
 // Routing of ONE token by one wave, branch-free: Router.select's selection
 // sort (Router.swift:78-98) tracked per element instead of per position.
@@ -247,11 +75,11 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
 // (nothing compares greater than NaN); then it swaps positions exactly as
 // `order.swapAt(p, best)`.  The plan is the single-token demand map: group,
 // slot and rank k are the k-th selected expert.
-// The selection itself: on return lane k < K holds the expert of rank k in
-// *sid and its softmax weight in *w (lanes >= K hold unspecified values).
+// On return lane k < K holds the expert of rank k in sid_out and its logit in
+// sv_out (lanes >= K hold unspecified values).
 template <int R>
-__device__ __forceinline__ void select_one(const float *__restrict__ logits, int E, int K,
-                                           int &sid_out, float &w_out)
+__device__ __forceinline__ void select_exact(const float *__restrict__ logits, int E, int K,
+                                             int &sid_out, float &sv_out)
 {
     const int lane = threadIdx.x & 63;
     float v[R];
@@ -319,6 +147,74 @@ __device__ __forceinline__ void select_one(const float *__restrict__ logits, int
         sid = lane == pos ? id : sid;
         sv = lane == pos ? val : sv;
     }
+    sid_out = sid;
+    sv_out = sv;
+}
+
+// The common case in a few instructions per rank: when no logit is NaN and
+// each of the K largest keys is held by one element only, the selection sort
+// picks those elements in descending order whatever its permutation holds, so
+// K wave-wide maxima give exactly its result.  A NaN, or a rank whose maximum
+// two elements share (a tie, -0 and +0 included), returns false and the
+// caller runs select_exact instead.  Same outputs as select_exact for the
+// first `npass` ranks (npass <= K; lanes >= npass hold unspecified values).
+template <int R>
+__device__ __forceinline__ bool select_fast(const float *__restrict__ logits, int E, int npass,
+                                            int &sid_out, float &sv_out)
+{
+    const int lane = threadIdx.x & 63;
+    float v[R];
+    uint32_t key[R];
+    bool nan = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = lane + 64 * r;
+        v[r] = logits[min(i, E - 1)];
+        const bool in = i < E;
+        nan |= in && __builtin_isnan(v[r]);
+        key[r] = in && !__builtin_isnan(v[r]) ? order_key(v[r]) : 0u;
+    }
+    if (__ballot(nan) != 0ull) return false;
+    int sid = 0;
+    float sv = 0.0f;
+    for (int pos = 0; pos < npass; ++pos) {
+        uint32_t km = key[0];
+#pragma unroll
+        for (int r = 1; r < R; ++r) km = max(km, key[r]);
+        const uint32_t kmax = wave_allmax_u32(km);
+        int count = 0, id = -1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const unsigned long long b = __ballot(key[r] == kmax);
+            count += __popcll(b);
+            if (id < 0 && b != 0ull) id = 64 * r + (int)__builtin_ctzll(b);
+        }
+        if (count != 1 || kmax == 0u) return false;
+        const int src = id & 63, rs = id >> 6;
+        float val = lane_value(v[0], src);
+#pragma unroll
+        for (int r = 1; r < R; ++r) val = rs == r ? lane_value(v[r], src) : val;
+#pragma unroll
+        for (int r = 0; r < R; ++r) key[r] = lane + 64 * r == id ? 0u : key[r];
+        sid = lane == pos ? id : sid;
+        sv = lane == pos ? val : sv;
+    }
+    sid_out = sid;
+    sv_out = sv;
+    return true;
+}
+
+// Top-K of one token's logits by one wave, then the softmax over the K
+// selected (Router.select, Router.swift:78-98).  On return lane k < K holds
+// the expert of rank k in sid_out and its softmax weight in w_out (lanes >= K
+// hold unspecified values).
+template <int R>
+__device__ __forceinline__ void select_one(const float *__restrict__ logits, int E, int K,
+                                           int &sid_out, float &w_out)
+{
+    int sid;
+    float sv;
+    if (!select_fast<R>(logits, E, K, sid, sv)) select_exact<R>(logits, E, K, sid, sv);
     // Softmax over the K selected logits (peak subtracted, summed in rank order).
     float peak = lane_value(sv, 0);
     for (int i = 1; i < K; ++i) {
@@ -332,15 +228,104 @@ __device__ __forceinline__ void select_one(const float *__restrict__ logits, int
     w_out = ex / total;
 }
 
+// Routing of T tokens by one wave (select_one per token) and the demand map
+// of TransformerLayer.swift:175-181: entries grouped by expert in order of
+// first appearance, each group's tokens in token order.
+template <int R>
+__device__ __forceinline__ void route_wave(const float *__restrict__ logits, int E, int K,
+                                           int T, const uint8_t *experts_base, int64_t stride,
+                                           Plan *plan, int32_t *ids_out, float *w_out)
+{
+    const int lane = threadIdx.x & 63;
+    int my_e = -1;
+    float my_w = 0.0f;
+    for (int t = 0; t < T; ++t) {
+        int sid;
+        float w;
+        select_one<R>(logits + (int64_t)t * E, E, K, sid, w);
+        const int src = lane - t * K;
+        const bool mine = src >= 0 && src < K;
+        int e_src = 0;
+        float w_src = 0.0f;
+        for (int i = 0; i < K; ++i) {   // entry (t, i) moves to lane t*K + i
+            const int ei = __builtin_amdgcn_readlane(sid, i);
+            const float wi = lane_value(w, i);
+            if (src == i) {
+                e_src = ei;
+                w_src = wi;
+            }
+        }
+        if (mine) {
+            my_e = e_src;
+            my_w = w_src;
+        }
+        if (ids_out && lane < K) ids_out[(int64_t)t * K + lane] = sid;
+        if (w_out && lane < K) w_out[(int64_t)t * K + lane] = w;
+    }
+
+    // Expert-major grouping of the T*K (token, rank) entries by first appearance.
+    const int n = T * K;
+    int first = -1, before = 0, same = 0;
+    for (int j = 0; j < n; ++j) {
+        const int ej = __builtin_amdgcn_readlane(my_e, j);
+        if (lane < n && ej == my_e) {
+            if (first < 0) first = j;
+            if (j < lane) ++before;
+            ++same;
+        }
+    }
+    const bool leader = lane < n && first == lane;
+    const unsigned long long leaders = __ballot(leader);
+    int slot0 = 0;
+    for (int j = 0; j < n; ++j) {
+        const int fj = __builtin_amdgcn_readlane(first, j);
+        if (lane < n && fj < first) ++slot0;
+    }
+    if (lane < n) {
+        const int gi = __popcll(leaders & ((1ull << first) - 1ull));
+        const int slot = slot0 + before;
+        const int t = lane / K, r = lane - (lane / K) * K;
+        plan->slot_token[slot] = t;
+        plan->slot_group[slot] = gi;
+        plan->slot_weight[slot] = my_w;
+        plan->tok_slots[t][r] = slot;
+        if (leader) {
+            plan->group_base[gi] = experts_base + (int64_t)my_e * stride;
+            plan->group_slot0[gi] = slot0;
+            plan->group_ntok[gi] = same;
+        }
+    }
+    if (lane < T) {
+        plan->tok_global[lane] = lane;
+        plan->tok_nslots[lane] = K;
+    }
+    if (lane == 0) {
+        plan->ngroups = __popcll(leaders);
+        plan->nslots = n;
+        plan->ntokens = T;
+        plan->pad0 = 0;
+    }
+}
+
+// One token's plan.  `need` ranks are enough for a caller that only streams
+// the rows of experts of rank < need (a gate_up workgroup's slice): it stops
+// the selection there and skips the softmax, and the plan's other ranks and
+// weights stay unspecified.  need >= K gives the whole plan with weights.
 template <int R>
 __device__ __forceinline__ void route_one(const float *__restrict__ logits, int E, int K,
                                           const uint8_t *experts_base, int64_t stride,
-                                          Plan *plan, int32_t *ids_out, float *w_out)
+                                          Plan *plan, int32_t *ids_out, float *w_out,
+                                          int need = 1 << 30)
 {
     const int lane = threadIdx.x & 63;
     int sid;
-    float w;
-    select_one<R>(logits, E, K, sid, w);
+    float w = 0.0f;
+    if (need >= K) {
+        select_one<R>(logits, E, K, sid, w);
+    } else {
+        float sv;
+        if (!select_fast<R>(logits, E, need, sid, sv)) select_exact<R>(logits, E, K, sid, sv);
+    }
     if (lane < K) {
         if (ids_out) ids_out[lane] = sid;
         if (w_out) w_out[lane] = w;

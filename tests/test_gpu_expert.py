@@ -319,6 +319,62 @@ def test_layer_routing_ties_exact(ctx, monkeypatch, experts, top_k, tokens, path
     runner.close()
 
 
+def _routing_logits(case, tokens, experts):
+    """Logits for the two device selection paths: distinct values (the fast
+    path), ties only below the top k (still fast), a tie inside the top k,
+    -0.0 against +0.0 at the top, a NaN among the rest, a NaN as the first
+    element (the reference's scan keeps it: nothing compares greater)."""
+    r = rng(1100 + len(case) + tokens)
+    lg = r.standard_normal((tokens, experts)).astype(np.float32)
+    for t in range(tokens):
+        order = np.argsort(-lg[t])
+        if case == "ties_below":
+            lg[t, order[6:]] = lg[t, order[6]]
+        elif case == "tie_inside":
+            lg[t, order[1]] = lg[t, order[0]]
+        elif case == "signed_zero":
+            lg[t] = -np.abs(lg[t]) - 1.0
+            lg[t, 5], lg[t, 9] = np.float32(-0.0), np.float32(0.0)
+        elif case == "nan_rest":
+            lg[t, order[-1]] = np.nan
+        elif case == "nan_first":
+            lg[t, 0] = np.nan
+    return lg
+
+
+@pytest.mark.parametrize("case", ["distinct", "ties_below", "tie_inside", "signed_zero",
+                                  "nan_rest", "nan_first"])
+@pytest.mark.parametrize("tokens,path", [(1, "stream"), (2, "stream"), (3, "grouped"),
+                                         (40, "grouped")])
+def test_routing_selection_paths(ctx, monkeypatch, case, tokens, path):
+    """Device routing equals Router.select (the oracle) for inputs that take the
+    fast selection and for those that fall back to the exact sort: decode
+    (fused into gate_up, one and two tokens), the grouping kernel (3 tokens)
+    and the prefill route kernel (40 tokens)."""
+    shape = SMALL
+    H, E, K = shape["hidden"], 64, 4
+    layout, experts_d, buf = _make_layer(ctx, shape, E, 1200)
+    monkeypatch.setenv("GODWIT_PREFILL_ABOVE", "8" if path == "stream" else "1")
+    runner = gw.ExpertRunner(ctx, H, shape["inter"], shape["act"])
+    logits = _routing_logits(case, tokens, E)
+    xbits, _ = normal_bf16(rng(1201), tokens * H)
+    lb, xb = ctx.buffer(logits), ctx.buffer(xbits)
+    out = ctx.empty(tokens * H * 4)
+    ids_b, w_b = ctx.empty(tokens * K * 4), ctx.empty(tokens * K * 4)
+    runner.layer_forward(buf.ptr, layout.stride, E, K, xb.ptr, gw.BF16, tokens, out.ptr,
+                         logits=lb.ptr, routing_ids=ids_b.ptr, routing_weights=w_b.ptr)
+    ctx.synchronize()
+    ids = ids_b.download(np.int32, tokens * K).reshape(tokens, K)
+    wts = w_b.download(np.float32, tokens * K).reshape(tokens, K)
+    for t in range(tokens):
+        rid, rw = oracle.router_select(logits[t], K)
+        assert list(ids[t]) == list(rid), (case, t, list(ids[t]), list(rid))
+        assert np.allclose(wts[t], rw, rtol=1e-6, atol=1e-7, equal_nan=True), (case, t)
+    for b in (lb, xb, out, ids_b, w_b, buf):
+        b.free()
+    runner.close()
+
+
 def test_layer_graph_replay_matches_eager(ctx):
     """A captured 3-layer chain replayed several times equals the eager result each time."""
     shape = SMALL
