@@ -265,7 +265,7 @@ def prefill_bench(gw, args) -> int:
         "us_per_layer": round(dt * 1e6, 2), "hbm_gbs": round(nbytes / dt / 1e9, 1),
         "tflops_algorithmic": round(flops / dt / 1e12, 2),
         "tflops_matrix_core": round(mfma_flops / dt / 1e12, 2),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "compute": "e2m1 weights widened exactly to bf16 (scale folded), bf16 x, fp32 MFMA",
         "data": "synthetic (seeded MXFP4, Zipf(1.1) top-4 routing, x N(0,1) bf16)",
         "config": {"workload": "gptoss120b-moe-layer-prefill-512", "tokens": T, "experts": E,
@@ -391,8 +391,8 @@ def qwen3_bench(gw, args, batch: int) -> int:
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
         "us_per_token": round(dt * 1e6 / batch, 2), "hbm_frac_of_peak": round(value / PEAK_HBM_GBS, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4",
-        "compute": "e2m1 weights x bf16 activations, fp32 accumulation",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "compute": "e2m1 weights (MXFP4, exact) x bf16 activations, fp32 products and sums",
         "data": "synthetic (seeded MXFP4, zero bias sections, logits N(0,1) per token and layer)",
         "config": {"workload": f"qwen3-moe-stack-decode-b{batch}", "layers": Lq, "experts": Eq,
                    "top_k": Kq, "hidden": Hq, "intermediate": Fq, "batch": batch,
@@ -556,13 +556,13 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "mxfp4",
-        "compute": "e2m1 weights x bf16/fp16 activations, fp32 accumulation",
+        "dtype": "f32",
+        "compute": "e2m1 weights (MXFP4, exact) x bf16 activations, fp32 products and sums",
         "data": "synthetic (seeded MXFP4 nibbles U{0..15}, scales U{119..127}, "
                 "biases N(0,0.02) bf16, logits N(0,1) per token)",
-        "config": {"workload": "gptoss120b-moe-stack-decode", "model": "GPT-OSS-120B MoE blocks",
-                   "layers": L, "experts": E, "top_k": K, "hidden": H, "intermediate": F,
-                   "global_batch": 1, "seq_len": 1, "parallelism": "single-gpu",
+        "config": {"workload": "gptoss120b-moe-stack-decode", "layers": L, "experts": E,
+                   "top_k": K, "hidden": H, "intermediate": F, "tokens_per_step": 1,
+                   "parallelism": "single-gpu",
                    "bytes_per_token": bytes_token, "resident_bytes": L * lay.layer_file_size},
         "kernels": kernels,
         "roofline": roofline,
