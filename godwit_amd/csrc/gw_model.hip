@@ -189,7 +189,12 @@ struct gw_model {
     std::string dir;
     gw_model_info info;
     std::vector<int> fds;   // per layer, opened on first use (-1: not yet)
+    // Two pinned staging buffers of kStageBytes for read_to_device, allocated
+    // on the first load and kept until gw_model_close (pinning is slow).
+    void *stage[2] = {nullptr, nullptr};
 };
+
+static constexpr size_t kStageBytes = (size_t)32 << 20;
 
 static std::string layer_path(const gw_model *m, int layer)
 {
@@ -303,6 +308,8 @@ extern "C" int gw_model_close(gw_model *m)
     if (!m) return GW_OK;
     for (int fd : m->fds)
         if (fd >= 0) close(fd);
+    for (void *p : m->stage)
+        if (p) (void)hipHostFree(p);
     delete m;
     return GW_OK;
 }
@@ -356,17 +363,17 @@ static int layer_fd(gw_model *m, int layer, int &fd)
 static int read_to_device(gw_context *ctx, gw_model *m, int layer, int64_t offset,
                           int64_t length, void *dst)
 {
-    constexpr size_t kChunk = (size_t)32 << 20;
+    constexpr size_t kChunk = kStageBytes;
     int fd = -1;
     int rc = layer_fd(m, layer, fd);
     if (rc != GW_OK) return rc;
     hipStream_t stream = static_cast<hipStream_t>(gw_context_stream(ctx));
-    void *stage[2] = {nullptr, nullptr};
+    void **stage = m->stage;
     hipEvent_t done[2] = {nullptr, nullptr};
     bool pending[2] = {false, false};
     hipError_t e = hipSuccess;
     for (int i = 0; i < 2 && e == hipSuccess; ++i) {
-        e = hipHostMalloc(&stage[i], kChunk, hipHostMallocDefault);
+        if (!stage[i]) e = hipHostMalloc(&stage[i], kChunk, hipHostMallocDefault);
         if (e == hipSuccess) e = hipEventCreateWithFlags(&done[i], hipEventDisableTiming);
     }
     int64_t filled = 0;
@@ -407,10 +414,8 @@ static int read_to_device(gw_context *ctx, gw_model *m, int layer, int64_t offse
             const hipError_t w = hipEventSynchronize(done[i]);
             if (e == hipSuccess) e = w;
         }
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 2; ++i)
         if (done[i]) (void)hipEventDestroy(done[i]);
-        if (stage[i]) (void)hipHostFree(stage[i]);
-    }
     if (rc != GW_OK) return rc;
     if (e != hipSuccess)
         return gw::set_error(e == hipErrorOutOfMemory ? GW_ERR_OOM : GW_ERR_HIP,

@@ -298,7 +298,10 @@ int gw_moe_prefill_forward(gw_expert_runner *runner, const gw_moe_layer_args *ar
  * gw_model_load_layer / _load_expert replace ModelReader.loadExpertStride and
  * read (:72-110): pread into pinned staging, copied to HBM by the context's
  * stream; they return when the bytes are on the device.  The loaded layer is
- * the experts_base of gw_moe_layer_forward, unchanged bytes. */
+ * the experts_base of gw_moe_layer_forward, unchanged bytes.  A gw_model keeps
+ * its two 32 MiB pinned staging buffers from the first load until
+ * gw_model_close, so loads through one handle must not overlap (use one handle
+ * per loading thread). */
 #define GW_GWT_FORMAT_VERSION 2
 
 typedef struct gw_model gw_model;
