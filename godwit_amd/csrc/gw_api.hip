@@ -562,7 +562,7 @@ struct gw_expert_runner {
     int pf_tokens = 0, pf_topk = 0, pf_experts = 0;
     void *pf_buf = nullptr;
     bool fused_enabled = false;      // GODWIT_FUSED_LAYER=1 at creation turns it on
-    int prefill_above = 2;           // batches larger than this run the grouped GEMMs
+    int prefill_above = 1;           // batches larger than this run the grouped GEMMs
     int ring_next = 0;
     int ring_used = 0;
 };
@@ -638,7 +638,7 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     }
     const char *env = getenv("GODWIT_FUSED_LAYER");
     r->fused_enabled = env && env[0] == '1';
-    const int pa = get_env_int("GODWIT_PREFILL_ABOVE", 2);
+    const int pa = get_env_int("GODWIT_PREFILL_ABOVE", 1);
     r->prefill_above = pa < 1 ? 1 : pa > gw::kMaxTokens ? gw::kMaxTokens : pa;
     *out = r;
     return GW_OK;
@@ -945,7 +945,7 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
 // which read each selected expert once per token group of a workgroup, or the
 // grouped GEMMs, which read each distinct expert once for the whole batch but
 // pay for routing, grouping and combining in kernels of their own.  Above
-// prefill_above tokens (GODWIT_PREFILL_ABOVE at creation, default 2) the
+// prefill_above tokens (GODWIT_PREFILL_ABOVE at creation, default 1) the
 // grouped GEMMs win; they are taken when the shape is one they accept and,
 // under graph capture, when their scratch is already large enough.
 static bool batch_takes_grouped_gemm(const gw_expert_runner *r, const gw_moe_layer_args *a)

@@ -247,7 +247,7 @@ int gw_expert_apply_assignments_async(gw_expert_runner *runner, const void *inpu
  * out [tokens, hidden] fp32 is overwritten with the combined expert output
  * (the residual add stays with the caller, :232-238).  Batches of more than
  * 8 tokens run the grouped GEMMs of gw_moe_prefill_forward; so do batches of
- * 3..8 tokens (more than GODWIT_PREFILL_ABOVE at runner creation, default 2)
+ * 2..8 tokens (more than GODWIT_PREFILL_ABOVE at runner creation, default 1)
  * when hidden and intermediate sizes are multiples of 32 and >= 128, x is
  * 16-byte aligned, there are at most 256 experts and, during graph capture,
  * the prefill scratch is already reserved.  Enqueue only. */

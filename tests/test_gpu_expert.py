@@ -269,7 +269,7 @@ def test_layer_given_logits_128_experts(ctx):
                                          (3, "grouped"), (8, "grouped")])
 def test_layer_qwen3_decode(ctx, monkeypatch, tokens, path):
     """BASELINE config 3 layer: Qwen3 shape, top-8 of 128, no biases, SiLU-GLU, batch 1/8.
-    A batch of 3..8 tokens takes the grouped GEMMs by default; GODWIT_PREFILL_ABOVE=8
+    A batch of 2..8 tokens takes the grouped GEMMs by default; GODWIT_PREFILL_ABOVE=8
     at runner creation keeps it on the streaming decode kernels."""
     monkeypatch.setenv("GODWIT_PREFILL_ABOVE", "8" if path == "stream" else "2")
     got, _, ids, wts, ref, rids, rw = _layer_case(ctx, QWEN3, 128, 8, tokens, 800 + tokens,
