@@ -135,6 +135,192 @@ def counter_pass(gw, args) -> int:
     return 0
 
 
+def gemv_bench(gw, args) -> int:
+    """one MXFP4 GEMV at the GPT-OSS-120B gate_up shape, y =
+    dequant(W) x + b, W 5760 x 2880 (nibbles U{0..15}, scales U{119..127}), x fp32
+    N(0,1), b fp32 N(0, 0.02).  128 distinct weight copies (1.13 GB) are cycled
+    so no launch finds its weights in the 256 MB MALL.  Reports GB/s of the
+    launch's algorithmic bytes (8,870,400: packed + scales + x + bias + y) and
+    the oracle's scalar GEMV timed on the host beside it."""
+    rows, cols, ncopy = 2 * F, H, 128
+    pbytes, sbytes = rows * cols // 2, rows * cols // 32
+    ctx = gw.Context(0)
+    wbuf = ctx.empty(ncopy * (pbytes + sbytes))
+    ctx.fill_uniform_u8(wbuf, 0, 255, args.seed * 7 + 1, offset=0, count=ncopy * pbytes)
+    ctx.fill_uniform_u8(wbuf, 119, 127, args.seed * 7 + 2, offset=ncopy * pbytes,
+                        count=ncopy * sbytes)
+    xb, bb, yb = ctx.empty(cols * 4), ctx.empty(rows * 4), ctx.empty(rows * 4)
+    ctx.fill_normal(xb, gw.F32, cols, 0.0, 1.0, args.seed * 7 + 3)
+    ctx.fill_normal(bb, gw.F32, rows, 0.0, 0.02, args.seed * 7 + 4)
+    ctx.synchronize()
+
+    class View:   # a copy's packed / scales sections as DeviceBuffer-like views
+        def __init__(self, ptr):
+            self.ptr = ptr
+
+    def launch(i):
+        k = i % ncopy
+        gw.mxfp4_gemv_bias(ctx, View(wbuf.address(k * pbytes)),
+                           View(wbuf.address(ncopy * pbytes + k * sbytes)), bb, gw.F32, xb,
+                           gw.F32, yb, rows, cols)
+
+    for i in range(args.warmup):
+        launch(i)
+    ctx.synchronize()
+    n = args.steps * 20
+    t0 = time.perf_counter()
+    for i in range(n):
+        launch(args.warmup + i)
+    ctx.synchronize()
+    dt = (time.perf_counter() - t0) / n
+    ctx.set_profiling(True)
+    ctx.profile_reset()
+    for i in range(n):
+        launch(i)
+    ctx.synchronize()
+    ms, cnt = ctx.profile("gemv")
+    ctx.set_profiling(False)
+    k_us = ms / cnt * 1e3
+    nbytes = pbytes + sbytes + cols * 4 + rows * 4 + rows * 4
+    value = nbytes / (k_us * 1e-6) / 1e9
+    log(f"gemv {rows}x{cols}: {k_us:.2f} us per launch (HIP events), {dt * 1e6:.2f} us "
+        f"per launch back to back, {value:.0f} GB/s ({value / PEAK_HBM_GBS * 100:.1f}% of "
+        f"{PEAK_HBM_GBS:.0f})")
+    cpu = None
+    if args.cpu_seconds > 0:
+        import oracle
+        r = np.random.default_rng(5)
+        packed = r.integers(0, 256, pbytes, dtype=np.uint8)
+        scales = r.integers(119, 128, sbytes, dtype=np.uint8)
+        x = r.standard_normal(cols).astype(np.float32)
+        bias = (r.standard_normal(rows) * 0.02).astype(np.float32)
+        calls, c0 = 0, time.perf_counter()
+        while time.perf_counter() - c0 < args.cpu_seconds:
+            oracle.gemv_bias(packed, scales, bias, x, rows, cols)
+            calls += 1
+        c_us = (time.perf_counter() - c0) / calls * 1e6
+        cpu = {"value": round(nbytes / (c_us * 1e-6) / 1e9, 4), "unit": "GB/s",
+               "us_per_gemv": round(c_us, 1), "cores": 1, "kind": "port",
+               "sample": f"{calls} GEMVs of the same shape (one weight set), scalar C oracle "
+                         f"(referenceMXFP4 + bias), 1 thread"}
+        log(f"cpu baseline: {c_us:.0f} us per GEMV")
+    print(json.dumps({
+        "metric": "HBM GB/s (% of peak), MXFP4 GEMV at the GPT-OSS-120B gate_up shape",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": n,
+        "warmup": args.warmup, "ms_per_step": round(k_us * 1e-3, 5),
+        "us_per_gemv_back_to_back": round(dt * 1e6, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "compute": "e2m1 weights (MXFP4, exact) x fp32 x, fp32 products and sums",
+        "data": "synthetic (seeded MXFP4 nibbles U{0..15}, scales U{119..127}, x N(0,1), "
+                "bias N(0,0.02) fp32; 128 weight copies cycled)",
+        "config": {"workload": "gptoss-gate_up-gemv", "rows": rows, "cols": cols,
+                   "weight_copies": ncopy, "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(value / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "gemv_kernel (MXFP4 GEMV + bias)", "bytes_per_launch": nbytes,
+                     "avg_launch_us": round(k_us, 3)},
+        "cpu_baseline": cpu}), flush=True)
+    ctx.close()
+    return 0
+
+
+def gptoss20b_bench(gw, args) -> int:
+    """one GPT-OSS-20B-shaped MoE layer at batch 1 with its fp32
+    router on the device: 32 experts (hidden 2880), router weights fp32 [32 x 2880]
+    N(0, 0.02), x bf16 N(0,1), top-4, softmax over the 4, SwiGLU (1.702, 7.0),
+    weighted sum.  Four copies of the layer (1.7 GB) run in turn, each step's
+    output feeding the next layer's input, so no copy stays in the MALL.  Reports
+    us per layer and GB/s of algorithmic bytes (4 experts + router + x + out)."""
+    E20, ncopy = 32, 4
+    ctx = gw.Context(0)
+    lay = gw.ExpertLayout(H, F, E20)
+    runner = gw.ExpertRunner(ctx, H, F, "gptOssClampedGLU", 7.0, 1.702)
+    o, sz = lay.offsets, lay.sizes
+    layers, routers = [], []
+    for l in range(ncopy):
+        buf = ctx.empty(lay.layer_file_size)
+        sd = args.seed * 1000003 + l * 7919
+        ctx.fill_uniform_u8(buf, 0, 255, sd)
+        for e in range(E20):
+            base = e * lay.stride
+            ctx.fill_uniform_u8(buf, 119, 127, sd * 131 + 4 * e + 1,
+                                offset=base + o["gate_up_scales"], count=sz["gate_up_scales"])
+            ctx.fill_uniform_u8(buf, 119, 127, sd * 131 + 4 * e + 2,
+                                offset=base + o["down_scales"], count=sz["down_scales"])
+            ctx.fill_normal(buf, gw.BF16, 2 * F, 0.0, 0.02, sd * 131 + 4 * e + 3,
+                            offset=base + o["gate_up_bias"])
+            ctx.fill_normal(buf, gw.BF16, H, 0.0, 0.02, sd * 131 + 4 * e + 4,
+                            offset=base + o["down_bias"])
+        rw = ctx.empty(E20 * H * 4)
+        ctx.fill_normal(rw, gw.F32, E20 * H, 0.0, 0.02, sd * 17 + 5)
+        layers.append(buf)
+        routers.append(rw)
+    xs = [ctx.empty(H * 2) for _ in range(ncopy + 1)]
+    ctx.fill_normal(xs[0], gw.BF16, H, 0.0, 1.0, args.seed * 31 + 9)
+    out = ctx.empty(H * 4)
+    ctx.synchronize()
+
+    def step():
+        for l in range(ncopy):
+            runner.layer_forward(layers[l].ptr, lay.stride, E20, K, xs[l].ptr, gw.BF16, 1,
+                                 out.ptr, router_weight=routers[l].ptr,
+                                 router_weight_dtype=gw.F32, out_bf16=xs[(l + 1) % ncopy].ptr)
+
+    graph = gw.Graph.capture(ctx, step)
+    for _ in range(args.warmup):
+        graph.launch()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.launch()
+    ctx.synchronize()
+    dt = (time.perf_counter() - t0) / (args.steps * ncopy)
+    kernels = {}
+    if not args.no_profile_pass:
+        ctx.set_profiling(True)
+        ctx.profile_reset()
+        for _ in range(args.steps):
+            step()
+        ctx.synchronize()
+        for name in ("router", "gate_up", "down"):
+            ms, n = ctx.profile(name)
+            if n:
+                kernels[name] = {"launches": n, "avg_us": ms / n * 1e3}
+        ctx.set_profiling(False)
+        log("kernels: " + ", ".join(f"{k} {v['avg_us']:.2f} us" for k, v in kernels.items()))
+    nbytes = K * expert_bytes(lay) + E20 * H * 4 + H * 2 + H * 4 + H * 2
+    value = nbytes / dt / 1e9
+    log(f"gpt-oss-20b layer: {dt * 1e6:.2f} us per layer, {value:.0f} GB/s "
+        f"({value / PEAK_HBM_GBS * 100:.1f}% of {PEAK_HBM_GBS:.0f})")
+    roof = None
+    if "gate_up" in kernels:
+        ach = gate_up_bytes(lay) / (kernels["gate_up"]["avg_us"] * 1e-6) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": "gate_up_kernel (fused MXFP4 gate_up GEMV + bias + SwiGLU)",
+                "bytes_per_launch": gate_up_bytes(lay),
+                "avg_launch_us": round(kernels["gate_up"]["avg_us"], 3)}
+    print(json.dumps({
+        "metric": "HBM GB/s (% of peak) + us/layer, GPT-OSS-20B MXFP4 MoE layer with its "
+                  "router, batch 1",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * ncopy * 1e3, 4),
+        "us_per_layer": round(dt * 1e6, 2), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "compute": "e2m1 weights (MXFP4, exact) x bf16 activations, fp32 products and sums; "
+                   "fp32 router",
+        "data": "synthetic (seeded MXFP4, biases N(0,0.02) bf16, router fp32 N(0,0.02), "
+                "x N(0,1) bf16)",
+        "config": {"workload": "gptoss20b-moe-layer-decode", "experts": E20, "top_k": K,
+                   "hidden": H, "intermediate": F, "layer_copies": ncopy,
+                   "parallelism": "single-gpu"},
+        "kernels": kernels, "roofline": roof, "cpu_baseline": None}), flush=True)
+    graph.destroy()
+    runner.close()
+    ctx.close()
+    return 0
+
+
 def cpu_baseline(seconds: float) -> dict:
     """The oracle (scalar C port of the reference CPU path: referenceMXFP4 + bias,
     gptoss activation with fp16 rounding, Router.select, sequential combine) on
@@ -419,11 +605,14 @@ def main() -> int:
                          "scales the counters to bytes)")
     ap.add_argument("--batch", type=int, default=None,
                     help="tokens per step for the qwen3 workloads (default 1, or 8 for qwen3-b8)")
-    ap.add_argument("--workload", choices=["decode", "prefill", "qwen3", "qwen3-b8"],
+    ap.add_argument("--workload", choices=["decode", "prefill", "qwen3", "qwen3-b8", "gemv",
+                                           "gptoss20b"],
                     default="decode",
                     help="decode: BASELINE config 2 (the headline line, default); prefill: "
                          "config 4, one GPT-OSS-120B layer, 512 Zipf-routed tokens; qwen3 / "
-                         "qwen3-b8: config 3, the Qwen3 stack at batch 1 / 8")
+                         "qwen3-b8: config 3, the Qwen3 stack at batch 1 / 8; gemv: config 0, "
+                         "one gate_up-shaped GEMV; gptoss20b: config 1, a 20B layer with its "
+                         "router")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -438,6 +627,10 @@ def main() -> int:
         return counter_pass(gw, args)
     if args.workload == "prefill":
         return prefill_bench(gw, args)
+    if args.workload == "gemv":
+        return gemv_bench(gw, args)
+    if args.workload == "gptoss20b":
+        return gptoss20b_bench(gw, args)
     if args.workload in ("qwen3", "qwen3-b8"):
         batch = args.batch or (8 if args.workload == "qwen3-b8" else 1)
         return qwen3_bench(gw, args, batch)

@@ -339,6 +339,7 @@ __device__ __forceinline__ void copy_plan(Plan *dst, const Plan *src)
 }
 
 constexpr int kFusedRouteR = 4;      // fused routing handles up to 256 experts
+constexpr int kMaxRouterTokens = 8;  // token rows per router_rows_kernel workgroup
 constexpr int kMaxExperts = 1024;    // the standalone route kernel, up to 1024
 
 // ---------------------------------------------------------------------------
@@ -631,6 +632,76 @@ __global__ __launch_bounds__(256) void router_kernel(const void *__restrict__ W,
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
     if (lane == 0) logits[(int64_t)t * E + e] = acc + (b ? load_as_f32(b, b_dt, e) : 0.0f);
+}
+
+// Eight consecutive elements as fp32 from a 16-byte aligned position (one
+// 16-byte load for 16-bit data, two for fp32).
+template <int DT>
+__device__ __forceinline__ void load8_f32(const void *p, int64_t i, float (&v)[8])
+{
+    if constexpr (DT == DT_F32) {
+        const float4 *q = reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
+        const float4 a = q[0], c = q[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+    } else {
+        const uint4 a = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i);
+        const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint16_t lo = (uint16_t)(w[k] & 0xFFFFu), hi = (uint16_t)(w[k] >> 16);
+            v[2 * k] = DT == DT_BF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+            v[2 * k + 1] = DT == DT_BF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+        }
+    }
+}
+
+// Router logits, wide form: workgroup (e, token block) reads expert e's
+// weight row in 8-element units (16-byte loads, all units of a thread in
+// flight together) and dots it with up to 8 token rows; the per-thread sums
+// are reduced across the workgroup.  Needs H % 8 == 0 and 16-byte aligned
+// rows; router_kernel covers the rest.
+template <int WDT, int XDT>
+__global__ __launch_bounds__(256) void router_rows_kernel(const void *__restrict__ W,
+                                                          const void *__restrict__ b, int b_dt,
+                                                          const void *__restrict__ x,
+                                                          float *__restrict__ logits, int E,
+                                                          int H, int T)
+{
+    __shared__ float red[4][kMaxRouterTokens];
+    const int e = blockIdx.x, t0 = blockIdx.y * kMaxRouterTokens;
+    const int nt = min(kMaxRouterTokens, T - t0);
+    const int H8 = H >> 3;
+    float acc[kMaxRouterTokens];
+#pragma unroll
+    for (int t = 0; t < kMaxRouterTokens; ++t) acc[t] = 0.0f;
+    for (int u = (int)threadIdx.x; u < H8; u += 256) {
+        float w[8];
+        load8_f32<WDT>(W, (int64_t)e * H + 8 * u, w);
+#pragma unroll
+        for (int t = 0; t < kMaxRouterTokens; ++t) {
+            if (t < nt) {
+                float xv[8];
+                load8_f32<XDT>(x, (int64_t)(t0 + t) * H + 8 * u, xv);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[t] += w[k] * xv[k];
+            }
+        }
+    }
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int t = 0; t < kMaxRouterTokens; ++t) {
+        float v = acc[t];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+        if (lane == 0) red[wv][t] = v;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < nt) {
+        const int t = threadIdx.x;
+        const float sum = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
+        logits[(int64_t)(t0 + t) * E + e] = sum + (b ? load_as_f32(b, b_dt, e) : 0.0f);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1264,6 +1335,25 @@ hipError_t launch_router(const Launch &L, const void *W, int w_dt, const void *b
 {
     const int waves = experts * tokens;
     if (waves == 0) return hipSuccess;
+    const bool wide = hidden % 8 == 0 && ((uintptr_t)W & 15u) == 0 &&
+                      ((uintptr_t)x & 15u) == 0 && div_up(tokens, kMaxRouterTokens) <= 65535;
+    if (wide) {
+        const dim3 grid(experts, div_up(tokens, kMaxRouterTokens));
+        auto go = [&](auto wdt, auto xdt) {
+            constexpr int WD = decltype(wdt)::value, XD = decltype(xdt)::value;
+            GW_LAUNCH((router_rows_kernel<WD, XD>), grid, dim3(256), 0, L, W, b, b_dt, x, logits,
+                      experts, hidden, tokens);
+        };
+        auto with_x = [&](auto wdt) {
+            if (x_dt == DT_F32) go(wdt, std::integral_constant<int, DT_F32>{});
+            else if (x_dt == DT_F16) go(wdt, std::integral_constant<int, DT_F16>{});
+            else go(wdt, std::integral_constant<int, DT_BF16>{});
+        };
+        if (w_dt == DT_F32) with_x(std::integral_constant<int, DT_F32>{});
+        else if (w_dt == DT_F16) with_x(std::integral_constant<int, DT_F16>{});
+        else with_x(std::integral_constant<int, DT_BF16>{});
+        return hipGetLastError();
+    }
     GW_LAUNCH(router_kernel, dim3(div_up(waves, 4)), dim3(256), 0, L, W, w_dt, b, b_dt, x, x_dt,
               logits, experts, hidden, tokens);
     return hipGetLastError();
