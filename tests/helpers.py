@@ -46,6 +46,21 @@ def expert_metric(got, ref):
     return float(np.max(np.abs(got - ref)) / max(np.mean(np.abs(ref)), 1e-30))
 
 
+def layer_check(got, ref):
+    """runLayerCheck's acceptance (GodwitCLI/main.swift:697-718), applied to a
+    layer's output: relative RMS error < 2e-3 and every |error| below
+    4 * max|ref| * 2^-11 (four fp16 ulps at the output's peak).  Returns
+    (relative_rms, worst_abs, bound_abs, passed)."""
+    got = np.asarray(got, np.float64).ravel()
+    ref = np.asarray(ref, np.float64).ravel()
+    rms = max(float(np.sqrt(np.mean(ref * ref))), 1e-6)
+    err = np.abs(got - ref)
+    rel_rms = float(np.sqrt(np.mean(err * err))) / rms
+    worst = float(np.max(err))
+    bound = 4.0 * float(np.max(np.abs(ref))) * 2.0 ** -11
+    return rel_rms, worst, bound, rel_rms < 2e-3 and worst < bound
+
+
 class ExpertData:
     """One expert's sections as host arrays, plus its bytes in the .gwt stride layout."""
 

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import expert_metric, gemv_metric
+from helpers import expert_metric, gemv_metric, layer_check
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 sys.path.insert(0, GOLDEN)
@@ -163,6 +163,8 @@ def test_gpu_layer_fixture(ctx, monkeypatch, name, path):
                        rtol=1e-6, atol=1e-7)
     for t in range(T):
         assert expert_metric(got[t], z["expected"][t]) < 1e-3, t
+    rel_rms, worst, bound, ok = layer_check(got, z["expected"])
+    assert ok, (rel_rms, worst, bound)
     for b in (xb, lb, out, ids_b, w_b, buf):
         b.free()
     runner.close()

@@ -10,7 +10,7 @@ import pytest
 
 import godwit_amd as gw
 import oracle
-from helpers import ExpertData, expert_metric, gemv_metric, normal_bf16, rng
+from helpers import ExpertData, expert_metric, gemv_metric, layer_check, normal_bf16, rng
 
 pytestmark = pytest.mark.gpu
 
@@ -258,11 +258,15 @@ def test_layer_config1_gptoss20b_router(ctx):
 
 
 def test_layer_given_logits_128_experts(ctx):
-    """BASELINE config 2 layer: 128 experts, logits ~ N(0,1), top-4."""
+    """BASELINE config 2 layer: 128 experts, logits ~ N(0,1), top-4.  Also the
+    reference's own layer acceptance (check-layer: routing exact, relative RMS
+    < 2e-3, max error < 4 fp16 ulps of the peak)."""
     got, _, ids, wts, ref, rids, rw = _layer_case(ctx, GPTOSS, 128, 4, 1, 700, router=False)
     assert np.array_equal(ids, rids)
     assert np.allclose(wts, rw, rtol=1e-6, atol=1e-7)
     _close(got[0], ref[0])
+    rel_rms, worst, bound, ok = layer_check(got, ref)
+    assert ok, (rel_rms, worst, bound)
 
 
 @pytest.mark.parametrize("tokens,path", [(1, "stream"), (3, "stream"), (8, "stream"),
@@ -277,6 +281,8 @@ def test_layer_qwen3_decode(ctx, monkeypatch, tokens, path):
     assert np.array_equal(ids, rids)
     for t in range(tokens):
         _close(got[t], ref[t])
+    rel_rms, worst, bound, ok = layer_check(got, ref)
+    assert ok, (rel_rms, worst, bound)
 
 
 @pytest.mark.parametrize("experts,top_k,tokens,path", [(128, 8, 8, "stream"), (64, 4, 3, "stream"),

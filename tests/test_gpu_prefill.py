@@ -15,7 +15,7 @@ import pytest
 
 import godwit_amd as gw
 import oracle
-from helpers import expert_metric, normal_bf16, rng
+from helpers import expert_metric, layer_check, normal_bf16, rng
 from test_gpu_expert import GPTOSS, QWEN3, SMALL, _make_layer
 
 pytestmark = pytest.mark.gpu
@@ -92,6 +92,8 @@ def test_prefill_matches_oracle(ctx, shape, E, K, T, x_dtype, seed):
     assert np.array_equal(ids, rids)
     assert np.allclose(wts, rw, rtol=1e-6, atol=1e-7)
     _close_batch(got, ref)
+    rel_rms, worst, bound, ok = layer_check(got, ref)       # check-layer's acceptance
+    assert ok, (rel_rms, worst, bound)
     assert np.array_equal(got16, oracle.f32_to_bf16_bits(got.ravel()))
     for b in (xb, lb, buf):
         b.free()
