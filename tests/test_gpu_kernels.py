@@ -205,6 +205,35 @@ def test_accumulate(ctx):
     db.free()
 
 
+class _At:
+    """A device address with the .ptr attribute the bindings read."""
+
+    def __init__(self, ptr):
+        self.ptr = ptr
+
+
+@pytest.mark.parametrize("E,H,shift", [(32, 2880, 0), (20, 100, 0), (16, 512, 2)],
+                         ids=["rows", "h100", "unaligned"])
+def test_router_logits_forms(ctx, E, H, shift):
+    """bf16_gemv_bias (router.metal:18-34) through both device forms: the
+    row-per-workgroup kernel (H % 8 == 0, 16-byte aligned rows) and the
+    one-wave-per-logit kernel it falls back to (H = 100; weights 2 bytes off
+    alignment)."""
+    r = rng(17 + H)
+    wbits = oracle.f32_to_bf16_bits((r.standard_normal(E * H) * 0.02).astype(np.float32))
+    bbits, bf = bias_bf16(r, E)
+    x16 = r.standard_normal(H).astype(np.float16)
+    store = np.zeros(E * H + 8, np.uint16)
+    store[shift // 2:shift // 2 + E * H] = wbits
+    wb, bb = ctx.buffer(store), ctx.buffer(bbits)
+    router = gw.Router(ctx, E, H, 4)
+    got = router.logits(x16, _At(wb.ptr + shift), bb)
+    ref = oracle.router_logits(oracle.bf16_bits_to_f32(wbits), bf, x16.astype(np.float32), E, H)
+    assert gemv_metric(got, ref) < 1e-5
+    wb.free()
+    bb.free()
+
+
 def test_router_logits(ctx):
     """bf16_gemv_bias (router.metal:18-34) for 128 experts, bf16 weights and bias."""
     r = rng(13)
