@@ -1196,7 +1196,7 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
         g.act_plane = (int64_t)T * K * r->inter;
         g.y_out = nullptr;
         ProfScope p(ctx, "prefill_gate_up");
-        GW_HIP(gw::launch_prefill_gemm(p.launch(L), true, planes, g, max_tiles));
+        GW_HIP(gw::launch_prefill_gemm(p.launch(L), true, planes, g, max_tiles, T * K));
     }
     {
         g.in = ps.act;
@@ -1211,7 +1211,7 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
         g.act_plane = 0;
         g.y_out = ps.y;
         ProfScope p(ctx, "prefill_down");
-        GW_HIP(gw::launch_prefill_gemm(p.launch(L), false, 2, g, max_tiles));
+        GW_HIP(gw::launch_prefill_gemm(p.launch(L), false, 2, g, max_tiles, T * K));
     }
     {
         ProfScope p(ctx, "prefill_combine");

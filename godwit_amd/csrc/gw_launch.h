@@ -92,7 +92,7 @@ struct PrefillGemm {
 };
 int prefill_max_tiles(int T, int K, int E);
 int prefill_planes(int in_dt);        // bf16 planes that hold a dtype exactly: 1, 2 or 3
-int prefill_gemm_lds_bytes(int planes, int kdim);
+int prefill_gemm_lds_bytes(int planes, int kdim, int waves);
 hipError_t launch_prefill_route(const Launch &L, const float *logits, int T, int E, int K,
                                 int32_t *ids, float *weights);
 // True when launch_prefill_group can route the batch itself (logits given).
@@ -105,8 +105,10 @@ hipError_t launch_prefill_group(const Launch &L, const float *logits, int T, int
                                 int32_t *tiles, int32_t *ntiles, int max_tiles);
 hipError_t launch_prefill_split(const Launch &L, const void *in, int in_dt, int64_t n,
                                 uint16_t *out);
+// tiles_hint: an upper bound on the work list's length (the entry count for
+// small batches), used to size the workgroups.
 hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const PrefillGemm &g,
-                               int max_tiles);
+                               int max_tiles, int tiles_hint);
 hipError_t launch_prefill_combine(const Launch &L, const float *y, const float *w, int T, int K,
                                   int H, float *out, uint16_t *out_bf16, int residual);
 

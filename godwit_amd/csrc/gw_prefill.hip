@@ -47,9 +47,6 @@ typedef const __attribute__((address_space(1))) u32x4v g_u32x4v;
 typedef const __attribute__((address_space(1))) uint8_t g_u8c;
 
 constexpr int kPT = 32;                 // tokens per tile (MFMA columns)
-constexpr int kPWaves = 8;              // waves per workgroup, 32 features each
-constexpr int kPThreads = 64 * kPWaves;
-constexpr int kPF = 32 * kPWaves;       // features per workgroup
 constexpr int kKC = 8;                  // 32-element blocks per staged activation chunk
 constexpr int kPrefillMaxExperts = 256;
 
@@ -232,17 +229,17 @@ constexpr int kPrefillLdsMax = 160 * 1024;
 
 // LDS layout of one GEMM workgroup (byte offsets): the kPT entry ids, the
 // [depth][planes] staged activation chunks (also the output tile at the end),
-// a copy of the workgroup's kPF rows of scale bytes (whole 1 KiB DMA pieces
+// a copy of the workgroup's 32 x waves rows of scale bytes (whole 1 KiB DMA pieces
 // from a 16-byte aligned start, plus room for reads one dword past the last
 // byte), and the bias tile.
 struct PrefillLds { int ring, scales, bias, total; };
-__host__ __device__ inline PrefillLds prefill_lds(int planes, int depth, int nb)
+__host__ __device__ inline PrefillLds prefill_lds(int planes, int depth, int nb, int waves)
 {
     PrefillLds l;
     l.ring = kPT * 4;
     l.scales = l.ring + depth * planes * kPlaneBytes;
-    l.bias = l.scales + ((kPF * nb + 32 + 1023) & ~1023);
-    l.total = l.bias + 1024;
+    l.bias = l.scales + ((32 * waves * nb + 32 + 1023) & ~1023);
+    l.total = l.bias + ((32 * waves * 4 + 1023) & ~1023);
     return l;
 }
 
@@ -293,9 +290,11 @@ template <int N> __device__ __forceinline__ void lds_wait()
     else static_assert(N == 0 || N == 2 || N == 3 || N == 4, "unsupported count");
 }
 
-template <int PL, bool GATE_UP>
-__global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
+template <int PL, bool GATE_UP, int W>
+__global__ __launch_bounds__(64 * W) void prefill_gemm_kernel(GemmArgs a)
 {
+    // W waves, 32 features each: a workgroup computes kF features x kPT entries.
+    constexpr int kF = 32 * W, kThreads = 64 * W;
     constexpr int D = PrefillDepth<PL>::value;
     constexpr int kNW = 4;                    // weight-ring loads per chunk (4 x 16 B)
     constexpr int kNX = 2 * PL;               // LDS-DMA loads per chunk per wave
@@ -307,7 +306,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
     uint8_t *lds8 = reinterpret_cast<uint8_t *>(plds);
     int *ent = reinterpret_cast<int *>(plds);
     const int nb = a.kdim >> 5;
-    const PrefillLds lay = prefill_lds(PL, D, nb);
+    const PrefillLds lay = prefill_lds(PL, D, nb, W);
     uint8_t *xring = lds8 + lay.ring;
     // Work unit -> (expert e, feature tile, entry tile m).  Units run expert by
     // expert, feature tile by feature tile, with the entry tiles of one
@@ -315,7 +314,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
     // weights run together; and each XCD (workgroup ids congruent mod 8) takes
     // one contiguous eighth of the units, so those workgroups share one L2.
     // floor(unit / nft) is always one of the unit's expert's tiles.
-    const int nft = (a.fdim + kPF - 1) / kPF;
+    const int nft = (a.fdim + kF - 1) / kF;
     const int units = *a.ntiles * nft;
     const int per = (units + 7) >> 3;
     const int jx = (int)(blockIdx.x >> 3);
@@ -336,7 +335,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int h = lane >> 5, c = lane & 31;
-    const int f0 = fidx * kPF;
+    const int f0 = fidx * kF;
     const int fbase = f0 + wave * 32;
     const int row = min(fbase + c, a.fdim - 1);       // clamped: rows past fdim are never stored
     const uint8_t *ex = a.experts_base + (int64_t)e * a.stride;
@@ -344,7 +343,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
 
     __syncthreads();                                  // ent[] is written
 
-    // The workgroup's scale bytes (rows f0 .. f0+255 are contiguous in the
+    // The workgroup's scale bytes (rows f0 .. f0+kF-1 are contiguous in the
     // scales section) and its bias tile, copied once by LDS-DMA in 1 KiB
     // pieces from a 16-byte aligned start; reads past a section's end
     // return zeros (buffer bounds).
@@ -353,26 +352,30 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
     {
         const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint8_t *>(ex + a.scales_off), (short)0, a.fdim * nb, 0x00020000);
-        const int ninst = (sshift + kPF * nb + 1023) >> 10;
-        for (int k = wave; k < ninst; k += kPWaves)
+        const int ninst = (sshift + kF * nb + 1023) >> 10;
+        for (int k = wave; k < ninst; k += W)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(sres, (l_void *)(lds8 + lay.scales + k * 1024),
                                                      16, s0 + k * 1024 + lane * 16, 0, 0, 0);
-        if (a.bias_dt >= 0 && wave == 0) {
-            const int esz = a.bias_dt == DT_F32 ? 4 : 2;
+        const int esz = a.bias_dt == DT_F32 ? 4 : 2;
+        if (a.bias_dt >= 0 && wave < (kF * esz + 1023) >> 10) {
             const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<uint8_t *>(ex + a.bias_off), (short)0, a.fdim * esz, 0x00020000);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (l_void *)(lds8 + lay.bias), 16,
-                                                     f0 * esz + lane * 16, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (l_void *)(lds8 + lay.bias + wave * 1024),
+                                                     16, f0 * esz + wave * 1024 + lane * 16, 0, 0,
+                                                     0);
         }
     }
 
-    // Staging: wave w copies rows 4w .. 4w+3 of each plane, two rows per DMA
-    // (lanes 0-31 row 4w+2n, lanes 32-63 the next); a lane's slot is lane & 31.
+    // Staging: wave w copies rows 4w' .. 4w'+3 of each plane (w' = w mod 8;
+    // waves past 8 repeat waves 0.. with the same bytes to the same slots, so
+    // every wave issues the same loads), two rows per DMA (lanes 0-31 row
+    // 4w'+2n, lanes 32-63 the next); a lane's slot is lane & 31.
+    const int sw = wave & 7;
     int64_t xrow[2];
     int xpiece[2];
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
-        const int t = 4 * wave + 2 * n + h;
+        const int t = 4 * sw + 2 * n + h;
         xpiece[n] = (lane & 31) ^ (t & 15);
         xrow[n] = (int64_t)(ent[t] / a.in_row_div) * a.kdim;
     }
@@ -391,7 +394,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
                 const int k = min(q * (kKC * 32) + xpiece[n] * 8, a.kdim - 8);
                 const uint32_t voff = (uint32_t)((p * a.in_plane + xrow[n] + k) * 2);
                 uint8_t *dst = xring + (size_t)(buf * PL + p) * kPlaneBytes +
-                               (4 * wave + 2 * n) * kRowBytes;
+                               (4 * sw + 2 * n) * kRowBytes;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (l_void *)dst, 16, voff, 0, 0, 0);
             }
         }
@@ -558,9 +561,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
                     : f16_bits_to_f32(reinterpret_cast<const uint16_t *>(lds8 + lay.bias)[rl]);
     }
     if constexpr (GATE_UP) {
-        // [2 planes][kPT entries][kPF/2 activations] bf16
+        // [2 planes][kPT entries][kF/2 activations] bf16
         uint16_t *tile = reinterpret_cast<uint16_t *>(xring);
-        constexpr int kCols = kPF / 2;
+        constexpr int kCols = kF / 2;
 #pragma unroll
         for (int v = 0; v < 16; v += 2) {
             const int rl = wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3);   // even: gate, +1: up
@@ -577,8 +580,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
         const int half = a.fdim >> 1;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            const int idx = (int)threadIdx.x + k * kPThreads;
-            const int p = idx >> 9, t = (idx >> 4) & 31, piece = idx & 15;
+            // 2 planes x kPT entries x kCols / 8 pieces = 2 kThreads
+            const int idx = (int)threadIdx.x + k * kThreads;
+            const int p = idx / (kPT * 2 * W), t = (idx / (2 * W)) % kPT, piece = idx % (2 * W);
             const int col0 = (f0 >> 1) + piece * 8;
             if (t < ntok && col0 + 8 <= half) {
                 const uint4 v = *reinterpret_cast<const uint4 *>(tile + (p * kPT + t) * kCols + piece * 8);
@@ -586,21 +590,22 @@ __global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(GemmArgs a)
             }
         }
     } else {
-        // [kPT entries][kPF rows] fp32
+        // [kPT entries][kF rows] fp32
         float *tile = reinterpret_cast<float *>(xring);
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int rl = wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-            tile[c * kPF + rl] = acc[v] + bv[v];
+            tile[c * kF + rl] = acc[v] + bv[v];
         }
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const int idx = (int)threadIdx.x + k * kPThreads;
-            const int t = idx >> 6, piece = idx & 63;
+            // kPT entries x kF / 4 pieces = 4 kThreads
+            const int idx = (int)threadIdx.x + k * kThreads;
+            const int t = idx / (8 * W), piece = idx % (8 * W);
             const int row0 = f0 + piece * 4;
             if (t < ntok && row0 + 4 <= a.fdim) {
-                const float4 v = *reinterpret_cast<const float4 *>(tile + t * kPF + piece * 4);
+                const float4 v = *reinterpret_cast<const float4 *>(tile + t * kF + piece * 4);
                 *reinterpret_cast<float4 *>(a.y_out + (int64_t)ent[t] * a.fdim + row0) = v;
             }
         }
@@ -683,12 +688,27 @@ hipError_t launch_prefill_group(const Launch &L, const float *logits, int T, int
 
 int prefill_planes(int in_dt) { return in_dt == DT_BF16 ? 1 : in_dt == DT_F16 ? 2 : 3; }
 
-int prefill_gemm_lds_bytes(int planes, int kdim)
+int prefill_gemm_lds_bytes(int planes, int kdim, int waves)
 {
     const int depth = planes == 1   ? PrefillDepth<1>::value
                       : planes == 2 ? PrefillDepth<2>::value
                                     : PrefillDepth<3>::value;
-    return prefill_lds(planes, depth, kdim / 32).total;
+    return prefill_lds(planes, depth, kdim / 32, waves).total;
+}
+
+// Waves per GEMM workgroup: 8 (256 features) by default, 12 (384 features)
+// when that needs fewer rounds of workgroups over the CUs in proportion to
+// their size — small batches, whose work list is a few dozen experts of one
+// tile each — and the LDS allows it.  `tiles_hint` bounds the work list.
+static int prefill_waves(int fdim, int kdim, int planes, int tiles_hint, int cus)
+{
+    auto cost = [&](int w) {
+        const int64_t units = (int64_t)tiles_hint * pdiv_up(fdim, 32 * w);
+        return (int64_t)pdiv_up(units, cus > 0 ? cus : 1) * w;
+    };
+    if (cost(12) < cost(8) && prefill_gemm_lds_bytes(planes, kdim, 12) <= kPrefillLdsMax)
+        return 12;
+    return 8;
 }
 
 hipError_t launch_prefill_split(const Launch &L, const void *in, int in_dt, int64_t n,
@@ -706,7 +726,7 @@ hipError_t launch_prefill_split(const Launch &L, const void *in, int in_dt, int6
 }
 
 hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const PrefillGemm &g,
-                               int max_tiles)
+                               int max_tiles, int tiles_hint)
 {
     // The staged rows are read 16 bytes at a time and the scale word 4 bytes
     // back from a row's end: K must be a multiple of 32 and at least 128.
@@ -740,26 +760,35 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
     a.act_kind = g.act_kind;
     a.limit = g.limit;
     a.alpha = g.alpha;
+    const int waves = prefill_waves(g.fdim, g.kdim, planes,
+                                    tiles_hint > 0 && tiles_hint < max_tiles ? tiles_hint : max_tiles,
+                                    L.cus);
     // One workgroup per (feature tile, tile) unit, rounded up to whole XCD
     // rounds; the kernel maps ids to units and retires the spare ones.
-    const dim3 grid((pdiv_up(g.fdim, kPF) * max_tiles + 7) / 8 * 8);
-    const int lds_bytes = prefill_gemm_lds_bytes(planes, g.kdim);
+    const dim3 grid((pdiv_up(g.fdim, 32 * waves) * max_tiles + 7) / 8 * 8);
+    const int lds_bytes = prefill_gemm_lds_bytes(planes, g.kdim, waves);
     if (lds_bytes > kPrefillLdsMax) return hipErrorInvalidValue;   // K too wide for the staging
     const size_t lds = (size_t)lds_bytes;
     hipError_t err = hipSuccess;
     auto go = [&](auto pl, auto gu) {
         constexpr int PL = decltype(pl)::value;
         constexpr bool GU = decltype(gu)::value;
-        // More than 64 KiB of dynamic LDS must be allowed explicitly, once per
-        // instantiation.
-        static bool lds_ok = false;
-        if (!lds_ok) {
-            err = hipFuncSetAttribute(reinterpret_cast<const void *>(&prefill_gemm_kernel<PL, GU>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, kPrefillLdsMax);
-            if (err != hipSuccess) return;
-            lds_ok = true;
-        }
-        GW_LAUNCH((prefill_gemm_kernel<PL, GU>), grid, dim3(kPThreads), lds, L, a);
+        auto with_waves = [&](auto wc) {
+            constexpr int W = decltype(wc)::value;
+            // More than 64 KiB of dynamic LDS must be allowed explicitly, once
+            // per instantiation.
+            static bool lds_ok = false;
+            if (!lds_ok) {
+                err = hipFuncSetAttribute(
+                    reinterpret_cast<const void *>(&prefill_gemm_kernel<PL, GU, W>),
+                    hipFuncAttributeMaxDynamicSharedMemorySize, kPrefillLdsMax);
+                if (err != hipSuccess) return;
+                lds_ok = true;
+            }
+            GW_LAUNCH((prefill_gemm_kernel<PL, GU, W>), grid, dim3(64 * W), lds, L, a);
+        };
+        if (waves == 12) with_waves(std::integral_constant<int, 12>{});
+        else with_waves(std::integral_constant<int, 8>{});
     };
     using P1 = std::integral_constant<int, 1>;
     using P2 = std::integral_constant<int, 2>;

@@ -285,6 +285,23 @@ def test_layer_qwen3_decode(ctx, monkeypatch, tokens, path):
     assert ok, (rel_rms, worst, bound)
 
 
+@pytest.mark.parametrize("shape,experts,top_k,tokens", [(GPTOSS, 16, 4, 3), (QWEN3, 128, 8, 5),
+                                                      (QWEN3, 128, 8, 8)],
+                         ids=["gptoss-gate_up-12-waves", "qwen3-down-12-waves",
+                              "qwen3-gate_up-12-waves"])
+def test_grouped_gemm_wide_workgroups(ctx, shape, experts, top_k, tokens):
+    """Small batches whose grouped GEMMs run 12-wave (384-feature) workgroups,
+    chosen when that takes one round of workgroups fewer: GPT-OSS gate_up at
+    12 entries, Qwen3 down at 40 entries, Qwen3 gate_up at 64 entries."""
+    got, _, ids, wts, ref, rids, rw = _layer_case(ctx, shape, experts, top_k, tokens,
+                                                  1500 + tokens, router=False)
+    assert np.array_equal(ids, rids)
+    for t in range(tokens):
+        _close(got[t], ref[t])
+    rel_rms, worst, bound, ok = layer_check(got, ref)
+    assert ok, (rel_rms, worst, bound)
+
+
 @pytest.mark.parametrize("experts,top_k,tokens,path", [(128, 8, 8, "stream"), (64, 4, 3, "stream"),
                                                         (300, 4, 2, "stream"),
                                                         (128, 8, 8, "grouped")])
