@@ -430,3 +430,33 @@ def test_layer_graph_replay_matches_eager(ctx):
     for b in xs + outs + [lb, buf]:
         b.free()
     runner.close()
+
+
+def _random_config(seed):
+    r = rng(5000 + seed)
+    H = int(r.choice([128, 160, 256, 384, 512]))
+    F = int(r.choice([128, 192, 256, 320]))
+    act, oact = (("gptOssClampedGLU", oracle.ACT_GPTOSS) if r.random() < 0.5
+                 else ("silu", oracle.ACT_SWIGLU))
+    E = int(r.integers(1, 40))
+    K = int(r.integers(1, min(8, E) + 1))
+    T = int(r.choice([1, 1, 2, 3, 5, 8, 13, 33]))
+    return dict(hidden=H, inter=F, act=act, oact=oact, bias=bool(r.random() < 0.7)), E, K, T
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_layer_random_configurations(ctx, seed):
+    """Seeded random shapes (hidden and intermediate multiples of 32 from 128 to
+    512, 1..39 experts, top-1..8, 1..33 tokens, either activation, with or
+    without biases) through gw_moe_layer_forward — the streaming kernels for one
+    token, the grouped GEMMs otherwise — against the oracle: routing exact,
+    outputs under the expert metric and the reference's layer acceptance."""
+    shape, E, K, T = _random_config(seed)
+    got, _, ids, wts, ref, rids, rw = _layer_case(ctx, shape, E, K, T, 5100 + seed,
+                                                  router=False)
+    assert np.array_equal(ids, rids), (shape["hidden"], shape["inter"], E, K, T)
+    assert np.allclose(wts, rw, rtol=1e-6, atol=1e-7)
+    for t in range(T):
+        _close(got[t], ref[t])
+    rel_rms, worst, bound, ok = layer_check(got, ref)
+    assert ok, (rel_rms, worst, bound, shape["hidden"], shape["inter"], E, K, T)
