@@ -77,7 +77,9 @@ def _run(ctx, runner, layout, buf, E, K, xb, x_dtype, lb, T, H, fn="prefill_forw
     (GPTOSS, 12, 4, 20, gw.F32, 3),      # three planes, 2880-wide K (11.25 chunks)
     (SMALL, 200, 4, 32, gw.BF16, 4),     # routed inside the group kernel, 4-wave expert scan
     (SMALL, 256, 8, 40, gw.BF16, 5),     # route kernel, then a scan over 256 experts
-], ids=["small-bf16", "qwen3-f16", "gptoss-f32", "small-e200-t32", "small-e256-t40"])
+    (SMALL, 8, 2, 2048, gw.BF16, 6),     # ~16 tiles per expert: many units per XCD eighth
+], ids=["small-bf16", "qwen3-f16", "gptoss-f32", "small-e200-t32", "small-e256-t40",
+        "small-e8-t2048"])
 def test_prefill_matches_oracle(ctx, shape, E, K, T, x_dtype, seed):
     H, F = shape["hidden"], shape["inter"]
     layout, experts, buf = _make_layer(ctx, shape, E, 2000 + seed)
