@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MXFP4 MoE expert hot path on one MI355X.
 
-Workload (the metric's "GPT-OSS-120B MXFP4 MoE layer,
+Workload (the benchmark definition config 2, the metric's "GPT-OSS-120B MXFP4 MoE layer,
 batch 1"): 36 MoE layers x 128 GPT-OSS-120B experts (hidden 2880,
 intermediate 2880, gate/up interleaved, bf16 biases in the .gwt stride layout),
 all resident in HBM (61.2 GB), decode batch 1, top-4 routing from per-layer
@@ -136,7 +136,7 @@ def counter_pass(gw, args) -> int:
 
 
 def gemv_bench(gw, args) -> int:
-    """one MXFP4 GEMV at the GPT-OSS-120B gate_up shape, y =
+    """Benchmark config 0: one MXFP4 GEMV at the GPT-OSS-120B gate_up shape, y =
     dequant(W) x + b, W 5760 x 2880 (nibbles U{0..15}, scales U{119..127}), x fp32
     N(0,1), b fp32 N(0, 0.02).  128 distinct weight copies (1.13 GB) are cycled
     so no launch finds its weights in the 256 MB MALL.  Reports GB/s of the
@@ -225,7 +225,7 @@ def gemv_bench(gw, args) -> int:
 
 
 def gptoss20b_bench(gw, args) -> int:
-    """one GPT-OSS-20B-shaped MoE layer at batch 1 with its fp32
+    """Benchmark config 1: one GPT-OSS-20B-shaped MoE layer at batch 1 with its fp32
     router on the device: 32 experts (hidden 2880), router weights fp32 [32 x 2880]
     N(0, 0.02), x bf16 N(0,1), top-4, softmax over the 4, SwiGLU (1.702, 7.0),
     weighted sum.  Four copies of the layer (1.7 GB) run in turn, each step's
@@ -362,7 +362,7 @@ PREFILL_T = 512
 
 def zipf_logits(T: int, seed: int, s_exp: float = 1.1) -> np.ndarray:
     """Logits whose top-4 per token is a Zipf(s)-popular draw of 4 distinct experts
-    ranked by decreasing logit."""
+    (benchmark config 4), ranked by decreasing logit."""
     r = np.random.default_rng(seed)
     p = 1.0 / np.arange(1, E + 1) ** s_exp
     p /= p.sum()
@@ -374,7 +374,7 @@ def zipf_logits(T: int, seed: int, s_exp: float = 1.1) -> np.ndarray:
 
 
 def prefill_bench(gw, args) -> int:
-    """one GPT-OSS-120B MoE layer (128 experts, 1.70 GB resident),
+    """Benchmark config 4: one GPT-OSS-120B MoE layer (128 experts, 1.70 GB resident),
     batched prefill of 512 tokens with Zipf(1.1)-popular top-4 routing, bf16 x.
     Reports µs per layer, HBM GB/s over the distinct experts touched, and matrix-core
     use: algorithmic flops (2 x tokens x 4 x (5760 x 2880 + 2880 x 2880)) against the
@@ -467,7 +467,7 @@ QWEN3 = dict(H=2048, F=768, E=128, K=8, L=48)
 
 
 def qwen3_bench(gw, args, batch: int) -> int:
-    """Qwen3 MoE stack, 48 layers x 128 experts (hidden 2048,
+    """Benchmark config 3: Qwen3 MoE stack, 48 layers x 128 experts (hidden 2048,
     expert intermediate 768, gate/up interleaved row-wise, zero bias sections as
     the reference's install writes them, SiLU-GLU), top-8, bf16 x; `batch` tokens
     per step (1 or 8) with independent N(0,1) logits per token and layer.  Bytes per
@@ -608,7 +608,7 @@ def main() -> int:
     ap.add_argument("--workload", choices=["decode", "prefill", "qwen3", "qwen3-b8", "gemv",
                                            "gptoss20b"],
                     default="decode",
-                    help="decode: BASELINE config 2 (the headline line, default); prefill: "
+                    help="decode: benchmark config 2 (the headline line, default); prefill: "
                          "config 4, one GPT-OSS-120B layer, 512 Zipf-routed tokens; qwen3 / "
                          "qwen3-b8: config 3, the Qwen3 stack at batch 1 / 8; gemv: config 0, "
                          "one gate_up-shaped GEMV; gptoss20b: config 1, a 20B layer with its "
@@ -617,8 +617,8 @@ def main() -> int:
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this "
-              "build (the MoE decode path runs on a single MI355X; see the sharding note in "
-              "DESIGN.md)", file=sys.stderr)
+              "build (the whole model fits one MI355X's HBM and every kernel here runs on a "
+              "single GPU; sharding across GPUs is a design note, not code)", file=sys.stderr)
         return 2
 
     import godwit_amd as gw

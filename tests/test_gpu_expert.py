@@ -246,7 +246,7 @@ def _layer_case(ctx, shape, n_experts, top_k, tokens, seed, router):
 
 
 def test_layer_config1_gptoss20b_router(ctx):
-    """BASELINE config 1 shape: 32 GPT-OSS experts, fp32 router N(0, 0.02), top-4,
+    """Benchmark config 1 shape: 32 GPT-OSS experts, fp32 router N(0, 0.02), top-4,
     bf16 x, batch 1."""
     got, got16, ids, wts, ref, rids, rw = _layer_case(ctx, GPTOSS, 32, 4, 1, 600, router=True)
     assert np.array_equal(ids, rids)
@@ -258,7 +258,7 @@ def test_layer_config1_gptoss20b_router(ctx):
 
 
 def test_layer_given_logits_128_experts(ctx):
-    """BASELINE config 2 layer: 128 experts, logits ~ N(0,1), top-4.  Also the
+    """Benchmark config 2 layer: 128 experts, logits ~ N(0,1), top-4.  Also the
     reference's own layer acceptance (check-layer: routing exact, relative RMS
     < 2e-3, max error < 4 fp16 ulps of the peak)."""
     got, _, ids, wts, ref, rids, rw = _layer_case(ctx, GPTOSS, 128, 4, 1, 700, router=False)
@@ -272,7 +272,7 @@ def test_layer_given_logits_128_experts(ctx):
 @pytest.mark.parametrize("tokens,path", [(1, "stream"), (3, "stream"), (8, "stream"),
                                          (3, "grouped"), (8, "grouped")])
 def test_layer_qwen3_decode(ctx, monkeypatch, tokens, path):
-    """BASELINE config 3 layer: Qwen3 shape, top-8 of 128, no biases, SiLU-GLU, batch 1/8.
+    """Benchmark config 3 layer: Qwen3 shape, top-8 of 128, no biases, SiLU-GLU, batch 1/8.
     A batch of 2..8 tokens takes the grouped GEMMs by default; GODWIT_PREFILL_ABOVE=8
     at runner creation keeps it on the streaming decode kernels."""
     monkeypatch.setenv("GODWIT_PREFILL_ABOVE", "8" if path == "stream" else "2")

@@ -2,7 +2,7 @@
 
 Mirrors Tests/GodwitTests/DequantGEMVTests.swift (GEMV vs referenceMXFP4 at
 64x256 and 32x2880, metric < 1e-3) and ActivationTests.swift (fixed vectors),
-and adds the bit-exact dequant table and the BASELINE config-0 shape.
+and adds the bit-exact dequant table and the benchmark config-0 shape.
 """
 import numpy as np
 import pytest
@@ -88,7 +88,7 @@ def test_gemv_hand_case(ctx):
 
 @pytest.mark.parametrize("x_dtype", [gw.F32, gw.F16, gw.BF16])
 def test_gemv_config0_shape(ctx, x_dtype):
-    """5760 x 2880, nibbles U{0..15}, scales U{119..127},
+    """Benchmark config 0: 5760 x 2880, nibbles U{0..15}, scales U{119..127},
     fp32 bias N(0, 0.02); x ~ N(0,1) in each supported dtype."""
     r = rng(7)
     rows, cols = 5760, 2880

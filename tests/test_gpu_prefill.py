@@ -36,7 +36,7 @@ def _close_batch(got, ref):
 
 def _zipf_logits(r, T, E, K, s=1.1):
     """Logits whose top-k per token is a Zipf(s)-popular draw of K distinct experts
-    (BASELINE config 4's assignment), ranked by decreasing logit."""
+    (benchmark config 4's assignment), ranked by decreasing logit."""
     p = 1.0 / np.arange(1, E + 1) ** s
     p /= p.sum()
     logits = (r.standard_normal((T, E)) - 10.0).astype(np.float32)
