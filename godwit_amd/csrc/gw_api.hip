@@ -7,6 +7,7 @@
 // route kernel for the device-driven layer call.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -563,6 +564,7 @@ struct gw_expert_runner {
     void *pf_buf = nullptr;
     bool fused_enabled = false;      // GODWIT_FUSED_LAYER=1 at creation turns it on
     int prefill_above = 1;           // batches larger than this run the grouped GEMMs
+    int self_group_max = 32;         // grouped batches up to this size group inside the GEMMs
     int ring_next = 0;
     int ring_used = 0;
 };
@@ -640,6 +642,8 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     r->fused_enabled = env && env[0] == '1';
     const int pa = get_env_int("GODWIT_PREFILL_ABOVE", 1);
     r->prefill_above = pa < 1 ? 1 : pa > gw::kMaxTokens ? gw::kMaxTokens : pa;
+    const int sg = get_env_int("GODWIT_SELF_GROUP_TOKENS", 32);
+    r->self_group_max = sg < 0 ? 0 : sg > 32 ? 32 : sg;
     *out = r;
     return GW_OK;
 }
@@ -1152,13 +1156,17 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
                                  a->x, a->x_dtype, ps.logits, E, (int)r->hidden, T));
         logits = ps.logits;
     }
-    const bool route_in_group = gw::prefill_routes_in_group(T, K);
-    if (!route_in_group) {
-        ProfScope p(ctx, "prefill_route");
-        GW_HIP(gw::launch_prefill_route(p.launch(L), logits, T, E, K, ps.ids, ps.weights));
-    }
-    const int max_tiles = gw::prefill_max_tiles(T, K, E);
-    {
+    // Up to self_group_max tokens every expert holds at most one tile, and
+    // the GEMMs route and group the batch themselves (no route or group
+    // kernel); larger batches get the tile list from the group kernel.
+    const bool self_group = T <= r->self_group_max && gw::prefill_self_groups(T, K, E);
+    const int max_tiles = self_group ? std::min(E, T * K) : gw::prefill_max_tiles(T, K, E);
+    if (!self_group) {
+        const bool route_in_group = gw::prefill_routes_in_group(T, K);
+        if (!route_in_group) {
+            ProfScope p(ctx, "prefill_route");
+            GW_HIP(gw::launch_prefill_route(p.launch(L), logits, T, E, K, ps.ids, ps.weights));
+        }
         ProfScope p(ctx, "prefill_group");
         GW_HIP(gw::launch_prefill_group(p.launch(L), route_in_group ? logits : nullptr, T, K,
                                         ps.weights, ps.ids, E, ps.offsets, ps.order, ps.tiles,
@@ -1166,6 +1174,14 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
     }
     const gw::Sections sec = sections_of(r->offsets);
     gw::PrefillGemm g;
+    if (self_group) {
+        g.sg_tokens = T;
+        g.sg_topk = K;
+        g.sg_experts = E;
+        g.sg_logits = logits;
+        g.sg_ids_out = ps.ids;
+        g.sg_w_out = ps.weights;
+    }
     g.tiles = ps.tiles;
     g.ntiles = ps.ntiles;
     g.offsets = ps.offsets;
@@ -1199,6 +1215,8 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
         GW_HIP(gw::launch_prefill_gemm(p.launch(L), true, planes, g, max_tiles, T * K));
     }
     {
+        g.sg_logits = nullptr;
+        g.sg_ids = self_group ? ps.ids : nullptr;
         g.in = ps.act;
         g.in_plane = (int64_t)T * K * r->inter;
         g.in_row_div = 1;

@@ -89,8 +89,19 @@ struct PrefillGemm {
     float *y_out;                 // down: [entries, fdim] fp32
     int act_kind;
     float limit, alpha;
+    // Self-grouped batch (sg_tokens > 0): the GEMM builds its own work list;
+    // gate_up routes from sg_logits and writes sg_ids_out / sg_w_out, down
+    // reads sg_ids.  tiles / ntiles / offsets / order are then unused.
+    int sg_tokens = 0, sg_topk = 0, sg_experts = 0;
+    const float *sg_logits = nullptr;
+    const int32_t *sg_ids = nullptr;
+    int32_t *sg_ids_out = nullptr;
+    float *sg_w_out = nullptr;
 };
 int prefill_max_tiles(int T, int K, int E);
+// True when a batch is small enough for the self-grouped GEMMs (every expert
+// at most one 32-entry tile); max_tiles is then min(E, T*K).
+bool prefill_self_groups(int T, int K, int E);
 int prefill_planes(int in_dt);        // bf16 planes that hold a dtype exactly: 1, 2 or 3
 int prefill_gemm_lds_bytes(int planes, int kdim, int waves);
 hipError_t launch_prefill_route(const Launch &L, const float *logits, int T, int E, int K,

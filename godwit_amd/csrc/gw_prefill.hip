@@ -207,7 +207,19 @@ struct GemmArgs {
     float *y_out;                 // down: [N, fdim] fp32
     int act_kind;
     float limit, alpha;
+    // Self-grouped batches (sg_tokens > 0, at most kSelfGroupTokens tokens):
+    // the gate_up launch routes from sg_logits [T, E] in every workgroup and
+    // workgroup 0 writes the routing to sg_ids_out / sg_w_out; the down
+    // launch groups from those ids (sg_ids).  The tile list is unused.
+    int sg_tokens, sg_topk, sg_experts;
+    const float *sg_logits;
+    const int32_t *sg_ids;
+    int32_t *sg_ids_out;
+    float *sg_w_out;
 };
+
+// A batch of at most this many tokens gives every expert at most one tile.
+constexpr int kSelfGroupTokens = kPT;
 
 template <int PL> struct PrefillDepth { static constexpr int value = PL == 3 ? 2 : 4; };
 
@@ -300,6 +312,8 @@ __global__ __launch_bounds__(64 * W) void prefill_gemm_kernel(GemmArgs a)
     constexpr int kNX = 2 * PL;               // LDS-DMA loads per chunk per wave
     // Loads a wave issues after a chunk's DMA until it waits for that DMA.
     constexpr int kYounger = kNW + (D - 2) * (kNX + kNW);
+    static_assert(D * PL * kPlaneBytes >= 2048 + kSelfGroupTokens * kPrefillMaxExperts * 4,
+                  "the self-grouping scratch must fit in the staging ring");
     // Dynamic LDS only (a static __shared__ variable would shift the dynamic
     // area off its alignment); layout in prefill_lds.
     extern __shared__ __align__(16) uint32_t plds[];
@@ -315,22 +329,108 @@ __global__ __launch_bounds__(64 * W) void prefill_gemm_kernel(GemmArgs a)
     // one contiguous eighth of the units, so those workgroups share one L2.
     // floor(unit / nft) is always one of the unit's expert's tiles.
     const int nft = (a.fdim + kF - 1) / kF;
-    const int units = *a.ntiles * nft;
-    const int per = (units + 7) >> 3;
     const int jx = (int)(blockIdx.x >> 3);
-    const int unit = (int)(blockIdx.x & 7) * per + jx;
-    if (jx >= per || unit >= units) return;           // uniform: the workgroup leaves
-    const int tq = unit / nft;
-    const int te = a.tiles[tq];
-    const int e = te >> 16;
-    const int t0 = tq - (te & 0xFFFF);
-    const int ecnt = a.offsets[e + 1] - a.offsets[e];
-    const int ne = (ecnt + kPT - 1) / kPT;
-    const int local = unit - t0 * nft;
-    const int fidx = local / ne, m = local - fidx * ne;
-    const int g0 = a.offsets[e] + m * kPT;
-    const int ntok = min(kPT, a.offsets[e + 1] - g0);
-    if (threadIdx.x < kPT) ent[threadIdx.x] = a.order[g0 + min((int)threadIdx.x, ntok - 1)];
+    int e, fidx, ntok;
+    if (a.sg_tokens > 0) {
+        // Self-grouped batch: every expert has at most sg_tokens <= kPT
+        // entries (top-k picks distinct experts), so a work unit is
+        // (active expert, feature tile) and each workgroup derives the whole
+        // list from the routing in its own LDS: the expert ids of the entries
+        // (selected here from the logits, or read from the routing the
+        // gate_up launch wrote), a 256-bit mask of active experts, and the
+        // unit's expert as the tq-th set bit.  Scratch lives in the staging
+        // ring, which no DMA targets yet.
+        const int tid = (int)threadIdx.x, T = a.sg_tokens, K = a.sg_topk, E = a.sg_experts;
+        const int N = T * K;
+        int *sid_l = reinterpret_cast<int *>(xring);                          // [N <= 256]
+        uint32_t *amask = reinterpret_cast<uint32_t *>(xring + 1024);         // [8]
+        int *ecount = reinterpret_cast<int *>(xring + 1024 + 32);
+        float *lg = reinterpret_cast<float *>(xring + 2048);                  // [T, E]
+        if (tid < 8) amask[tid] = 0u;
+        if (tid == 8) *ecount = 0;
+        if (a.sg_logits) {
+            // All logits into LDS with every load in flight, then one wave
+            // per token selects from there.
+            constexpr int kLU = (kSelfGroupTokens * kPrefillMaxExperts + kThreads - 1) / kThreads;
+            const int n = T * E;
+            float v[kLU];
+#pragma unroll
+            for (int u = 0; u < kLU; ++u) {
+                const int i = tid + u * kThreads;
+                v[u] = i < n ? a.sg_logits[i] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < kLU; ++u) {
+                const int i = tid + u * kThreads;
+                if (i < n) lg[i] = v[u];
+            }
+            __syncthreads();
+            const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), ln = tid & 63;
+            for (int t = wv; t < T; t += W) {
+                int sid;
+                float w;
+                if (E <= 128) select_one<2>(lg + t * E, E, K, sid, w);
+                else select_one<4>(lg + t * E, E, K, sid, w);
+                if (ln < K) {
+                    sid_l[t * K + ln] = sid;
+                    if (blockIdx.x == 0) {                // one copy for down and combine
+                        a.sg_ids_out[t * K + ln] = sid;
+                        a.sg_w_out[t * K + ln] = w;
+                    }
+                }
+            }
+        } else if (tid < N) {
+            sid_l[tid] = a.sg_ids[tid];
+        }
+        __syncthreads();
+        if (tid < N && (unsigned)sid_l[tid] < (unsigned)E)
+            atomicOr(&amask[sid_l[tid] >> 5], 1u << (sid_l[tid] & 31));
+        __syncthreads();
+        uint32_t words[8];
+        int active = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            words[i] = __builtin_amdgcn_readfirstlane(amask[i]);
+            active += __builtin_popcount(words[i]);
+        }
+        const int units = active * nft;
+        const int per = (units + 7) >> 3;
+        const int unit = (int)(blockIdx.x & 7) * per + jx;
+        if (jx >= per || unit >= units) return;       // uniform: the workgroup leaves
+        const int tq = unit / nft;
+        fidx = unit - tq * nft;
+        // The tq-th active expert in id order.
+        int rem = tq, wi = 0;
+        while (wi < 7 && rem >= __builtin_popcount(words[wi])) rem -= __builtin_popcount(words[wi++]);
+        uint32_t x = words[wi];
+        for (int i = 0; i < rem; ++i) x &= x - 1;
+        e = wi * 32 + __builtin_ctz(x);
+        // Its entries, in any order (an entry's results depend on its row only).
+        if (tid < N && sid_l[tid] == e) {
+            const int pos = atomicAdd(ecount, 1);
+            if (pos < kPT) ent[pos] = tid;   // always: a token picks an expert once
+        }
+        __syncthreads();
+        ntok = min(__builtin_amdgcn_readfirstlane(*ecount), kPT);
+        if (tid < kPT && tid >= ntok) ent[tid] = ent[ntok - 1];
+    } else {
+        const int units = *a.ntiles * nft;
+        const int per = (units + 7) >> 3;
+        const int unit = (int)(blockIdx.x & 7) * per + jx;
+        if (jx >= per || unit >= units) return;       // uniform: the workgroup leaves
+        const int tq = unit / nft;
+        const int te = a.tiles[tq];
+        e = te >> 16;
+        const int t0 = tq - (te & 0xFFFF);
+        const int ecnt = a.offsets[e + 1] - a.offsets[e];
+        const int ne = (ecnt + kPT - 1) / kPT;
+        const int local = unit - t0 * nft;
+        fidx = local / ne;
+        const int m = local - fidx * ne;
+        const int g0 = a.offsets[e] + m * kPT;
+        ntok = min(kPT, a.offsets[e + 1] - g0);
+        if (threadIdx.x < kPT) ent[threadIdx.x] = a.order[g0 + min((int)threadIdx.x, ntok - 1)];
+    }
 
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
@@ -369,7 +469,10 @@ __global__ __launch_bounds__(64 * W) void prefill_gemm_kernel(GemmArgs a)
     // Staging: wave w copies rows 4w' .. 4w'+3 of each plane (w' = w mod 8;
     // waves past 8 repeat waves 0.. with the same bytes to the same slots, so
     // every wave issues the same loads), two rows per DMA (lanes 0-31 row
-    // 4w'+2n, lanes 32-63 the next); a lane's slot is lane & 31.
+    // 4w'+2n, lanes 32-63 the next); a lane's slot is lane & 31.  The padding
+    // rows of a partial tile (t >= ntok) are read past the buffer's end: the
+    // DMA puts zeros in their slots without a memory access, and their
+    // columns of the tile are never stored.
     const int sw = wave & 7;
     int64_t xrow[2];
     int xpiece[2];
@@ -377,7 +480,7 @@ __global__ __launch_bounds__(64 * W) void prefill_gemm_kernel(GemmArgs a)
     for (int n = 0; n < 2; ++n) {
         const int t = 4 * sw + 2 * n + h;
         xpiece[n] = (lane & 31) ^ (t & 15);
-        xrow[n] = (int64_t)(ent[t] / a.in_row_div) * a.kdim;
+        xrow[n] = t < ntok ? (int64_t)(ent[t] / a.in_row_div) * a.kdim : -1;
     }
     // Pieces past kdim read the row's last piece instead; the weights of the
     // blocks there are zeroed, so they add exact zeros (for finite inputs).
@@ -392,7 +495,9 @@ __global__ __launch_bounds__(64 * W) void prefill_gemm_kernel(GemmArgs a)
 #pragma unroll
             for (int n = 0; n < 2; ++n) {
                 const int k = min(q * (kKC * 32) + xpiece[n] * 8, a.kdim - 8);
-                const uint32_t voff = (uint32_t)((p * a.in_plane + xrow[n] + k) * 2);
+                const uint32_t voff =
+                    xrow[n] < 0 ? 0x80000000u   // >= in_bytes (< 2^31): out of range
+                                : (uint32_t)((p * a.in_plane + xrow[n] + k) * 2);
                 uint8_t *dst = xring + (size_t)(buf * PL + p) * kPlaneBytes +
                                (4 * sw + 2 * n) * kRowBytes;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (l_void *)dst, 16, voff, 0, 0, 0);
@@ -675,6 +780,12 @@ int prefill_max_tiles(int T, int K, int E) { return pdiv_up((int64_t)T * K, kPT)
 
 bool prefill_routes_in_group(int T, int K) { return T <= kRouteGroupTokens && K <= kMaxTopK; }
 
+bool prefill_self_groups(int T, int K, int E)
+{
+    return T >= 1 && T <= kSelfGroupTokens && K >= 1 && K <= kMaxTopK && E >= K &&
+           E <= kPrefillMaxExperts;
+}
+
 hipError_t launch_prefill_group(const Launch &L, const float *logits, int T, int K, float *weights,
                                 int32_t *ids, int E, int32_t *offsets, int32_t *order,
                                 int32_t *tiles, int32_t *ntiles, int max_tiles)
@@ -760,6 +871,21 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
     a.act_kind = g.act_kind;
     a.limit = g.limit;
     a.alpha = g.alpha;
+    a.sg_tokens = g.sg_tokens;
+    a.sg_topk = g.sg_topk;
+    a.sg_experts = g.sg_experts;
+    a.sg_logits = g.sg_logits;
+    a.sg_ids = g.sg_ids;
+    a.sg_ids_out = g.sg_ids_out;
+    a.sg_w_out = g.sg_w_out;
+    if (g.sg_tokens > 0) {
+        // The workgroup routes or reads T*K <= 256 entries, one per thread,
+        // and stages T*E <= 8192 logits in its staging ring.
+        if (!prefill_self_groups(g.sg_tokens, g.sg_topk, g.sg_experts)) return hipErrorInvalidValue;
+        if (gate_up ? (!g.sg_logits || !g.sg_ids_out || !g.sg_w_out) : !g.sg_ids)
+            return hipErrorInvalidValue;
+        if (max_tiles < std::min(g.sg_experts, g.sg_tokens * g.sg_topk)) return hipErrorInvalidValue;
+    }
     const int waves = prefill_waves(g.fdim, g.kdim, planes,
                                     tiles_hint > 0 && tiles_hint < max_tiles ? tiles_hint : max_tiles,
                                     L.cus);

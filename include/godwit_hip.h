@@ -250,7 +250,11 @@ int gw_expert_apply_assignments_async(gw_expert_runner *runner, const void *inpu
  * 2..8 tokens (more than GODWIT_PREFILL_ABOVE at runner creation, default 1)
  * when hidden and intermediate sizes are multiples of 32 and >= 128, x is
  * 16-byte aligned, there are at most 256 experts and, during graph capture,
- * the prefill scratch is already reserved.  Enqueue only. */
+ * the prefill scratch is already reserved.  Batches of up to 32 tokens are
+ * routed and grouped inside the grouped GEMMs themselves (every expert then
+ * holds at most one 32-entry tile); GODWIT_SELF_GROUP_TOKENS at runner
+ * creation (0..32, default 32) lowers that bound, larger batches use the
+ * group kernel's tile list.  Enqueue only. */
 typedef struct gw_moe_layer_args {
     const uint8_t *experts_base;
     int64_t expert_stride;

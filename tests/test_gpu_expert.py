@@ -270,12 +270,15 @@ def test_layer_given_logits_128_experts(ctx):
 
 
 @pytest.mark.parametrize("tokens,path", [(1, "stream"), (3, "stream"), (8, "stream"),
-                                         (3, "grouped"), (8, "grouped")])
+                                         (3, "grouped"), (8, "grouped"), (8, "listed")])
 def test_layer_qwen3_decode(ctx, monkeypatch, tokens, path):
     """Benchmark config 3 layer: Qwen3 shape, top-8 of 128, no biases, SiLU-GLU, batch 1/8.
-    A batch of 2..8 tokens takes the grouped GEMMs by default; GODWIT_PREFILL_ABOVE=8
-    at runner creation keeps it on the streaming decode kernels."""
+    A batch of 2..8 tokens takes the grouped GEMMs by default, which group it
+    themselves; GODWIT_SELF_GROUP_TOKENS=0 gives them the group kernel's tile list
+    ("listed") and GODWIT_PREFILL_ABOVE=8 keeps the batch on the streaming decode
+    kernels (both read at runner creation)."""
     monkeypatch.setenv("GODWIT_PREFILL_ABOVE", "8" if path == "stream" else "2")
+    monkeypatch.setenv("GODWIT_SELF_GROUP_TOKENS", "0" if path == "listed" else "32")
     got, _, ids, wts, ref, rids, rw = _layer_case(ctx, QWEN3, 128, 8, tokens, 800 + tokens,
                                                   router=False)
     assert np.array_equal(ids, rids)
@@ -310,7 +313,7 @@ def test_layer_routing_ties_exact(ctx, monkeypatch, experts, top_k, tokens, path
     included: logits drawn from 6 distinct values, so most top-k picks are ties
     broken by the sort's swap history.  300 experts exercises the standalone route
     kernel, the other streaming cases the routing fused into the gate_up kernel, the
-    grouped case the grouped GEMMs' route kernel."""
+    grouped case the routing inside the self-grouped gate_up GEMM."""
     monkeypatch.setenv("GODWIT_PREFILL_ABOVE", "8" if path == "stream" else "2")
     shape = SMALL
     H = shape["hidden"]
@@ -368,16 +371,18 @@ def _routing_logits(case, tokens, experts):
 @pytest.mark.parametrize("case", ["distinct", "ties_below", "tie_inside", "signed_zero",
                                   "nan_rest", "nan_first"])
 @pytest.mark.parametrize("tokens,path", [(1, "stream"), (2, "stream"), (3, "grouped"),
-                                         (40, "grouped")])
+                                         (32, "grouped"), (3, "listed"), (40, "grouped")])
 def test_routing_selection_paths(ctx, monkeypatch, case, tokens, path):
     """Device routing equals Router.select (the oracle) for inputs that take the
     fast selection and for those that fall back to the exact sort: decode
-    (fused into gate_up, one and two tokens), the grouping kernel (3 tokens)
-    and the prefill route kernel (40 tokens)."""
+    (fused into gate_up, one and two tokens), the self-grouped GEMMs (3 and 32
+    tokens, selecting from logits staged in LDS), the grouping kernel (3 tokens
+    with GODWIT_SELF_GROUP_TOKENS=0) and the prefill route kernel (40 tokens)."""
     shape = SMALL
     H, E, K = shape["hidden"], 64, 4
     layout, experts_d, buf = _make_layer(ctx, shape, E, 1200)
     monkeypatch.setenv("GODWIT_PREFILL_ABOVE", "8" if path == "stream" else "1")
+    monkeypatch.setenv("GODWIT_SELF_GROUP_TOKENS", "0" if path == "listed" else "32")
     runner = gw.ExpertRunner(ctx, H, shape["inter"], shape["act"])
     logits = _routing_logits(case, tokens, E)
     xbits, _ = normal_bf16(rng(1201), tokens * H)

@@ -75,7 +75,7 @@ def _run(ctx, runner, layout, buf, E, K, xb, x_dtype, lb, T, H, fn="prefill_forw
     (SMALL, 16, 4, 72, gw.BF16, 1),      # experts with 2-3 tiles, partial feature tiles
     (QWEN3, 32, 8, 24, gw.F16, 2),       # two activation planes, no biases, SiLU-GLU
     (GPTOSS, 12, 4, 20, gw.F32, 3),      # three planes, 2880-wide K (11.25 chunks)
-    (SMALL, 200, 4, 32, gw.BF16, 4),     # routed inside the group kernel, 4-wave expert scan
+    (SMALL, 200, 4, 32, gw.BF16, 4),     # self-grouped: 200 experts, 32 tokens
     (SMALL, 256, 8, 40, gw.BF16, 5),     # route kernel, then a scan over 256 experts
     (SMALL, 8, 2, 2048, gw.BF16, 6),     # ~16 tiles per expert: many units per XCD eighth
 ], ids=["small-bf16", "qwen3-f16", "gptoss-f32", "small-e200-t32", "small-e256-t40",
@@ -184,3 +184,65 @@ def test_prefill_router_and_graph_replay(ctx):
     for b in (xb, wb, out, buf):
         b.free()
     runner.close()
+
+
+@pytest.mark.parametrize("shape,E,K,T,x_dtype,seed", [
+    (QWEN3, 128, 8, 8, gw.BF16, 1),      # benchmark config 3's batch
+    (SMALL, 8, 2, 32, gw.BF16, 2),       # many entries per expert (a full 32-entry tile)
+    (SMALL, 256, 8, 32, gw.F16, 3),      # 256 experts, 256 entries, 8192 staged logits
+    (GPTOSS, 12, 4, 20, gw.F32, 4),      # three planes, 2880-wide K
+    (SMALL, 64, 4, 2, gw.BF16, 5),       # the smallest grouped batch
+], ids=["qwen3-t8", "small-e8-t32", "small-e256-t32", "gptoss-f32-t20", "small-t2"])
+def test_self_grouped_equals_tile_list(ctx, monkeypatch, shape, E, K, T, x_dtype, seed):
+    """Batches of at most 32 tokens are routed and grouped inside the grouped
+    GEMMs (every expert holds at most one 32-entry tile); GODWIT_SELF_GROUP_TOKENS=0
+    sends them through the group kernel's tile list instead.  Both equal the
+    oracle, and each other bit for bit (an entry's outputs depend only on its own
+    column of the tile), routing included; a captured self-grouped layer replays
+    to the same bytes."""
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _make_layer(ctx, shape, E, 2500 + seed)
+    r = rng(2600 + seed)
+    xb, xw = _x(ctx, r, T, H, x_dtype)
+    logits = _zipf_logits(r, T, E, K) if seed % 2 else r.standard_normal((T, E)).astype(np.float32)
+    lb = ctx.buffer(logits)
+    runs = {}
+    for mode in ("self", "list"):
+        monkeypatch.setenv("GODWIT_SELF_GROUP_TOKENS", "32" if mode == "self" else "0")
+        runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+        ctx.set_profiling(True)
+        ctx.profile_reset()
+        runs[mode] = _run(ctx, runner, layout, buf, E, K, xb, x_dtype, lb, T, H,
+                          "prefill_forward")
+        n_group = ctx.profile("prefill_group")[1]
+        ctx.set_profiling(False)
+        assert n_group == (0 if mode == "self" else 1), (mode, n_group)
+        if mode == "self":
+            runner.reserve_prefill(T, K, E)
+            out = ctx.empty(T * H * 4)
+
+            def body():
+                runner.prefill_forward(buf.ptr, layout.stride, E, K, xb.ptr, x_dtype, T, out.ptr,
+                                       logits=lb.ptr)
+
+            graph = gw.Graph.capture(ctx, body)
+            for _ in range(3):
+                out.zero()
+                graph.launch()
+                ctx.synchronize()
+                assert np.array_equal(out.download(np.float32, T * H), runs["self"][0].ravel())
+            graph.destroy()
+            out.free()
+        runner.close()
+    for i in range(4):
+        assert np.array_equal(runs["self"][i], runs["list"][i]), i
+    got, _, ids, wts = runs["self"]
+    ref, rids, rw = oracle.moe_layer([e.oracle_expert() for e in experts], K, logits, xw, H, F,
+                                     shape["oact"])
+    assert np.array_equal(ids, rids)
+    assert np.allclose(wts, rw, rtol=1e-6, atol=1e-7)
+    _close_batch(got, ref)
+    rel_rms, worst, bound, ok = layer_check(got, ref)
+    assert ok, (rel_rms, worst, bound)
+    for b in (xb, lb, buf):
+        b.free()
