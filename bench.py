@@ -17,7 +17,9 @@ biases, plus the logits, activations and outputs, per token, divided by the
 wall time per token measured around the timed steps.  The `roofline` object
 covers the dominant kernel (fused gate_up) timed with hipEvents on the
 library's stream; `cpu_baseline` is the CPU oracle (a scalar port of the
-reference's CPU path) on a bounded sample of the same workload.
+reference's CPU path) on a bounded sample of the same workload, one thread,
+with the same port's GEMV rows split over the host's cores beside it
+(`all_cores`).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -321,13 +323,22 @@ def gptoss20b_bench(gw, args) -> int:
     return 0
 
 
-def cpu_baseline(seconds: float) -> dict:
+def host_threads() -> int:
+    """Host threads for the all-core CPU baseline: the process's CPU share
+    (OMP_NUM_THREADS when set, else the affinity mask), at most 16."""
+    n = int(os.environ.get("OMP_NUM_THREADS") or 0) or len(os.sched_getaffinity(0))
+    return max(1, min(16, n))
+
+
+def cpu_baseline(seconds: float, threads: int = 1) -> dict:
     """The oracle (scalar C port of the reference CPU path: referenceMXFP4 + bias,
     gptoss activation with fp16 rounding, Router.select, sequential combine) on
     whole tokens of the same workload until `seconds` have elapsed.  Eight
     distinct synthetic layer weight sets are cycled so no layer's 53 MB stays
-    in the host caches."""
+    in the host caches.  threads > 1 splits each GEMV's rows over that many
+    OpenMP threads (same results)."""
     import oracle
+    oracle.set_threads(threads)
     r = np.random.default_rng(77)
     sets = []
     for _ in range(8):
@@ -353,7 +364,9 @@ def cpu_baseline(seconds: float) -> dict:
         dt = time.perf_counter() - t0
         if dt >= seconds:
             break
-    return {"tokens": tokens, "seconds": dt, "us_per_token": dt / tokens * 1e6}
+    oracle.set_threads(1)
+    return {"tokens": tokens, "seconds": dt, "us_per_token": dt / tokens * 1e6,
+            "threads": threads}
 
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 matrix peak
@@ -735,6 +748,15 @@ def main() -> int:
         except OSError:
             pass
         log(f"cpu baseline: {c['us_per_token']:.0f} us/token ({cpu['value']:.3f} GB/s)")
+        # The same port with each GEMV's rows split over the host's cores.
+        ca = cpu_baseline(args.cpu_seconds / 2, host_threads())
+        cpu["all_cores"] = {
+            "value": round(bytes_token / (ca["us_per_token"] * 1e-6) / 1e9, 4), "unit": "GB/s",
+            "us_per_token": round(ca["us_per_token"], 1), "cores": ca["threads"],
+            "sample": f"{ca['tokens']} token(s), same workload, GEMV rows over "
+                      f"{ca['threads']} OpenMP threads, {ca['seconds']:.1f} s"}
+        log(f"cpu baseline, {ca['threads']} threads: {ca['us_per_token']:.0f} us/token "
+            f"({cpu['all_cores']['value']:.3f} GB/s)")
 
     result = {
         "metric": METRIC,

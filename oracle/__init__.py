@@ -53,6 +53,7 @@ def _load() -> ctypes.CDLL:
         "gwo_encode": (None, [_P, _I64, _P, _P]),
         "gwo_reference_mxfp4": (None, [_P, _P, _P, _P, _I64, _I64]),
         "gwo_gemv_bias": (None, [_P, _P, _P, _P, _P, _I64, _I64]),
+        "gwo_set_threads": (None, [ctypes.c_int]),
         "gwo_gptoss_activation_f32": (_F, [_F, _F, _F, _F]),
         "gwo_swiglu_f32": (_F, [_F, _F]),
         "gwo_activation": (None, [ctypes.c_int, _P, _P, _I64, _F, _F]),
@@ -151,6 +152,11 @@ def reference_mxfp4(packed, scales, x, rows: int, cols: int) -> np.ndarray:
     y = np.empty(rows, np.float32)
     _lib.gwo_reference_mxfp4(_ptr(p), _ptr(s), _ptr(xv), _ptr(y), rows, cols)
     return y
+
+
+def set_threads(threads: int) -> None:
+    """Row-parallel GEMVs on `threads` host threads (1: serial); same results."""
+    _lib.gwo_set_threads(int(threads))
 
 
 def gemv_bias(packed, scales, bias, x, rows: int, cols: int) -> np.ndarray:

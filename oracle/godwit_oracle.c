@@ -189,10 +189,18 @@ void gwo_encode(const float *weights, int64_t count, uint8_t *packed, uint8_t *s
 /* DequantGEMVBenchmark.referenceMXFP4 —
  * Sources/Godwit/Benchmark/DequantGEMVBenchmark.swift:100-120.  Per-block
  * partial in element order, then acc += partial * scale over blocks in order. */
+/* Threads for the row loop below (1 = the reference's serial loop).  Rows
+ * are independent and each is summed by one thread in the order above, so
+ * any count gives the same bytes; only the all-core CPU baseline raises it. */
+static int g_threads = 1;
+
+void gwo_set_threads(int threads) { g_threads = threads < 1 ? 1 : threads; }
+
 void gwo_reference_mxfp4(const uint8_t *packed, const uint8_t *scales, const float *x,
                          float *y, int64_t rows, int64_t cols)
 {
     int64_t bpr = cols / 32;
+#pragma omp parallel for num_threads(g_threads) if (g_threads > 1) schedule(static)
     for (int64_t row = 0; row < rows; ++row) {
         float acc = 0.0f;
         for (int64_t block = 0; block < bpr; ++block) {

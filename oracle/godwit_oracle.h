@@ -38,6 +38,8 @@ void    gwo_encode(const float *weights, int64_t count, uint8_t *packed, uint8_t
 
 /* ---- fused dequant GEMV ------------------------------------------------ */
 /* x is already widened to fp32 (the reference widens fp16 x with Float(x)). */
+/* Row-parallel threads for the GEMVs (default 1; results do not depend on it). */
+void gwo_set_threads(int threads);
 void gwo_reference_mxfp4(const uint8_t *packed, const uint8_t *scales, const float *x,
                          float *y, int64_t rows, int64_t cols);
 /* bias may be NULL (no bias); otherwise fp32 values (bf16 biases are widened first). */

@@ -196,6 +196,24 @@ def test_gemv_row_and_column_order():
     assert list(y) == [0.0, 12.0, 0.0]
 
 
+def test_gemv_row_parallel_is_identical():
+    """The all-core CPU baseline splits GEMV rows over threads; each row keeps
+    its serial summation order, so the bytes do not change."""
+    r = np.random.default_rng(5)
+    rows, cols = 333, 256
+    packed = r.integers(0, 256, rows * cols // 2, dtype=np.uint8)
+    scales = r.integers(110, 135, rows * cols // 32, dtype=np.uint8)
+    bias = oracle.round_to_bf16((r.standard_normal(rows) * 0.02).astype(np.float32))
+    x = r.standard_normal(cols).astype(np.float32)
+    serial = oracle.gemv_bias(packed, scales, bias, x, rows, cols)
+    try:
+        oracle.set_threads(4)
+        parallel = oracle.gemv_bias(packed, scales, bias, x, rows, cols)
+    finally:
+        oracle.set_threads(1)
+    assert np.array_equal(serial, parallel)
+
+
 def test_xorshift_generator_matches_swift_recipe():
     """DequantGEMVBenchmark.swift:35-54, restated independently in Python."""
     def ref_bytes(seed, n):
