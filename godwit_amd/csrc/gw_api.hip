@@ -565,6 +565,7 @@ struct gw_expert_runner {
     bool fused_enabled = false;      // GODWIT_FUSED_LAYER=1 at creation turns it on
     int prefill_above = 1;           // batches larger than this run the grouped GEMMs
     int self_group_max = 32;         // grouped batches up to this size group inside the GEMMs
+    int gemm_waves = 0, gemm_depth = 0;   // forced grouped-GEMM shape (0: chosen per launch)
     int ring_next = 0;
     int ring_used = 0;
 };
@@ -644,6 +645,13 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     r->prefill_above = pa < 1 ? 1 : pa > gw::kMaxTokens ? gw::kMaxTokens : pa;
     const int sg = get_env_int("GODWIT_SELF_GROUP_TOKENS", 32);
     r->self_group_max = sg < 0 ? 0 : sg > 32 ? 32 : sg;
+    if (const char *shape = getenv("GODWIT_PREFILL_SHAPE")) {
+        int w = 0, d = 0;
+        if (sscanf(shape, "%dx%d", &w, &d) == 2 && (w == 8 || w == 12) && (d == 2 || d == 4)) {
+            r->gemm_waves = w;
+            r->gemm_depth = d;
+        }
+    }
     *out = r;
     return GW_OK;
 }
@@ -1174,6 +1182,8 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
     }
     const gw::Sections sec = sections_of(r->offsets);
     gw::PrefillGemm g;
+    g.force_waves = r->gemm_waves;
+    g.force_depth = r->gemm_depth;
     if (self_group) {
         g.sg_tokens = T;
         g.sg_topk = K;

@@ -97,13 +97,18 @@ struct PrefillGemm {
     const int32_t *sg_ids = nullptr;
     int32_t *sg_ids_out = nullptr;
     float *sg_w_out = nullptr;
+    // Forced workgroup shape (waves 8 or 12, ring depth 2 or 4; 0: chosen per
+    // launch).  12 waves run 4 deep and three activation planes 2 deep
+    // whatever is asked; a shape whose LDS does not fit is not forced.  Same
+    // results either way.
+    int force_waves = 0, force_depth = 0;
 };
 int prefill_max_tiles(int T, int K, int E);
 // True when a batch is small enough for the self-grouped GEMMs (every expert
 // at most one 32-entry tile); max_tiles is then min(E, T*K).
 bool prefill_self_groups(int T, int K, int E);
 int prefill_planes(int in_dt);        // bf16 planes that hold a dtype exactly: 1, 2 or 3
-int prefill_gemm_lds_bytes(int planes, int kdim, int waves);
+int prefill_gemm_lds_bytes(int planes, int kdim, int waves, int depth);
 hipError_t launch_prefill_route(const Launch &L, const float *logits, int T, int E, int K,
                                 int32_t *ids, float *weights);
 // True when launch_prefill_group can route the batch itself (logits given).

@@ -221,7 +221,6 @@ struct GemmArgs {
 // A batch of at most this many tokens gives every expert at most one tile.
 constexpr int kSelfGroupTokens = kPT;
 
-template <int PL> struct PrefillDepth { static constexpr int value = PL == 3 ? 2 : 4; };
 
 // Calls f(integral_constant<int, S>) for S = B .. E-1 in order.
 template <int B, int E> struct Unroll {
@@ -302,18 +301,20 @@ template <int N> __device__ __forceinline__ void lds_wait()
     else static_assert(N == 0 || N == 2 || N == 3 || N == 4, "unsupported count");
 }
 
-template <int PL, bool GATE_UP, int W>
-__global__ __launch_bounds__(64 * W) void prefill_gemm_kernel(GemmArgs a)
+// W waves, D-deep ring.  The 8-wave, 2-deep form is held to 128 VGPRs (four
+// waves per SIMD), so two of its workgroups share a CU when their LDS fits;
+// the others hold ~165 VGPRs and one workgroup per CU.
+template <int PL, bool GATE_UP, int W, int D>
+__global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm_kernel(GemmArgs a)
 {
     // W waves, 32 features each: a workgroup computes kF features x kPT entries.
     constexpr int kF = 32 * W, kThreads = 64 * W;
-    constexpr int D = PrefillDepth<PL>::value;
+    static_assert(D >= 2 && D <= 4, "ring depth");
     constexpr int kNW = 4;                    // weight-ring loads per chunk (4 x 16 B)
     constexpr int kNX = 2 * PL;               // LDS-DMA loads per chunk per wave
     // Loads a wave issues after a chunk's DMA until it waits for that DMA.
     constexpr int kYounger = kNW + (D - 2) * (kNX + kNW);
-    static_assert(D * PL * kPlaneBytes >= 2048 + kSelfGroupTokens * kPrefillMaxExperts * 4,
-                  "the self-grouping scratch must fit in the staging ring");
+    static_assert(D * PL * kPlaneBytes >= 2048, "the self-grouping lists must fit in the ring");
     // Dynamic LDS only (a static __shared__ variable would shift the dynamic
     // area off its alignment); layout in prefill_lds.
     extern __shared__ __align__(16) uint32_t plds[];
@@ -349,28 +350,34 @@ __global__ __launch_bounds__(64 * W) void prefill_gemm_kernel(GemmArgs a)
         if (tid < 8) amask[tid] = 0u;
         if (tid == 8) *ecount = 0;
         if (a.sg_logits) {
-            // All logits into LDS with every load in flight, then one wave
-            // per token selects from there.
-            constexpr int kLU = (kSelfGroupTokens * kPrefillMaxExperts + kThreads - 1) / kThreads;
+            // All logits into LDS with every load in flight when they fit
+            // the ring (else each wave reads its tokens' rows itself), then
+            // one wave per token selects.
+            constexpr int kRing = D * PL * kPlaneBytes - 2048;
+            constexpr int kLU = (kRing / 4 + kThreads - 1) / kThreads;
             const int n = T * E;
-            float v[kLU];
+            const bool staged = n * 4 <= kRing;
+            if (staged) {
+                float v[kLU];
 #pragma unroll
-            for (int u = 0; u < kLU; ++u) {
-                const int i = tid + u * kThreads;
-                v[u] = i < n ? a.sg_logits[i] : 0.0f;
-            }
+                for (int u = 0; u < kLU; ++u) {
+                    const int i = tid + u * kThreads;
+                    v[u] = i < n ? a.sg_logits[i] : 0.0f;
+                }
 #pragma unroll
-            for (int u = 0; u < kLU; ++u) {
-                const int i = tid + u * kThreads;
-                if (i < n) lg[i] = v[u];
+                for (int u = 0; u < kLU; ++u) {
+                    const int i = tid + u * kThreads;
+                    if (i < n) lg[i] = v[u];
+                }
+                __syncthreads();
             }
-            __syncthreads();
+            const float *src = staged ? lg : a.sg_logits;
             const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), ln = tid & 63;
             for (int t = wv; t < T; t += W) {
                 int sid;
                 float w;
-                if (E <= 128) select_one<2>(lg + t * E, E, K, sid, w);
-                else select_one<4>(lg + t * E, E, K, sid, w);
+                if (E <= 128) select_one<2>(src + t * E, E, K, sid, w);
+                else select_one<4>(src + t * E, E, K, sid, w);
                 if (ln < K) {
                     sid_l[t * K + ln] = sid;
                     if (blockIdx.x == 0) {                // one copy for down and combine
@@ -615,7 +622,10 @@ __global__ __launch_bounds__(64 * W) void prefill_gemm_kernel(GemmArgs a)
         constexpr int s = decltype(s_const)::value;
         constexpr int sn = (s + D - 1) % D;
         if (q >= nq) return;                          // uniform: past the last chunk
+        // The counted wait below relies on a chunk's DMA being issued
+        // before its weights: the scheduler may not swap them.
         xload(sn, q + D - 1);
+        __builtin_amdgcn_sched_barrier(0);
         wload(sn, q + D - 1);
         __builtin_amdgcn_sched_barrier(0);
         multiply(q, s_const);
@@ -637,7 +647,9 @@ __global__ __launch_bounds__(64 * W) void prefill_gemm_kernel(GemmArgs a)
 #pragma unroll
     for (int s = 0; s < D - 1; ++s) {
         xload(s, s);
+        __builtin_amdgcn_sched_barrier(0);
         wload(s, s);
+        __builtin_amdgcn_sched_barrier(0);
     }
     __builtin_amdgcn_sched_barrier(0);
     wait_vmcnt<kYounger>();
@@ -799,27 +811,42 @@ hipError_t launch_prefill_group(const Launch &L, const float *logits, int T, int
 
 int prefill_planes(int in_dt) { return in_dt == DT_BF16 ? 1 : in_dt == DT_F16 ? 2 : 3; }
 
-int prefill_gemm_lds_bytes(int planes, int kdim, int waves)
+int prefill_gemm_lds_bytes(int planes, int kdim, int waves, int depth)
 {
-    const int depth = planes == 1   ? PrefillDepth<1>::value
-                      : planes == 2 ? PrefillDepth<2>::value
-                                    : PrefillDepth<3>::value;
     return prefill_lds(planes, depth, kdim / 32, waves).total;
 }
 
-// Waves per GEMM workgroup: 8 (256 features) by default, 12 (384 features)
-// when that needs fewer rounds of workgroups over the CUs in proportion to
-// their size — small batches, whose work list is a few dozen experts of one
-// tile each — and the LDS allows it.  `tiles_hint` bounds the work list.
-static int prefill_waves(int fdim, int kdim, int planes, int tiles_hint, int cus)
+// Workgroup shape of a grouped GEMM launch: W waves (256 or 384 features)
+// and ring depth D.  The cost of a shape is the feature rows the busiest CU
+// computes, ceil(units / CUs) x features per workgroup, times 8 — or times 7
+// for the 8-wave, 2-deep form when two of its workgroups share a CU (LDS
+// permitting, and more units than CUs): co-resident workgroups overlap each
+// other's latencies (Qwen3 batch-8 down GEMM 25.9 -> 19 us, 512-token gate_up
+// 426 -> 403 us), while one workgroup per CU runs better with a 4-deep ring
+// (a 12-wave gate_up that fits the CUs in one round: 35 against 40 us).  Ties
+// keep the earlier shape in the list.  `tiles_hint` bounds the work list.
+struct PrefillShape { int waves, depth; };
+
+static PrefillShape prefill_shape(int fdim, int kdim, int planes, int tiles_hint, int cus)
 {
-    auto cost = [&](int w) {
-        const int64_t units = (int64_t)tiles_hint * pdiv_up(fdim, 32 * w);
-        return (int64_t)pdiv_up(units, cus > 0 ? cus : 1) * w;
-    };
-    if (cost(12) < cost(8) && prefill_gemm_lds_bytes(planes, kdim, 12) <= kPrefillLdsMax)
-        return 12;
-    return 8;
+    const int c = cus > 0 ? cus : 1;
+    const PrefillShape cand[3] = {{8, planes == 3 ? 2 : 4}, {12, planes == 3 ? 2 : 4}, {8, 2}};
+    PrefillShape best = cand[0];
+    int64_t best_cost = -1;
+    for (int i = 0; i < (planes == 3 ? 2 : 3); ++i) {
+        const PrefillShape sh = cand[i];
+        const int lds = prefill_gemm_lds_bytes(planes, kdim, sh.waves, sh.depth);
+        if (lds > kPrefillLdsMax) continue;
+        const int64_t units = (int64_t)tiles_hint * pdiv_up(fdim, 32 * sh.waves);
+        const int64_t per_cu = (units + c - 1) / c;
+        const bool shared = sh.waves == 8 && sh.depth == 2 && 2 * lds <= kPrefillLdsMax && per_cu >= 2;
+        const int64_t cost = per_cu * 32 * sh.waves * (shared ? 7 : 8);
+        if (best_cost < 0 || cost < best_cost) {
+            best = sh;
+            best_cost = cost;
+        }
+    }
+    return best;
 }
 
 hipError_t launch_prefill_split(const Launch &L, const void *in, int in_dt, int64_t n,
@@ -886,35 +913,53 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
             return hipErrorInvalidValue;
         if (max_tiles < std::min(g.sg_experts, g.sg_tokens * g.sg_topk)) return hipErrorInvalidValue;
     }
-    const int waves = prefill_waves(g.fdim, g.kdim, planes,
-                                    tiles_hint > 0 && tiles_hint < max_tiles ? tiles_hint : max_tiles,
-                                    L.cus);
+    PrefillShape sh = prefill_shape(
+        g.fdim, g.kdim, planes, tiles_hint > 0 && tiles_hint < max_tiles ? tiles_hint : max_tiles,
+        L.cus);
+    if (g.force_waves == 8 || g.force_waves == 12) {
+        // Built shapes: 8x4, 12x4 and 8x2 for one or two planes; 8x2 and
+        // 12x2 for three.
+        const int d = planes == 3 ? 2 : g.force_waves == 12 ? 4 : g.force_depth == 2 ? 2 : 4;
+        const PrefillShape f = {g.force_waves, d};
+        if (prefill_gemm_lds_bytes(planes, g.kdim, f.waves, f.depth) <= kPrefillLdsMax) sh = f;
+    }
     // One workgroup per (feature tile, tile) unit, rounded up to whole XCD
     // rounds; the kernel maps ids to units and retires the spare ones.
-    const dim3 grid((pdiv_up(g.fdim, 32 * waves) * max_tiles + 7) / 8 * 8);
-    const int lds_bytes = prefill_gemm_lds_bytes(planes, g.kdim, waves);
+    const dim3 grid((pdiv_up(g.fdim, 32 * sh.waves) * max_tiles + 7) / 8 * 8);
+    const int lds_bytes = prefill_gemm_lds_bytes(planes, g.kdim, sh.waves, sh.depth);
     if (lds_bytes > kPrefillLdsMax) return hipErrorInvalidValue;   // K too wide for the staging
     const size_t lds = (size_t)lds_bytes;
     hipError_t err = hipSuccess;
     auto go = [&](auto pl, auto gu) {
         constexpr int PL = decltype(pl)::value;
         constexpr bool GU = decltype(gu)::value;
-        auto with_waves = [&](auto wc) {
+        auto with_shape = [&](auto wc, auto dc) {
             constexpr int W = decltype(wc)::value;
+            constexpr int D = decltype(dc)::value;
             // More than 64 KiB of dynamic LDS must be allowed explicitly, once
             // per instantiation.
             static bool lds_ok = false;
             if (!lds_ok) {
                 err = hipFuncSetAttribute(
-                    reinterpret_cast<const void *>(&prefill_gemm_kernel<PL, GU, W>),
+                    reinterpret_cast<const void *>(&prefill_gemm_kernel<PL, GU, W, D>),
                     hipFuncAttributeMaxDynamicSharedMemorySize, kPrefillLdsMax);
                 if (err != hipSuccess) return;
                 lds_ok = true;
             }
-            GW_LAUNCH((prefill_gemm_kernel<PL, GU, W>), grid, dim3(64 * W), lds, L, a);
+            GW_LAUNCH((prefill_gemm_kernel<PL, GU, W, D>), grid, dim3(64 * W), lds, L, a);
         };
-        if (waves == 12) with_waves(std::integral_constant<int, 12>{});
-        else with_waves(std::integral_constant<int, 8>{});
+        using I2 = std::integral_constant<int, 2>;
+        using I4 = std::integral_constant<int, 4>;
+        using I8 = std::integral_constant<int, 8>;
+        using I12 = std::integral_constant<int, 12>;
+        if constexpr (PL == 3) {
+            if (sh.waves == 12) with_shape(I12{}, I2{});
+            else with_shape(I8{}, I2{});
+        } else {
+            if (sh.waves == 12) with_shape(I12{}, I4{});
+            else if (sh.depth == 2) with_shape(I8{}, I2{});
+            else with_shape(I8{}, I4{});
+        }
     };
     using P1 = std::integral_constant<int, 1>;
     using P2 = std::integral_constant<int, 2>;

@@ -246,3 +246,42 @@ def test_self_grouped_equals_tile_list(ctx, monkeypatch, shape, E, K, T, x_dtype
     assert ok, (rel_rms, worst, bound)
     for b in (xb, lb, buf):
         b.free()
+
+
+@pytest.mark.parametrize("shape,E,K,T,x_dtype,seed", [
+    (QWEN3, 128, 8, 8, gw.BF16, 1),      # config 3's batch: one plane in, two for down
+    (SMALL, 16, 4, 72, gw.F16, 2),       # two planes in, several tiles per expert (tile list)
+    (GPTOSS, 12, 4, 20, gw.F32, 3),      # three planes: 2-deep rings only
+    (SMALL, 256, 8, 32, gw.BF16, 4),     # 32 KB of logits: past the 8x2 ring, read in place
+], ids=["qwen3-t8", "small-f16-t72", "gptoss-f32-t20", "small-e256-t32"])
+def test_gemm_shapes_bit_identical(ctx, monkeypatch, shape, E, K, T, x_dtype, seed):
+    """The grouped GEMMs run 8 waves with a 4-deep ring, 12 waves (4-deep), or 8
+    waves with a 2-deep ring held to 128 VGPRs so that two workgroups share a
+    CU; the launcher picks one per launch and GODWIT_PREFILL_SHAPE forces one at
+    runner creation.  Every shape gives the same bytes (each output keeps its
+    chunk and MFMA order), and the chosen one equals the oracle."""
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _make_layer(ctx, shape, E, 2700 + seed)
+    r = rng(2800 + seed)
+    xb, xw = _x(ctx, r, T, H, x_dtype)
+    logits = _zipf_logits(r, T, E, K)
+    lb = ctx.buffer(logits)
+    runs = {}
+    for forced in ("", "8x4", "12x4", "8x2"):
+        monkeypatch.setenv("GODWIT_PREFILL_SHAPE", forced)
+        runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+        runs[forced] = _run(ctx, runner, layout, buf, E, K, xb, x_dtype, lb, T, H,
+                            "prefill_forward")
+        runner.close()
+    for forced in ("8x4", "12x4", "8x2"):
+        for i in range(4):
+            assert np.array_equal(runs[forced][i], runs[""][i]), (forced, i)
+    got, _, ids, wts = runs[""]
+    ref, rids, rw = oracle.moe_layer([e.oracle_expert() for e in experts], K, logits, xw, H, F,
+                                     shape["oact"])
+    assert np.array_equal(ids, rids)
+    _close_batch(got, ref)
+    rel_rms, worst, bound, ok = layer_check(got, ref)
+    assert ok, (rel_rms, worst, bound)
+    for b in (xb, lb, buf):
+        b.free()
