@@ -70,7 +70,7 @@ GATE_UP_TRAFFIC_BYTES = 35_944_526
 # The same for the prefill gate_up GEMM launch (512 tokens, seed 1):
 # `bench.py --workload prefill` under rocprofv3 --pmc, the copy scale of the
 # decode run (profiles/prefill_gemm_gptoss_512.md).
-PREFILL_GATE_UP_TRAFFIC_BYTES = 1_241_689_122
+PREFILL_GATE_UP_TRAFFIC_BYTES = 1_294_336_732
 
 
 def build_model(ctx, gw, lay, seed: int):
