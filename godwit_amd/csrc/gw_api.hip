@@ -566,6 +566,7 @@ struct gw_expert_runner {
     int prefill_above = 1;           // batches larger than this run the grouped GEMMs
     int self_group_max = 32;         // grouped batches up to this size group inside the GEMMs
     int gemm_waves = 0, gemm_depth = 0;   // forced grouped-GEMM shape (0: chosen per launch)
+    int fused_combine_max = 32;      // grouped batches up to this size combine inside the down GEMM
     int ring_next = 0;
     int ring_used = 0;
 };
@@ -645,6 +646,8 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     r->prefill_above = pa < 1 ? 1 : pa > gw::kMaxTokens ? gw::kMaxTokens : pa;
     const int sg = get_env_int("GODWIT_SELF_GROUP_TOKENS", 32);
     r->self_group_max = sg < 0 ? 0 : sg > 32 ? 32 : sg;
+    const int fc = get_env_int("GODWIT_FUSED_COMBINE_TOKENS", 32);
+    r->fused_combine_max = fc < 0 ? 0 : fc;
     if (const char *shape = getenv("GODWIT_PREFILL_SHAPE")) {
         int w = 0, d = 0;
         if (sscanf(shape, "%dx%d", &w, &d) == 2 && (w == 8 || w == 12) && (d == 2 || d == 4)) {
@@ -1069,6 +1072,7 @@ struct PrefillScratch {
     uint16_t *xsplit;   // [planes][T, hidden] bf16 planes of a fp16 or fp32 x
     uint16_t *act;      // [2][N, inter] bf16 planes of the fp16 activations
     float *y;
+    uint32_t *arrive;   // [T, ceil(hidden / 256)] combine counters, zero between launches
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1097,6 +1101,8 @@ size_t prefill_layout(const gw_expert_runner *r, int T, int K, int E, char *base
     s.xsplit = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * 3 * (size_t)T * r->hidden));
     s.act = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * 2 * N * r->inter));
     s.y = reinterpret_cast<float *>(take(sizeof(float) * N * r->hidden));
+    s.arrive = reinterpret_cast<uint32_t *>(
+        take(sizeof(uint32_t) * (size_t)T * (size_t)((r->hidden + 255) / 256)));
     if (ps) *ps = s;
     return o;
 }
@@ -1124,6 +1130,11 @@ extern "C" int gw_expert_runner_reserve_prefill(gw_expert_runner *r, int32_t max
     r->pf_buf = nullptr;
     r->pf_tokens = r->pf_topk = r->pf_experts = 0;
     GW_HIP(hipMalloc(&r->pf_buf, bytes));
+    PrefillScratch ps;
+    prefill_layout(r, T, K, E, static_cast<char *>(r->pf_buf), &ps);
+    GW_HIP(hipMemsetAsync(ps.arrive, 0, sizeof(uint32_t) * (size_t)T * ((r->hidden + 255) / 256),
+                          r->ctx->stream));
+    GW_HIP(hipStreamSynchronize(r->ctx->stream));
     r->pf_tokens = T;
     r->pf_topk = K;
     r->pf_experts = E;
@@ -1181,6 +1192,13 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
                                         ps.ntiles, max_tiles));
     }
     const gw::Sections sec = sections_of(r->offsets);
+    // Up to fused_combine_max tokens the combine runs inside the down GEMM
+    // (the workgroup that completes a token's feature tile sums it), saving a
+    // launch; larger batches keep the combine kernel, since the coherent
+    // write-through of y costs more there than the launch (512 tokens: down
+    // 238 -> 270 us against a 9 us combine).
+    const bool fuse_combine = T <= r->fused_combine_max &&
+                              (int64_t)sizeof(float) * T * K * r->hidden < ((int64_t)1 << 31);
     gw::PrefillGemm g;
     g.force_waves = r->gemm_waves;
     g.force_depth = r->gemm_depth;
@@ -1238,10 +1256,19 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
         g.act_out = nullptr;
         g.act_plane = 0;
         g.y_out = ps.y;
+        g.y_bytes = (int64_t)sizeof(float) * T * K * r->hidden;
+        if (fuse_combine) {
+            g.arrive = ps.arrive;
+            g.comb_w = ps.weights;
+            g.comb_out = a->out;
+            g.comb_out_bf16 = a->out_bf16;
+            g.comb_topk = K;
+            g.comb_residual = out_mode == 2 ? 1 : 0;
+        }
         ProfScope p(ctx, "prefill_down");
         GW_HIP(gw::launch_prefill_gemm(p.launch(L), false, 2, g, max_tiles, T * K));
     }
-    {
+    if (!fuse_combine) {
         ProfScope p(ctx, "prefill_combine");
         GW_HIP(gw::launch_prefill_combine(p.launch(L), ps.y, ps.weights, T, K, (int)r->hidden,
                                           a->out, a->out_bf16, out_mode == 2 ? 1 : 0));

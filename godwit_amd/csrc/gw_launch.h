@@ -102,6 +102,16 @@ struct PrefillGemm {
     // whatever is asked; a shape whose LDS does not fit is not forced.  Same
     // results either way.
     int force_waves = 0, force_depth = 0;
+    // Down launch with the combine fused in (arrive != null): arrive holds
+    // T x ceil(fdim / 256) zeroed counters (left zeroed), y_bytes the size of
+    // y_out, and the combine writes out [T, fdim] (+ out_bf16) from weights
+    // [T, K], adding to out when residual.
+    uint32_t *arrive = nullptr;
+    int64_t y_bytes = 0;
+    const float *comb_w = nullptr;
+    float *comb_out = nullptr;
+    uint16_t *comb_out_bf16 = nullptr;
+    int comb_topk = 0, comb_residual = 0;
 };
 int prefill_max_tiles(int T, int K, int E);
 // True when a batch is small enough for the self-grouped GEMMs (every expert

@@ -47,6 +47,7 @@ typedef const __attribute__((address_space(1))) u32x4v g_u32x4v;
 typedef const __attribute__((address_space(1))) uint8_t g_u8c;
 
 constexpr int kPT = 32;                 // tokens per tile (MFMA columns)
+constexpr int kCachePolicySc1 = 16;     // buffer access cache policy: device-coherent (sc1)
 constexpr int kKC = 8;                  // 32-element blocks per staged activation chunk
 constexpr int kPrefillMaxExperts = 256;
 
@@ -216,6 +217,16 @@ struct GemmArgs {
     const int32_t *sg_ids;
     int32_t *sg_ids_out;
     float *sg_w_out;
+    // Combine fused into the down launch (arrive != null): y rows are stored
+    // device-coherent, every entry counts itself on arrive[token * tiles +
+    // feature tile], and the workgroup whose count completes a token's tile
+    // sums that tile into comb_out (weights comb_w [T, K], router order).
+    uint32_t *arrive;
+    uint32_t y_bytes;             // bytes of y_out (below 2^31)
+    const float *comb_w;
+    float *comb_out;
+    uint16_t *comb_out_bf16;
+    int comb_topk, comb_residual;
 };
 
 // A batch of at most this many tokens gives every expert at most one tile.
@@ -304,7 +315,7 @@ template <int N> __device__ __forceinline__ void lds_wait()
 // W waves, D-deep ring.  The 8-wave, 2-deep form is held to 128 VGPRs (four
 // waves per SIMD), so two of its workgroups share a CU when their LDS fits;
 // the others hold ~165 VGPRs and one workgroup per CU.
-template <int PL, bool GATE_UP, int W, int D>
+template <int PL, bool GATE_UP, int W, int D, bool COMB>
 __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm_kernel(GemmArgs a)
 {
     // W waves, 32 features each: a workgroup computes kF features x kPT entries.
@@ -715,6 +726,8 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
             tile[c * kF + rl] = acc[v] + bv[v];
         }
         __syncthreads();
+        const __amdgpu_buffer_rsrc_t yres =
+            __builtin_amdgcn_make_buffer_rsrc(a.y_out, (short)0, (int)a.y_bytes, 0x00020000);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             // kPT entries x kF / 4 pieces = 4 kThreads
@@ -723,7 +736,67 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
             const int row0 = f0 + piece * 4;
             if (t < ntok && row0 + 4 <= a.fdim) {
                 const float4 v = *reinterpret_cast<const float4 *>(tile + t * kF + piece * 4);
-                *reinterpret_cast<float4 *>(a.y_out + (int64_t)ent[t] * a.fdim + row0) = v;
+                const int64_t o = (int64_t)ent[t] * a.fdim + row0;
+                if constexpr (COMB)   // write-through (sc1): read back by another workgroup
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, v), yres,
+                                                           (int)(o * 4), 0, kCachePolicySc1);
+                else
+                    *reinterpret_cast<float4 *>(a.y_out + o) = v;
+            }
+        }
+        if constexpr (COMB) {
+            // Each thread waits for its own stores, then one relaxed count per
+            // entry of the tile; the count that reaches K hands the token's
+            // tile to this workgroup (and clears the counter for the next
+            // launch: all K entries have counted).
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            int *todo = reinterpret_cast<int *>(xring + kPT * kF * 4);   // [kPT], then the count
+            if (threadIdx.x == 0) todo[kPT] = 0;
+            __syncthreads();
+            const int K = a.comb_topk;
+            if ((int)threadIdx.x < ntok) {
+                const int tok = ent[threadIdx.x] / K;
+                uint32_t *cnt = a.arrive + (int64_t)tok * nft + fidx;
+                const uint32_t before =
+                    __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (before == (uint32_t)(K - 1)) {
+                    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    todo[atomicAdd(&todo[kPT], 1)] = tok;
+                }
+            }
+            __syncthreads();
+            const int ndo = todo[kPT];
+            // out[tok, row] = sum_k w[tok, k] * y[tok*K + k, row], product and
+            // sum rounded separately in router order (expert_accumulate), as
+            // prefill_combine_kernel does; y read coherently (sc1).
+            for (int idx = (int)threadIdx.x; idx < ndo * (kF / 4); idx += kThreads) {
+                const int tok = todo[idx / (kF / 4)], row0 = f0 + (idx % (kF / 4)) * 4;
+                if (row0 + 4 > a.fdim) continue;
+                u32x4v yv[kMaxTopK];
+#pragma unroll
+                for (int k = 0; k < kMaxTopK; ++k)
+                    if (k < K)
+                        yv[k] = __builtin_amdgcn_raw_buffer_load_b128(
+                            yres, (int)((((int64_t)tok * K + k) * a.fdim + row0) * 4), 0,
+                            kCachePolicySc1);
+                float d[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int k = 0; k < kMaxTopK; ++k) {
+                    if (k < K) {
+                        const float w = a.comb_w[(int64_t)tok * K + k];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            d[i] = add_scaled_rn(d[i], __uint_as_float(yv[k][i]), w);
+                    }
+                }
+                const int64_t o = (int64_t)tok * a.fdim + row0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float r = a.comb_residual ? a.comb_out[o + i] + d[i] : d[i];
+                    a.comb_out[o + i] = r;
+                    if (a.comb_out_bf16) a.comb_out_bf16[o + i] = f32_to_bf16_bits(r);
+                }
             }
         }
     }
@@ -905,6 +978,23 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
     a.sg_ids = g.sg_ids;
     a.sg_ids_out = g.sg_ids_out;
     a.sg_w_out = g.sg_w_out;
+    a.arrive = nullptr;
+    a.y_bytes = 0;
+    a.comb_w = g.comb_w;
+    a.comb_out = g.comb_out;
+    a.comb_out_bf16 = g.comb_out_bf16;
+    a.comb_topk = g.comb_topk;
+    a.comb_residual = g.comb_residual;
+    if (!gate_up) {
+        // y is addressed through a 32-bit buffer range.
+        if (g.y_bytes <= 0 || g.y_bytes >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+        a.y_bytes = (uint32_t)g.y_bytes;
+        if (g.arrive) {
+            if (!g.comb_w || !g.comb_out || g.comb_topk < 1 || g.comb_topk > kMaxTopK)
+                return hipErrorInvalidValue;
+            a.arrive = g.arrive;
+        }
+    }
     if (g.sg_tokens > 0) {
         // The workgroup routes or reads T*K <= 256 entries, one per thread,
         // and stages T*E <= 8192 logits in its staging ring.
@@ -936,17 +1026,27 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
         auto with_shape = [&](auto wc, auto dc) {
             constexpr int W = decltype(wc)::value;
             constexpr int D = decltype(dc)::value;
-            // More than 64 KiB of dynamic LDS must be allowed explicitly, once
-            // per instantiation.
-            static bool lds_ok = false;
-            if (!lds_ok) {
-                err = hipFuncSetAttribute(
-                    reinterpret_cast<const void *>(&prefill_gemm_kernel<PL, GU, W, D>),
-                    hipFuncAttributeMaxDynamicSharedMemorySize, kPrefillLdsMax);
-                if (err != hipSuccess) return;
-                lds_ok = true;
+            auto with_comb = [&](auto cc) {
+                constexpr bool C = decltype(cc)::value;
+                // More than 64 KiB of dynamic LDS must be allowed explicitly,
+                // once per instantiation.
+                static bool lds_ok = false;
+                if (!lds_ok) {
+                    err = hipFuncSetAttribute(
+                        reinterpret_cast<const void *>(&prefill_gemm_kernel<PL, GU, W, D, C>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kPrefillLdsMax);
+                    if (err != hipSuccess) return;
+                    lds_ok = true;
+                }
+                GW_LAUNCH((prefill_gemm_kernel<PL, GU, W, D, C>), grid, dim3(64 * W), lds, L, a);
+            };
+            // The fused combine is compiled into the down kernel only.
+            if constexpr (!GU) {
+                if (a.arrive) with_comb(std::true_type{});
+                else with_comb(std::false_type{});
+            } else {
+                with_comb(std::false_type{});
             }
-            GW_LAUNCH((prefill_gemm_kernel<PL, GU, W, D>), grid, dim3(64 * W), lds, L, a);
         };
         using I2 = std::integral_constant<int, 2>;
         using I4 = std::integral_constant<int, 4>;

@@ -254,7 +254,9 @@ int gw_expert_apply_assignments_async(gw_expert_runner *runner, const void *inpu
  * routed and grouped inside the grouped GEMMs themselves (every expert then
  * holds at most one 32-entry tile); GODWIT_SELF_GROUP_TOKENS at runner
  * creation (0..32, default 32) lowers that bound, larger batches use the
- * group kernel's tile list.  Enqueue only. */
+ * group kernel's tile list.  Up to GODWIT_FUSED_COMBINE_TOKENS tokens (default
+ * 32, 0 disables) the weighted combine runs inside the down GEMM instead of
+ * a kernel of its own; results are the same bytes either way.  Enqueue only. */
 typedef struct gw_moe_layer_args {
     const uint8_t *experts_base;
     int64_t expert_stride;

@@ -285,3 +285,48 @@ def test_gemm_shapes_bit_identical(ctx, monkeypatch, shape, E, K, T, x_dtype, se
     assert ok, (rel_rms, worst, bound)
     for b in (xb, lb, buf):
         b.free()
+
+
+@pytest.mark.parametrize("shape,E,K,T,x_dtype,seed", [
+    (QWEN3, 128, 8, 8, gw.BF16, 1),      # self-grouped, 8x2 down GEMM, 8 counts per tile
+    (SMALL, 16, 4, 72, gw.F16, 2),       # tile list, several tiles per expert
+    (GPTOSS, 12, 4, 20, gw.F32, 3),      # 2880 rows: a partial last feature tile
+    (SMALL, 8, 1, 40, gw.BF16, 4),       # top-1: every count completes at once
+], ids=["qwen3-t8", "small-f16-t72", "gptoss-f32-t20", "small-top1-t40"])
+def test_fused_combine_equals_kernel(ctx, monkeypatch, shape, E, K, T, x_dtype, seed):
+    """The down GEMM combines in its epilogue: each entry counts itself on its
+    (token, feature tile) and the workgroup whose count completes the tile sums
+    it in router order (y stored and read device-coherent).  By default batches
+    of up to 32 tokens do so; GODWIT_FUSED_COMBINE_TOKENS sets the bound (0: the
+    separate combine kernel always).  Bit-identical to the combine kernel, on
+    three calls in a row (the counters return to zero), and equal to the oracle."""
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _make_layer(ctx, shape, E, 2900 + seed)
+    r = rng(3000 + seed)
+    xb, xw = _x(ctx, r, T, H, x_dtype)
+    logits = _zipf_logits(r, T, E, K) if K > 1 else r.standard_normal((T, E)).astype(np.float32)
+    lb = ctx.buffer(logits)
+    runs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("GODWIT_FUSED_COMBINE_TOKENS", "0" if mode == "0" else "100000")
+        runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+        ctx.set_profiling(True)
+        ctx.profile_reset()
+        runs[mode] = [_run(ctx, runner, layout, buf, E, K, xb, x_dtype, lb, T, H,
+                           "prefill_forward") for _ in range(3)]
+        n_comb = ctx.profile("prefill_combine")[1]
+        ctx.set_profiling(False)
+        assert n_comb == (0 if mode == "1" else 3), (mode, n_comb)
+        runner.close()
+    for call in range(3):
+        for i in range(4):
+            assert np.array_equal(runs["1"][call][i], runs["0"][0][i]), (call, i)
+    got, _, ids, wts = runs["1"][0]
+    ref, rids, rw = oracle.moe_layer([e.oracle_expert() for e in experts], K, logits, xw, H, F,
+                                     shape["oact"])
+    assert np.array_equal(ids, rids)
+    _close_batch(got, ref)
+    rel_rms, worst, bound, ok = layer_check(got, ref)
+    assert ok, (rel_rms, worst, bound)
+    for b in (xb, lb, buf):
+        b.free()
