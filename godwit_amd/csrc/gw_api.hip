@@ -564,7 +564,7 @@ struct gw_expert_runner {
     void *pf_buf = nullptr;
     bool fused_enabled = false;      // GODWIT_FUSED_LAYER=1 at creation turns it on
     int prefill_above = 1;           // batches larger than this run the grouped GEMMs
-    int self_group_max = 32;         // grouped batches up to this size group inside the GEMMs
+    int self_group_max = 16;         // grouped batches up to this size group inside the GEMMs
     int gemm_waves = 0, gemm_depth = 0;   // forced grouped-GEMM shape (0: chosen per launch)
     int fused_combine_max = 32;      // grouped batches up to this size combine inside the down GEMM
     int ring_next = 0;
@@ -644,7 +644,10 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     r->fused_enabled = env && env[0] == '1';
     const int pa = get_env_int("GODWIT_PREFILL_ABOVE", 1);
     r->prefill_above = pa < 1 ? 1 : pa > gw::kMaxTokens ? gw::kMaxTokens : pa;
-    const int sg = get_env_int("GODWIT_SELF_GROUP_TOKENS", 32);
+    // 16: at 32 tokens the selection in every gate_up workgroup (three rounds
+    // of workgroups per CU) costs more than the group kernel (Qwen3: 5478
+    // against 5006 us per step); at 16 the two tie, at 8 self-grouping wins.
+    const int sg = get_env_int("GODWIT_SELF_GROUP_TOKENS", 16);
     r->self_group_max = sg < 0 ? 0 : sg > 32 ? 32 : sg;
     const int fc = get_env_int("GODWIT_FUSED_COMBINE_TOKENS", 32);
     r->fused_combine_max = fc < 0 ? 0 : fc;

@@ -75,7 +75,7 @@ def _run(ctx, runner, layout, buf, E, K, xb, x_dtype, lb, T, H, fn="prefill_forw
     (SMALL, 16, 4, 72, gw.BF16, 1),      # experts with 2-3 tiles, partial feature tiles
     (QWEN3, 32, 8, 24, gw.F16, 2),       # two activation planes, no biases, SiLU-GLU
     (GPTOSS, 12, 4, 20, gw.F32, 3),      # three planes, 2880-wide K (11.25 chunks)
-    (SMALL, 200, 4, 32, gw.BF16, 4),     # self-grouped: 200 experts, 32 tokens
+    (SMALL, 200, 4, 32, gw.BF16, 4),     # 200 experts, 32 tokens routed in the group kernel
     (SMALL, 256, 8, 40, gw.BF16, 5),     # route kernel, then a scan over 256 experts
     (SMALL, 8, 2, 2048, gw.BF16, 6),     # ~16 tiles per expert: many units per XCD eighth
 ], ids=["small-bf16", "qwen3-f16", "gptoss-f32", "small-e200-t32", "small-e256-t40",
