@@ -22,7 +22,7 @@ LIB = os.path.join(HERE, "libgodwit_hip.so")
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["gw_kernels.hip", "gw_prefill.hip", "gw_model.hip", "gw_api.hip"]
+SOURCES = ["gw_kernels.hip", "gw_decode.hip", "gw_prefill.hip", "gw_model.hip", "gw_api.hip"]
 OBJDIR = os.path.join(HERE, "_build")
 
 FLAGS = [

@@ -559,10 +559,11 @@ struct gw_expert_runner {
     float *logits = nullptr;         // [kMaxTokens, kMaxExperts]
     Plan *staging = nullptr;         // pinned host mirror of `plans`
     unsigned *sync_buf = nullptr;    // fused layer exchange: counters | epochs | error word
+    uint64_t *xchg_buf = nullptr;    // one-kernel layer: tagged activation words (zeroed once)
     // prefill scratch, sized for pf_tokens tokens x pf_topk ranks x pf_experts
     int pf_tokens = 0, pf_topk = 0, pf_experts = 0;
     void *pf_buf = nullptr;
-    bool fused_enabled = false;      // GODWIT_FUSED_LAYER=1 at creation turns it on
+    bool decode_layer = true;        // one-token layers in one kernel (GODWIT_DECODE_LAYER=0: two)
     int prefill_above = 1;           // batches larger than this run the grouped GEMMs
     int self_group_max = 16;         // grouped batches up to this size group inside the GEMMs
     int gemm_waves = 0, gemm_depth = 0;   // forced grouped-GEMM shape (0: chosen per launch)
@@ -571,7 +572,7 @@ struct gw_expert_runner {
     int ring_used = 0;
 };
 
-static constexpr int kSyncEpochWords = 8192;   // >= any fused grid (2 x CUs)
+static constexpr int kSyncEpochWords = gw::kSyncEpochCapacity;
 
 static gw::SyncArgs sync_of(gw_expert_runner *r)
 {
@@ -593,6 +594,7 @@ extern "C" int gw_expert_runner_destroy(gw_expert_runner *r)
     (void)hipFree(r->logits);
     (void)hipHostFree(r->staging);
     (void)hipFree(r->sync_buf);
+    (void)hipFree(r->xchg_buf);
     (void)hipFree(r->pf_buf);
     delete r;
     return GW_OK;
@@ -635,13 +637,16 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     const size_t sync_bytes = sizeof(unsigned) * (gw::kSyncWords + kSyncEpochWords + 64);
     if (e == hipSuccess) e = hipMalloc((void **)&r->sync_buf, sync_bytes);
     if (e == hipSuccess) e = hipMemset(r->sync_buf, 0, sync_bytes);
+    const size_t xchg_bytes = sizeof(uint64_t) * gw::kDecodeMaxGrid * gw::kDecodeXWords;
+    if (e == hipSuccess) e = hipMalloc((void **)&r->xchg_buf, xchg_bytes);
+    if (e == hipSuccess) e = hipMemset(r->xchg_buf, 0, xchg_bytes);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         gw_expert_runner_destroy(r);
         return fail(e == hipErrorOutOfMemory ? GW_ERR_OOM : GW_ERR_HIP, "runner scratch: %s",
                     hipGetErrorString(e));
     }
-    const char *env = getenv("GODWIT_FUSED_LAYER");
-    r->fused_enabled = env && env[0] == '1';
+    r->decode_layer = get_env_int("GODWIT_DECODE_LAYER", 1) != 0;
     const int pa = get_env_int("GODWIT_PREFILL_ABOVE", 1);
     r->prefill_above = pa < 1 ? 1 : pa > gw::kMaxTokens ? gw::kMaxTokens : pa;
     // 16: at 32 tokens the selection in every gate_up workgroup (three rounds
@@ -1021,16 +1026,37 @@ static int moe_layer_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int o
     route.ids_out = a->routing_ids;
     route.w_out = a->routing_weights;
     const gw::Sections sec = sections_of(r->offsets);
-    // One token: the whole layer in one kernel when the shape and the
-    // occupancy allow it.
-    if (a->tokens == 1 && r->fused_enabled && out_mode == 0) {
-        const int grid = gw::fused_layer_grid(L, (int)r->hidden, (int)r->inter, a->x_dtype,
-                                              (int)a->top_k, (int)a->expert_count);
-        if (grid > 0 && grid <= kSyncEpochWords) {
+    // One token: the whole layer in one kernel when the shape, the dtype and
+    // the occupancy allow it.
+    if (a->tokens == 1 && r->decode_layer) {
+        gw::DecodeArgs d = {};
+        size_t lds = 0;
+        const int grid = gw::decode_layer_plan(L, (int)r->hidden, (int)r->inter, a->x_dtype,
+                                               (int)a->top_k, (int)a->expert_count,
+                                               a->expert_stride, r->bias_dt, &d, &lds);
+        if (grid > 0) {
+            d.logits = logits;
+            d.experts = (int)a->expert_count;
+            d.top_k = (int)a->top_k;
+            d.base = a->experts_base;
+            d.stride = a->expert_stride;
+            d.ids_out = a->routing_ids;
+            d.w_out = a->routing_weights;
+            d.x = a->x;
+            d.hidden = (int)r->hidden;
+            d.inter = (int)r->inter;
+            d.sec = sec;
+            d.bias_dt = r->bias_dt;
+            d.xchg = r->xchg_buf;
+            d.act_kind = r->act;
+            d.limit = r->limit;
+            d.alpha = r->alpha;
+            d.out = a->out;
+            d.out_bf16 = a->out_bf16;
+            d.accumulate = out_mode;
+            d.sync = sync_of(r);
             ProfScope ps(ctx, "moe_layer");
-            GW_HIP(gw::launch_fused_layer(ps.launch(L), grid, route, a->x, a->x_dtype, (int)r->hidden,
-                                          (int)r->inter, sec, r->bias_dt, r->act_buf, r->act,
-                                          r->limit, r->alpha, a->out, a->out_bf16, sync_of(r)));
+            GW_HIP(gw::launch_decode_layer(ps.launch(L), grid, lds, a->x_dtype, d));
             return GW_OK;
         }
     }

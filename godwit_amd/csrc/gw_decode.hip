@@ -1,0 +1,576 @@
+// gw_decode.hip — the one-token MoE layer as ONE kernel (decode, batch 1).
+//
+// TransformerLayer.forward's MoE block for one token
+// (Sources/Godwit/Runtime/TransformerLayer.swift:140-238): routing
+// (Router.select, Runtime/Router.swift:78-98), the gate_up GEMV with bias and
+// activation (Metal/MoE/expert.metal:311-368 then :82-102 or :380-393), the
+// down GEMV with bias and the weighted combine (expert.metal:107-116), in one
+// launch of one 512-thread workgroup per compute unit.
+//
+// At batch 1 the layer is two dependent streams of weights: k experts' gate_up
+// rows (4 x 8.8 MB for GPT-OSS), then their down rows (4 x 4.4 MB), which
+// need every activation of their expert.  The down rows' addresses are known
+// as soon as the routing is, so a workgroup issues its whole share of both
+// right after routing: its gate_up rows into a ring of registers (consumed as
+// they land) and, behind them, its down rows with their scales and biases
+// straight into LDS by buffer LDS-DMA (no registers held).  Loads of a wave
+// complete in issue order, so the gate_up rows land first; the activations
+// are exchanged across the grid while the down rows are still streaming in,
+// and the down products are computed from LDS once both are there.  The two
+// streams thus share one ramp, and the exchange waits behind the down stream
+// instead of adding to it.
+//
+// The exchange: a workgroup stores its activations with their launch tag in
+// 8-byte words (device-coherent stores, no wait); every workgroup polls all
+// words until each carries the current tag (a bounded spin: a wait that gives
+// up sets an error word, read by gw_expert_runner_sync_errors, so no
+// workgroup ever waits unboundedly) and stages the activations in LDS.  The
+// grid must be co-resident (one workgroup per CU; the host checks occupancy).
+//
+// The gate_up rows are computed exactly as in the two-kernel form
+// (gate_up_kernel): the same widening, block dots, scale products, lane order
+// and reductions, so the activations are the same bytes.  The down rows are
+// split over the lanes differently (see step 6), so their fp32 sums may round
+// differently; both forms hold the reference's tolerance.
+#include <hip/hip_ext.h>
+
+#include <type_traits>
+
+#include "gw_device.h"
+#include "gw_launch.h"
+#include "gw_route.h"
+
+namespace gw {
+
+namespace {
+
+constexpr int kDT = 512;          // threads per workgroup
+constexpr int kDW = kDT / 64;     // waves per workgroup
+constexpr int kDmaWaves = kDW;   // waves issuing the down stream's LDS-DMA
+constexpr int kChunk = 1024;      // bytes one wave-wide 16-byte LDS-DMA moves
+constexpr int kRsrcWord3 = 0x00020000;   // raw (untyped) buffer access
+constexpr int kSc1 = 16;                 // buffer cache policy: device-coherent (sc1)
+constexpr uint32_t kOutOfRange = 0x80000000u;   // buffer offset past any layer (reads zero)
+constexpr int kXWords = kDecodeXWords;   // exchange words per workgroup (3 activations each)
+constexpr unsigned kSpinLimit = 1u << 18;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4 g_u32x4;
+typedef const __attribute__((address_space(1))) uint8_t g_u8;
+typedef const __attribute__((address_space(1))) uint32_t g_u32;
+typedef __attribute__((address_space(3))) void l_void;
+
+template <int TPR_, int M_> struct DShape {
+    static constexpr int TPR = TPR_;   // lanes per row
+    static constexpr int M = M_;       // 16-byte blocks per lane (lane l: l, l+TPR, ...)
+};
+
+}  // namespace
+
+// Byte layout of the kernel's LDS (host and device compute the same).
+__host__ __device__ inline DecodeLds decode_lds(int hidden, int inter, int top_k, int nrmax,
+                                               int sw_total, int rows_per_wg)
+{
+    DecodeLds l;
+    const int hb = hidden / 32, fb = inter / 32;
+    l.route = 0;                                   // int32 ids[8], float w[8]
+    l.xs = 64;                                     // x, 20 dwords per block
+    l.actl = l.xs + hb * 80;                       // this workgroup's fp16 activations
+    l.dma = (l.actl + rows_per_wg + 255) & ~255;   // the down stream (+ one spare chunk)
+    const int dma_bytes = (top_k * sw_total + kChunk - 1) / kChunk * kChunk + kChunk;
+    l.as = l.dma + dma_bytes;                      // all activations, 20 dwords per block
+    l.vals = l.as + top_k * fb * 80;               // down outputs [top_k][nrmax]
+    l.total = l.vals + top_k * nrmax * 4;
+    return l;
+}
+
+// Per-expert windows of the down stream in LDS: the workgroup's down rows,
+// their scale bytes and their biases, each from a 16-byte aligned start.
+__host__ __device__ inline void decode_windows(int hidden, int inter, int nrmax, int bias_bytes,
+                                               int &sww, int &sws, int &swb)
+{
+    (void)hidden;
+    const int fb = inter / 32;
+    sww = nrmax * fb * 16;
+    sws = (nrmax * fb + 15 + 15) & ~15;
+    swb = bias_bytes > 0 ? (nrmax * bias_bytes + 15 + 15) & ~15 : 0;
+}
+
+namespace {
+
+__device__ __forceinline__ void store_coherent_u16(uint16_t *p, uint16_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The bias element of a gate_up row is read with the stage as the aligned
+// dword containing it (one load whatever the dtype).
+__device__ __forceinline__ float bias_of(uint32_t bw, int bshift, int bias_dt)
+{
+    if (bias_dt < 0) return 0.0f;
+    if (bias_dt == DT_F32) return __uint_as_float(bw);
+    const uint16_t b = (uint16_t)(bw >> bshift);
+    return bias_dt == DT_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+__device__ __forceinline__ void widen_v(const u32x4 &w, WBlock<DT_BF16> &o)
+{ uint4 v; v.x = w.x; v.y = w.y; v.z = w.z; v.w = w.w; widen<DT_BF16>(v, o); }
+__device__ __forceinline__ void widen_v(const u32x4 &w, WBlock<DT_F16> &o)
+{ uint4 v; v.x = w.x; v.y = w.y; v.z = w.z; v.w = w.w; widen<DT_F16>(v, o); }
+
+// The value of the up row of a gate/up pair, whose segment follows the gate
+// row's segment in the wave: the next 16-lane row (permlane16 swap) or the
+// other half of this 16-lane row (row rotate by 8), without going through LDS.
+template <int TPR> __device__ __forceinline__ float next_segment(float v)
+{
+    if constexpr (TPR == 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                        false, false);
+        return __uint_as_float(p[1]);
+    } else {
+        static_assert(TPR == 8, "row segments are 8 or 16 lanes");
+        return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v),
+                                                          0x128, 0xF, 0xF, false));
+    }
+}
+
+}  // namespace
+
+// XK: x dtype (bf16 or fp16).  GS / DS: row shapes of gate_up (hidden wide)
+// and down (intermediate wide) rows.  NSG: gate_up stages (of kDW * 64 / TPR
+// rows) a workgroup's share fills; they are all in flight at once.  NDMA:
+// 1 KiB LDS-DMA pieces each of waves 1.. issues for the down stream.
+template <int XK, class GS, int NSG, class DS, int NDMA>
+__global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
+{
+    constexpr int TPG = GS::TPR, MG = GS::M, SEGG = 64 / TPG, RGW = kDW * SEGG;
+    constexpr int TPD = DS::TPR, MD = DS::M, SEGD = 64 / TPD, RGD = kDW * SEGD;
+    constexpr int BD = XL<XK>::kBlockDw;
+    constexpr int BDA = XL<DT_F16>::kBlockDw;
+    extern __shared__ __align__(16) uint32_t lds[];
+    uint8_t *lds8 = reinterpret_cast<uint8_t *>(lds);
+
+    const int H = a.hidden, F = a.inter, K = a.top_k;
+    const int hb = H >> 5, fb = F >> 5;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int b = blockIdx.x;
+    const int bsz = a.bias_dt == DT_F32 ? 4 : 2;
+    int sww, sws, swb;
+    decode_windows(H, F, a.nrmax, a.bias_dt >= 0 ? bsz : 0, sww, sws, swb);
+    const int swt = sww + sws + swb;
+    int p0, p1;                          // gate_up: (expert, feature) pairs [p0, p1)
+    slice_of(K * F, p0, p1);
+    int r0, r1;                          // down: output rows [r0, r1) of every expert
+    slice_of(H, r0, r1);
+    const int nr = r1 - r0;
+    const DecodeLds L = decode_lds(H, F, K, a.nrmax, swt, RGW * NSG);
+    int32_t *eid = reinterpret_cast<int32_t *>(lds8 + L.route);
+    float *ew = reinterpret_cast<float *>(lds8 + L.route + 32);
+    uint32_t *xs = reinterpret_cast<uint32_t *>(lds8 + L.xs);
+    uint16_t *actl = reinterpret_cast<uint16_t *>(lds8 + L.actl);
+    uint32_t *as = reinterpret_cast<uint32_t *>(lds8 + L.as);
+    float *vals = reinterpret_cast<float *>(lds8 + L.vals);
+    // Launches this workgroup has completed (written back at the end).
+    const unsigned epoch1 = a.sync.epochs[b] + 1;
+
+    // ---- 1. route (wave 0) while waves 1.. stage x -------------------------
+    if (wave == 0) {
+        int sid;
+        float w;
+        if (a.experts <= 128) select_one<2>(a.logits, a.experts, K, sid, w);
+        else select_one<4>(a.logits, a.experts, K, sid, w);
+        if (lane < K) {
+            eid[lane] = sid;
+            ew[lane] = w;
+            if (b == 0 && a.ids_out) a.ids_out[lane] = sid;
+            if (b == 0 && a.w_out) a.w_out[lane] = w;
+        }
+    } else {
+        stage_vector<XK>(xs, a.x, H, threadIdx.x - 64, kDT - 64);
+    }
+    __syncthreads();
+
+    const int segg = lane / TPG, tlg = lane % TPG;
+
+    // ---- 3. issue: every gate_up stage, then (waves 1..) the down stream ----
+    const int nrows = 2 * (p1 - p0);
+    const int two_f = 2 * F;
+    const float inv_two_f = 1.0f / (float)two_f;
+    const int64_t rbg = (int64_t)hb * 16;
+    u32x4 W[NSG][MG];
+    uint32_t SC[NSG][MG];
+    uint32_t BW[NSG];
+    int BSH[NSG];
+#pragma unroll
+    for (int s = 0; s < NSG; ++s) {
+        const int i = s * RGW + wave * SEGG + segg;
+        const int rg = 2 * p0 + (i < nrows ? i : 0);
+        int k, r;
+        divmod_small(rg, two_f, inv_two_f, k, r);
+        const uint8_t *ebase = a.base + (int64_t)eid[k] * a.stride;
+        const uint8_t *row = ebase + a.sec.gu_blocks + r * rbg;
+        const uint8_t *srow = ebase + a.sec.gu_scales + (int64_t)r * hb;
+#pragma unroll
+        for (int m = 0; m < MG; ++m) {
+            const int cb = min(tlg + m * TPG, hb - 1);
+            W[s][m] = __builtin_nontemporal_load((g_u32x4 *)row + cb);
+            SC[s][m] = ((g_u8 *)srow)[cb];
+        }
+        const uintptr_t ba = a.bias_dt >= 0
+                                 ? reinterpret_cast<uintptr_t>(ebase + a.sec.gu_bias + (int64_t)r * bsz)
+                                 : reinterpret_cast<uintptr_t>(srow);
+        BSH[s] = (int)(ba & 2u) * 8;
+        BW[s] = *(g_u32 *)(ba & ~(uintptr_t)3);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // The down stream's DMA pieces, issued just before the last gate_up stage
+    // is consumed: the earlier gate_up loads are in by then and the rest are
+    // queued, so every gate_up row lands ahead of the down stream and the
+    // exchange can complete while the down rows are still arriving.  Piece c
+    // of wave w is packed position (w + kDmaWaves*c) KiB of the per-expert
+    // windows [rows | scale bytes | biases] x top_k.  Every wave issues NDMA
+    // pieces (those past the end read zeros into the spare chunk without a
+    // memory access), so the compiler's load counts are the same on every
+    // path.  The pieces' experts are read from LDS before the first of them
+    // is issued (the compiler makes any LDS read after an LDS-DMA wait for
+    // every load in flight).
+    // This lane's activation blocks into registers, read with ds_read_b128
+    // written out: the compiler would make an LDS read after the LDS-DMA wait
+    // for every load in flight; x was stored before the barrier above.
+    uint4 X[MG][4];
+    {
+        const uint32_t xa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)xs;
+        u32x4 xv[MG][4];
+#pragma unroll
+        for (int m = 0; m < MG; ++m) {
+            const int cb = tlg + m * TPG;
+            const uint32_t addr = xa + (uint32_t)((cb < hb ? cb : 0) * BD * 4);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(xv[m][q]) : "v"(addr), "i"(q * 16));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int m = 0; m < MG; ++m)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                u32x4 v = xv[m][q];
+                asm volatile("" : "+v"(v));
+                X[m][q] = make_uint4(v.x, v.y, v.z, v.w);
+            }
+    }
+
+    // ---- 4. gate_up: consume the stages as they land -----------------------
+    static_assert(NSG >= 2, "the down stream is issued before the last gate_up stage");
+#pragma unroll
+    for (int s = 0; s < NSG; ++s) {
+        if (s == NSG - 1) {
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint8_t *>(a.base), (short)0, (int)a.base_bytes, kRsrcWord3);
+            const int total = K * swt;
+            const int nchunks = (total + kChunk - 1) / kChunk;
+            const int rbd = fb * 16;
+            const int s0 = r0 * fb, b0 = r0 * bsz;
+            const int s0a = s0 & ~15, b0a = b0 & ~15;
+            const int lim_w = nr * rbd, lim_s = (s0 - s0a) + nr * fb;
+            const int lim_b = a.bias_dt >= 0 ? (b0 - b0a) + nr * bsz : 0;
+            const uint32_t rel_w = (uint32_t)(a.sec.dn_blocks + (int64_t)r0 * rbd);
+            const uint32_t rel_s = (uint32_t)(a.sec.dn_scales + s0a) - (uint32_t)sww;
+            const uint32_t rel_b = (uint32_t)(a.sec.dn_bias + b0a) - (uint32_t)(sww + sws);
+            const float inv_swt = 1.0f / (float)swt;
+            uint32_t eo_c[NDMA];
+#pragma unroll
+            for (int c = 0; c < NDMA; ++c) {
+                const int pos = (wave + kDmaWaves * c) * kChunk + lane * 16;
+                int k, o;
+                divmod_small(pos, swt, inv_swt, k, o);
+                eo_c[c] = (uint32_t)eid[min(k, K - 1)] * (uint32_t)a.stride;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int c = 0; c < NDMA; ++c) {
+                const int chunk = wave + kDmaWaves * c;
+                const int pos = chunk * kChunk + lane * 16;
+                int k, o;
+                divmod_small(pos, swt, inv_swt, k, o);
+                const bool is_w = o < sww, is_s = !is_w && o < sww + sws;
+                const int lim = is_w ? lim_w : is_s ? lim_s + sww : lim_b + sww + sws;
+                const uint32_t rel = is_w ? rel_w : is_s ? rel_s : rel_b;
+                const bool ok = pos < total && o < lim;
+                const uint32_t voff = ok ? eo_c[c] + rel + (uint32_t)o : kOutOfRange;
+                uint8_t *dst = lds8 + L.dma + (chunk < nchunks ? chunk : nchunks) * kChunk;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (l_void *)dst, 16, voff, 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const int i = s * RGW + wave * SEGG + segg;
+        const bool valid = i < nrows;
+        float acc = 0.0f;
+#pragma unroll
+        for (int m = 0; m < MG; ++m) {
+            const int cb = tlg + m * TPG;
+            const bool use = valid && cb < hb;
+            WBlock<XK> wb;
+            widen_v(W[s][m], wb);
+            const float d = block_dot_r<XK>(wb, X[m]) * decode_scale(SC[s][m]);
+            acc += use ? d : 0.0f;
+        }
+        acc = seg_sum<TPG>(acc);
+        const float up = next_segment<TPG>(acc);
+        const float b_own = bias_of(BW[s], BSH[s], a.bias_dt);
+        const float b_next = next_segment<TPG>(b_own);
+        if (valid && (segg & 1) == 0 && tlg == 0) {
+            const float v = apply_activation(a.act_kind, acc + b_own, up + b_next, a.limit, a.alpha);
+            actl[i >> 1] = f32_to_f16_bits(v);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // A bare barrier: __syncthreads' fence would wait for the down stream too.
+    // Only this workgroup's LDS writes (the activations) must be visible.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+
+    // ---- 5. exchange ---------------------------------------------------------
+    // Workgroup b publishes its activations as kXWords 8-byte words, three
+    // fp16 values and the 16-bit launch tag each, with device-coherent stores;
+    // an aligned 8-byte store is seen whole or not at all, so the tag marks
+    // the word valid and no separate flag, wait or counter is needed.  Every
+    // workgroup then reads all words, keeping those carrying this launch's
+    // tag and polling the rest (a bounded spin), and places the activations
+    // in LDS.  Every workgroup completes every launch, so all agree on the tag.
+    const int G = gridDim.x;
+    const int npair = K * F;
+    const unsigned pq = (unsigned)npair / (unsigned)G, pr = (unsigned)npair - pq * (unsigned)G;
+    const uint64_t tag = (uint64_t)(epoch1 & 0xFFFFu);
+    uint64_t *xw = a.xchg;
+    if (wave == 0 && 3 * lane < p1 - p0) {
+        uint64_t v = tag << 48;
+#pragma unroll
+        for (int e = 0; e < 3; ++e) {
+            const int j = 3 * lane + e;
+            v |= (uint64_t)(j < p1 - p0 ? actl[j] : 0) << (16 * e);
+        }
+        __hip_atomic_store(xw + b * kXWords + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);                // this wave's part of the down stream is in LDS
+    {
+        constexpr int WPT = 8;                    // words per thread (G * kXWords <= WPT * kDT)
+        const float inv_f = 1.0f / (float)F;
+        uint32_t pending = 0;
+#pragma unroll
+        for (int u = 0; u < WPT; ++u) {
+            const int idx = (int)threadIdx.x + u * kDT;
+            const int pb = idx / kXWords, j = idx % kXWords;
+            const int np = (int)pq + (pb < (int)pr ? 1 : 0);
+            if (pb < G && 3 * j < np) pending |= 1u << u;
+        }
+        unsigned spins = 0;
+        while (pending) {
+            uint64_t v[WPT];
+#pragma unroll
+            for (int u = 0; u < WPT; ++u)
+                v[u] = (pending >> u) & 1u
+                           ? __hip_atomic_load(xw + (int)threadIdx.x + u * kDT, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT)
+                           : 0ull;
+#pragma unroll
+            for (int u = 0; u < WPT; ++u) {
+                if (((pending >> u) & 1u) && (v[u] >> 48) == tag) {
+                    pending &= ~(1u << u);
+                    const int idx = (int)threadIdx.x + u * kDT;
+                    const int pb = idx / kXWords, j = idx % kXWords;
+                    const int np = (int)pq + (pb < (int)pr ? 1 : 0);
+                    const int pbase = pb * (int)pq + min(pb, (int)pr);
+#pragma unroll
+                    for (int e = 0; e < 3; ++e) {
+                        if (3 * j + e < np) {
+                            int k, f;
+                            divmod_small(pbase + 3 * j + e, F, inv_f, k, f);
+                            reinterpret_cast<uint16_t *>(as + k * fb * BDA + (f >> 5) * BDA)[f & 31] =
+                                (uint16_t)(v[u] >> (16 * e));
+                        }
+                    }
+                }
+            }
+            if (pending) {
+                if (++spins > kSpinLimit) {
+                    atomicOr(a.sync.err, 1u);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- 6. down from LDS -------------------------------------------------------
+    // Groups of RPW rows (one per TPD-lane segment of a wave) of one expert;
+    // each wave takes a contiguous run of groups, so the blocks of its
+    // expert's activations that its lanes need are read from LDS into
+    // registers once per expert, not once per block.
+    {
+        constexpr int RPW = SEGD;
+        const int segd = lane / TPD, tld = lane % TPD;
+        const int rbd = fb * 16;
+        const int shs = (r0 * fb) & 15, shb = (r0 * bsz) & 15;
+        const int gpk = (nr + RPW - 1) / RPW;            // groups per expert
+        const int ngroups = K * gpk;
+        const int gpw = (ngroups + kDW - 1) / kDW;       // groups per wave
+        const int g0 = wave * gpw, g1 = min(g0 + gpw, ngroups);
+        int kx = -1;
+        uint4 A[MD][4];
+        for (int g = g0; g < g1; ++g) {
+            const int k = g / gpk;
+            const int q = (g - k * gpk) * RPW + segd;
+            const bool valid = q < nr;
+            if (k != kx) {                                // wave-uniform
+                const uint32_t *xk = as + k * fb * BDA;
+#pragma unroll
+                for (int m = 0; m < MD; ++m) {
+                    const int cb = tld + m * TPD;
+                    const uint4 *xv = reinterpret_cast<const uint4 *>(xk + (cb < fb ? cb : 0) * BDA);
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) A[m][qq] = xv[qq];
+                }
+                kx = k;
+            }
+            const int qc = valid ? q : 0;
+            const uint8_t *wrow = lds8 + L.dma + k * swt + qc * rbd;
+            const uint8_t *srow = lds8 + L.dma + k * swt + sww + shs + qc * fb;
+            float acc = 0.0f;
+#pragma unroll
+            for (int m = 0; m < MD; ++m) {
+                const int cb = tld + m * TPD;
+                const bool use = valid && cb < fb;
+                const int cbc = use ? cb : 0;
+                const u32x4 wv = *reinterpret_cast<const u32x4 *>(wrow + cbc * 16);
+                WBlock<DT_F16> wb;
+                widen_v(wv, wb);
+                const float d = block_dot_r<DT_F16>(wb, A[m]) * decode_scale(srow[cbc]);
+                acc += use ? d : 0.0f;
+            }
+            acc = seg_sum<TPD>(acc);
+            if (valid && tld == 0) {
+                float bias = 0.0f;
+                if (a.bias_dt >= 0) {
+                    const uint8_t *bp = lds8 + L.dma + k * swt + sww + sws + shb + q * bsz;
+                    bias = a.bias_dt == DT_F32 ? *reinterpret_cast<const float *>(bp)
+                                               : load_as_f32(bp, a.bias_dt, 0);
+                }
+                vals[k * a.nrmax + q] = acc + bias;
+            }
+        }
+    }
+    __syncthreads();
+
+    // Combine in router order: dst += out_k * w_k, the product and the sum
+    // rounded separately (expert_accumulate).  accumulate: 0 overwrite; 1 add
+    // to out (applyAssignments); 2 out += the finished sum (the residual add
+    // after the block, TransformerLayer.swift:232-238).
+    for (int q = threadIdx.x; q < nr; q += kDT) {
+        const int64_t o = r0 + q;
+        float dst = a.accumulate == 1 ? a.out[o] : 0.0f;
+        for (int k = 0; k < K; ++k) dst = add_scaled_rn(dst, vals[k * a.nrmax + q], ew[k]);
+        if (a.accumulate == 2) dst = a.out[o] + dst;
+        a.out[o] = dst;
+        if (a.out_bf16) a.out_bf16[o] = f32_to_bf16_bits(dst);
+    }
+    if (threadIdx.x == 0) a.sync.epochs[b] = epoch1;
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// Instantiations: GPT-OSS (hidden = intermediate = 2880: 90-block rows, up to
+// top-4: 90 gate_up rows a workgroup on 256 CUs, three 32-row stages) and
+// Qwen3-30B-A3B (2048 / 768: 64- and 24-block rows, up to top-8).
+enum { kShapeGptOss = 0, kShapeQwen3 = 1 };
+constexpr int kNdma[2] = {10, 5};
+constexpr int kStagesG[2] = {3, 2};
+constexpr int kRowsPerStage[2] = {kDW * 64 / 16, kDW * 64 / 16};
+
+int shape_of(int hidden, int inter)
+{
+    const int hb = hidden / 32, fb = inter / 32;
+    if (hidden % 32 || inter % 32) return -1;
+    if (hb > 64 && hb <= 96 && fb > 64 && fb <= 96) return kShapeGptOss;
+    if (hb > 24 && hb <= 64 && fb > 8 && fb <= 24) return kShapeQwen3;
+    return -1;
+}
+
+// Calls f(kernel) with the instantiation for (shape, x dtype).
+template <class F> void with_kernel(int shape, int x_dt, F &&f)
+{
+    if (shape == kShapeGptOss) {
+        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 6>, 3, DShape<32, 3>, kNdma[kShapeGptOss]>);
+        else f(decode_layer_kernel<DT_F16, DShape<16, 6>, 3, DShape<32, 3>, kNdma[kShapeGptOss]>);
+    } else {
+        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 4>, 2, DShape<8, 3>, kNdma[kShapeQwen3]>);
+        else f(decode_layer_kernel<DT_F16, DShape<16, 4>, 2, DShape<8, 3>, kNdma[kShapeQwen3]>);
+    }
+}
+
+}  // namespace
+
+int decode_layer_plan(const Launch &L, int hidden, int inter, int x_dt, int top_k, int experts,
+                      int64_t stride, int bias_dt, DecodeArgs *args, size_t *lds_bytes)
+{
+    const int shape = shape_of(hidden, inter);
+    if (shape < 0 || (x_dt != DT_BF16 && x_dt != DT_F16)) return 0;
+    if (top_k < 1 || top_k > kMaxTopK || experts > 256 || experts < top_k) return 0;
+    if ((int64_t)experts * stride >= (int64_t)kOutOfRange) return 0;   // 32-bit buffer offsets
+    const int G = L.cus;
+    if (G <= 0 || G > kDecodeMaxGrid) return 0;
+    // Each workgroup publishes at most 3 * kXWords activations.
+    if (((int64_t)top_k * inter + G - 1) / G > 3 * kXWords) return 0;
+    // Every workgroup's gate_up share must fit the register stages.
+    const int rows_g = 2 * (int)(((int64_t)top_k * inter + G - 1) / G);
+    if (rows_g > kStagesG[shape] * kRowsPerStage[shape]) return 0;
+    const int nrmax = (hidden + G - 1) / G;
+    const int bsz = bias_dt == DT_F32 ? 4 : bias_dt >= 0 ? 2 : 0;
+    int sww, sws, swb;
+    decode_windows(hidden, inter, nrmax, bsz, sww, sws, swb);
+    const int swt = sww + sws + swb;
+    const int chunks = (top_k * swt + kChunk - 1) / kChunk;
+    if (chunks > kDmaWaves * kNdma[shape]) return 0;
+    const DecodeLds l = decode_lds(hidden, inter, top_k, nrmax, swt,
+                                   kStagesG[shape] * kRowsPerStage[shape]);
+    if (l.total > kDecodeLdsMax) return 0;
+    // The exchange needs the whole grid resident: one workgroup per CU.
+    const void *fn = nullptr;
+    with_kernel(shape, x_dt, [&](auto k) { fn = reinterpret_cast<const void *>(k); });
+    static const void *attr_done[4] = {};
+    int slot = -1;
+    for (int i = 0; i < 4; ++i)
+        if (attr_done[i] == fn || attr_done[i] == nullptr) { slot = i; break; }
+    if (slot < 0) return 0;
+    if (attr_done[slot] != fn) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kDecodeLdsMax) !=
+            hipSuccess)
+            return 0;
+        attr_done[slot] = fn;
+    }
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kDT, (size_t)l.total) != hipSuccess ||
+        occ < 1)
+        return 0;
+    if (args) {
+        args->nrmax = nrmax;
+        args->base_bytes = (uint32_t)((int64_t)experts * stride);
+    }
+    if (lds_bytes) *lds_bytes = (size_t)l.total;
+    return G;
+}
+
+hipError_t launch_decode_layer(const Launch &L, int grid, size_t lds, int x_dt, const DecodeArgs &a)
+{
+    const int shape = shape_of(a.hidden, a.inter);
+    if (shape < 0 || grid <= 0) return hipErrorInvalidValue;
+    with_kernel(shape, x_dt, [&](auto kernel) { GW_LAUNCH(kernel, dim3(grid), dim3(kDT), lds, L, a); });
+    return hipGetLastError();
+}
+
+}  // namespace gw

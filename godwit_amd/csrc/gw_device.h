@@ -279,4 +279,52 @@ __device__ __forceinline__ float apply_activation(int kind, float g, float u, fl
     return kind == 0 ? gptoss_glu(g, u, limit, alpha) : silu_glu(g, u);
 }
 
+// --- work split and row reductions (shared by the streaming kernels) ------
+
+// a = q*d + r for 0 <= a < 2^22, without a loop or an integer divide: the
+// float quotient is off by at most one and is corrected with selects (the
+// engine keeps control flow out of its load path).
+__device__ __forceinline__ void divmod_small(int a, int d, float inv_d, int &q, int &r)
+{
+    q = (int)((float)a * inv_d);
+    r = a - q * d;
+    q = r < 0 ? q - 1 : q;
+    r = r < 0 ? r + d : r;
+    q = r >= d ? q + 1 : q;
+    r = r >= d ? r - d : r;
+}
+
+// This workgroup's share [lo, hi) of `total` items in balanced contiguous
+// ranges (the first total % G workgroups take one more), with one 32-bit
+// division instead of 64-bit products and quotients.
+__device__ __forceinline__ void slice_of(int total, int &lo, int &hi)
+{
+    const unsigned G = gridDim.x, b = blockIdx.x;
+    const unsigned q = (unsigned)total / G, r = (unsigned)total - q * G;
+    lo = (int)(b * q + min(b, r));
+    hi = lo + (int)q + (b < r ? 1 : 0);
+}
+
+// Sum over the TPR lanes of a row segment with DPP butterflies inside a
+// 16-lane row (pair swap, quad swap, half mirror, mirror): every lane ends with
+// the same bits (each step adds two equal partial sums in either order).
+#define GW_DPPF(x, ctrl) __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), (ctrl), 0xF, 0xF, false))
+// 32-lane segments add the neighbouring 16-lane row last (permlane16 swap),
+// the same two partial sums in the same order in both rows.
+template <int TPR> __device__ __forceinline__ float seg_sum(float v)
+{
+    static_assert(TPR == 8 || TPR == 16 || TPR == 32, "row segments are 8, 16 or 32 lanes");
+    v += GW_DPPF(v, 0xB1);                      // quad_perm [1,0,3,2]
+    v += GW_DPPF(v, 0x4E);                      // quad_perm [2,3,0,1]
+    v += GW_DPPF(v, 0x141);                     // row_half_mirror
+    if constexpr (TPR >= 16) v += GW_DPPF(v, 0x140);   // row_mirror
+    if constexpr (TPR == 32) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                        false, false);
+        v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    return v;
+}
+#undef GW_DPPF
+
 }  // namespace gw

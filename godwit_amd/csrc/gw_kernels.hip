@@ -25,17 +25,6 @@
 
 namespace gw {
 
-// Launches on the Launch's stream; when the Launch carries a start/stop event
-// pair (profiling), they are attached to the kernel's own dispatch, so they
-// time the kernel alone, not the gaps around it.
-#define GW_LAUNCH(KERNEL, GRID, BLOCK, LDS, L, ...)                                          \
-    do {                                                                                      \
-        if ((L).ev_start)                                                                     \
-            hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, (L).stream, (L).ev_start,          \
-                                  (L).ev_stop, 0, __VA_ARGS__);                               \
-        else                                                                                  \
-            hipLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, (L).stream, __VA_ARGS__);            \
-    } while (0)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -139,45 +128,6 @@ __device__ __forceinline__ float decode_bias(uint32_t bw, int bshift, int bias_d
     const uint16_t b = (uint16_t)(bw >> bshift);
     return bias_dt == DT_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
 }
-
-// a = q*d + r for 0 <= a < 2^22, without a loop or an integer divide: the
-// float quotient is off by at most one and is corrected with selects (the
-// engine keeps control flow out of its load path).
-__device__ __forceinline__ void divmod_small(int a, int d, float inv_d, int &q, int &r)
-{
-    q = (int)((float)a * inv_d);
-    r = a - q * d;
-    q = r < 0 ? q - 1 : q;
-    r = r < 0 ? r + d : r;
-    q = r >= d ? q + 1 : q;
-    r = r >= d ? r - d : r;
-}
-
-// This workgroup's share [lo, hi) of `total` items in balanced contiguous
-// ranges (the first total % G workgroups take one more), with one 32-bit
-// division instead of 64-bit products and quotients.
-__device__ __forceinline__ void slice_of(int total, int &lo, int &hi)
-{
-    const unsigned G = gridDim.x, b = blockIdx.x;
-    const unsigned q = (unsigned)total / G, r = (unsigned)total - q * G;
-    lo = (int)(b * q + min(b, r));
-    hi = lo + (int)q + (b < r ? 1 : 0);
-}
-
-// Sum over the TPR lanes of a row segment with DPP butterflies inside a
-// 16-lane row (pair swap, quad swap, half mirror, mirror): every lane ends with
-// the same bits (each step adds two equal partial sums in either order).
-#define GW_DPPF(x, ctrl) __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), (ctrl), 0xF, 0xF, false))
-template <int TPR> __device__ __forceinline__ float seg_sum(float v)
-{
-    static_assert(TPR == 8 || TPR == 16, "row segments are 8 or 16 lanes");
-    v += GW_DPPF(v, 0xB1);                      // quad_perm [1,0,3,2]
-    v += GW_DPPF(v, 0x4E);                      // quad_perm [2,3,0,1]
-    v += GW_DPPF(v, 0x141);                     // row_half_mirror
-    if constexpr (TPR == 16) v += GW_DPPF(v, 0x140);   // row_mirror
-    return v;
-}
-#undef GW_DPPF
 
 // Issues the M block loads (and M scale loads) of one stage.  Every lane issues
 // all of them: a column past the end re-reads the row's last block, and a row
@@ -704,242 +654,6 @@ __global__ __launch_bounds__(256) void router_rows_kernel(const void *__restrict
     }
 }
 
-// ---------------------------------------------------------------------------
-// Fused decode layer (one token): route -> gate_up + activation -> down +
-// weighted combine in ONE kernel.  Every workgroup owns a slice of the gate_up
-// rows and a slice of the output rows.  It computes its gate_up rows and
-// writes their activations with coherent (sc1) stores, then signals one of 16
-// counters (spread over separate lines so arrivals do not serialise on one
-// address) and waits, with a bounded spin, until every workgroup has
-// signalled.  It then stages all activations (sc1 loads), runs its down rows
-// and combines them in router order.  The grid must be co-resident (the host
-// checks occupancy); a wait that gives up sets *sync.err instead of hanging.
-// ---------------------------------------------------------------------------
-
-constexpr int kSyncCounters = 16;
-constexpr int kSyncStride = 1088;          // uint32 apart: 4 KiB + 256 B, a separate page and line each
-constexpr unsigned kSpinLimit = 1u << 18;
-
-__device__ __forceinline__ void store_coherent_u16(uint16_t *p, uint16_t v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Buffer resource word 3 for raw (untyped) buffer access, and the cache-policy
-// bit that makes a load device-coherent (sc1): the same access a relaxed
-// agent-scope atomic load performs, but batchable.
-constexpr int kBufferRsrcWord3 = 0x00020000;
-constexpr int kCachePolicySc1 = 16;
-constexpr int kActBatch = 8;
-
-template <int XK, class SG, class SD>
-__global__ __launch_bounds__(kNT) void moe_layer_kernel(
-    RouteArgs route, const void *__restrict__ x, int hidden, int inter, Sections sec,
-    int bias_dt, uint16_t *__restrict__ act, int act_kind, float limit, float alpha,
-    float *__restrict__ out, uint16_t *__restrict__ out_bf16, SyncArgs sync, int chunks_g,
-    int chunks_d, int nmax)
-{
-    extern __shared__ __align__(16) uint32_t lds[];
-    constexpr int BDX = XL<XK>::kBlockDw;
-    constexpr int BDA = XL<DT_F16>::kBlockDw;
-    constexpr int TPRG = SG::TPR, TPRD = SD::TPR;
-    Plan *plan = reinterpret_cast<Plan *>(lds);
-    const int bpr_g = hidden >> 5, bpr_d = inter >> 5;
-    const int xstride = bpr_g * BDX, astride = bpr_d * BDA;
-    const int K = route.top_k;
-    // Launches this workgroup has completed (uniform; written back at the end).
-    // Kept in a register: a static __shared__ variable here would shift the
-    // dynamic LDS off its 16-byte alignment and split every ds_read_b128.
-    const unsigned epoch1 = sync.epochs[blockIdx.x] + 1;
-    uint32_t *xs = lds + sizeof(Plan) / 4;                     // [xstride]
-    uint32_t *as = xs + xstride;                                // [K][astride]
-    float *vals = reinterpret_cast<float *>(as + K * astride);  // [K][nmax]
-    // This workgroup's fp16 activations until they are stored; the area is
-    // free until the exchange (it later holds all experts' activations).
-    uint16_t *act_loc = reinterpret_cast<uint16_t *>(as);
-
-    if (threadIdx.x < 64) {
-        route_one<kFusedRouteR>(route.logits, route.experts, K, route.experts_base,
-                                route.stride, plan, blockIdx.x == 0 ? route.ids_out : nullptr,
-                                blockIdx.x == 0 ? route.w_out : nullptr);
-    } else {
-        stage_vector<XK>(xs, x, hidden, threadIdx.x - 64, kNT - 64);
-    }
-    __syncthreads();
-
-    const int G = gridDim.x;
-    const int64_t row_bytes_g = (int64_t)bpr_g * 16, row_bytes_d = (int64_t)bpr_d * 16;
-    const int bsz = bias_dt == DT_F32 ? 4 : 2;
-
-    // gate_up slice: (expert, pair) range [p0, p1)
-    int p0, p1;
-    slice_of(K * inter, p0, p1);
-    const int ng_items = 2 * (p1 - p0);
-    const float inv_inter = 1.0f / (float)inter;
-    int g_start, i_start;
-    divmod_small(p0, inter, inv_inter, g_start, i_start);
-    auto locate = [&](int item, int &g, int &i) {
-        int q, r;
-        divmod_small(i_start + (item >> 1), inter, inv_inter, q, r);
-        g = g_start + q;
-        i = r;
-    };
-    auto rowfn_g = [&](int item) {
-        RowRef<1> r;
-        int g, i;
-        locate(item, g, i);
-        const int row = 2 * i + (item & 1);
-        const uint8_t *base = plan->group_base[g];
-        r.packed = base + sec.gu_blocks + row * row_bytes_g;
-        r.scales = base + sec.gu_scales + row * bpr_g;
-        r.bias = bias_dt >= 0 ? base + sec.gu_bias + row * bsz : r.scales;
-        r.ntok = 1;
-        r.xoff[0] = 0;
-        return r;
-    };
-    auto epi_g = [&](int item, bool valid, int, float (&acc)[1], uint32_t bw, int bsh) {
-        const float up = __shfl_down(acc[0], TPRG);
-        const float b_own = decode_bias(bw, bsh, bias_dt);
-        const float b_next = __shfl_down(b_own, TPRG);
-        if (valid && (item & 1) == 0 && (threadIdx.x % TPRG) == 0) {
-            const float v = apply_activation(act_kind, acc[0] + b_own, up + b_next, limit, alpha);
-            act_loc[item >> 1] = f32_to_f16_bits(v);
-        }
-    };
-
-    // down slice: output rows [r0, r1) of every selected expert
-    int r0, r1;
-    slice_of(hidden, r0, r1);
-    const int n = r1 - r0;
-    const int nd_items = K * n;
-    const float inv_n = 1.0f / (float)n;
-    auto rowfn_d = [&](int item) {
-        RowRef<1> r;
-        int gl, q;
-        divmod_small(item, n, inv_n, gl, q);
-        const uint8_t *base = plan->group_base[gl];
-        const int64_t row = r0 + q;
-        r.packed = base + sec.dn_blocks + row * row_bytes_d;
-        r.scales = base + sec.dn_scales + row * bpr_d;
-        r.bias = bias_dt >= 0 ? base + sec.dn_bias + row * bsz : r.scales;
-        r.ntok = 1;
-        r.xoff[0] = plan->group_slot0[gl] * astride;
-        return r;
-    };
-    auto epi_d = [&](int item, bool valid, int, float (&acc)[1], uint32_t bw, int bsh) {
-        if (valid && (threadIdx.x % TPRD) == 0) {
-            int gl, q;
-            divmod_small(item, n, inv_n, gl, q);
-            vals[plan->group_slot0[gl] * nmax + q] = acc[0] + decode_bias(bw, bsh, bias_dt);
-        }
-    };
-
-    EngineRing<kGateUpDepth, 1, SG> gu;
-    engine_prime<kGateUpDepth, 1, SG>(gu, ng_items, chunks_g, bpr_g, rowfn_g);
-    engine_run<kGateUpDepth, XK, 1, SG, true>(gu, ng_items, chunks_g, bpr_g, xs, rowfn_g, epi_g);
-    __syncthreads();
-
-    // The workgroup's activations leave in one batch of coherent (sc1) stores
-    // (a store per gate_up stage would make every later stage's loads wait for
-    // its write-through), then each wave waits for its own stores and one
-    // relaxed add on this workgroup's counter signals them.
-    for (int t = threadIdx.x; t < (p1 - p0); t += kNT) {
-        int g, i;
-        divmod_small(p0 + t, inter, inv_inter, g, i);
-        store_coherent_u16(act + (int64_t)plan->group_slot0[g] * inter + i, act_loc[t]);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(sync.counters + (blockIdx.x % kSyncCounters) * kSyncStride, 1u,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
-    // Lanes 0..15 of wave 0 each watch one counter; counter c receives one add
-    // per launch from every workgroup b with b % 16 == c.  Comparisons are
-    // wrap-safe: the counters only ever grow by whole launches.
-    const int c = threadIdx.x;
-    const unsigned target =
-        c < kSyncCounters ? epoch1 * (unsigned)((G - c + kSyncCounters - 1) / kSyncCounters) : 0u;
-    auto all_arrived = [&]() {
-        bool ok = true;
-        if (c < kSyncCounters)
-            ok = (int)(__hip_atomic_load(sync.counters + c * kSyncStride, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT) - target) >= 0;
-        return __all(ok);
-    };
-    // One probe first.  A workgroup that still has to wait loads its first two
-    // down stages meanwhile (they do not depend on the exchange; issued before
-    // the probe they would delay it, as wave 0's loads complete in order).
-    if (threadIdx.x < 64) {
-        const bool done = all_arrived();
-        if (threadIdx.x == 0) plan->pad0 = done ? 1 : 0;
-    }
-    __syncthreads();
-    const bool waiting = plan->pad0 == 0;
-    EngineRing<kDownDepth, 1, SD> down;
-    if (waiting) {
-        engine_prime<kDownDepth, 1, SD>(down, nd_items, chunks_d, bpr_d, rowfn_d);
-        if (threadIdx.x < 64) {
-            unsigned spins = 0;
-            while (!all_arrived()) {
-                __builtin_amdgcn_s_sleep(1);
-                if (++spins > kSpinLimit) {
-                    if (threadIdx.x == 0) atomicOr(sync.err, 1u);
-                    break;
-                }
-            }
-        }
-        __syncthreads();
-    }
-
-    // Every activation is now visible: stage them with coherent (sc1) buffer
-    // loads, issued as one batch per thread.  A buffer load past the buffer's
-    // end returns zero instead of faulting; such lanes write nothing.
-    {
-        const int q4 = inter >> 3;                 // 16-byte groups per slot
-        const int total = K * q4;
-        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-            act, 0, total * 16, kBufferRsrcWord3);
-        const float inv_q4 = 1.0f / (float)q4;
-        for (int base = 0; base < total; base += kActBatch * kNT) {
-            u32x4 v[kActBatch];
-#pragma unroll
-            for (int u = 0; u < kActBatch; ++u)
-                v[u] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rsrc, (base + u * kNT + (int)threadIdx.x) * 16, 0, kCachePolicySc1);
-#pragma unroll
-            for (int u = 0; u < kActBatch; ++u) {
-                const int i = base + u * kNT + (int)threadIdx.x;
-                if (i < total) {
-                    int sidx, j4;
-                    divmod_small(i, q4, inv_q4, sidx, j4);
-                    const int j = j4 * 4;
-                    *reinterpret_cast<u32x4 *>(as + sidx * astride + (j >> 4) * BDA + (j & 15)) =
-                        v[u];
-                }
-            }
-        }
-    }
-    __syncthreads();
-
-    if (!waiting) engine_prime<kDownDepth, 1, SD>(down, nd_items, chunks_d, bpr_d, rowfn_d);
-    engine_run<kDownDepth, DT_F16, 1, SD, false>(down, nd_items, chunks_d, bpr_d, as, rowfn_d,
-                                                 epi_d);
-    __syncthreads();
-
-    // Combine in router order: dst = 0; dst += out_e * w_e (expert_accumulate).
-    for (int q = threadIdx.x; q < n; q += kNT) {
-        float dst = 0.0f;
-        for (int k = 0; k < plan->tok_nslots[0]; ++k) {
-            const int sl = plan->tok_slots[0][k];
-            dst = add_scaled_rn(dst, vals[sl * nmax + q], plan->slot_weight[sl]);
-        }
-        out[r0 + q] = dst;
-        if (out_bf16) out_bf16[r0 + q] = f32_to_bf16_bits(dst);
-    }
-    if (threadIdx.x == 0) sync.epochs[blockIdx.x] = epoch1;
-}
-
 // Standalone routing (more than 256 experts, or a host that wants the plan
 // only): one wave builds the plan in LDS and copies it out.
 __global__ __launch_bounds__(64) void route_kernel(RouteArgs route, Plan *__restrict__ gplan)
@@ -1181,98 +895,6 @@ static void down_dispatch(const Launch &L, const RowShape &s, int grid, size_t l
                            act, hidden, inter, sec, bias_dt, out, out_bf16, accumulate, smax,
                            nmax, s.chunks);
     });
-}
-
-int fused_layer_lds_bytes(int hidden, int inter, int x_dt, int top_k, int grid)
-{
-    const int nmax = (hidden + grid - 1) / grid;
-    return (int)sizeof(Plan) + (hidden / 32) * x_block_dw(x_dt) * 4 +
-           top_k * (inter / 32) * 20 * 4 + top_k * nmax * 4;
-}
-
-// Which (gate_up, down) shape classes the fused kernel is built for.
-static int fused_shape_pair(int hidden, int inter)
-{
-    const RowShape g = row_shape(hidden / 32), d = row_shape(inter / 32);
-    if (g.tpr == 16 && g.m == 6 && d.tpr == 16 && d.m == 6) return 0;   // GPT-OSS 2880/2880
-    if (g.tpr == 16 && g.m == 4 && d.tpr == 8 && d.m == 3) return 1;    // Qwen3 2048/768
-    return -1;
-}
-
-template <int XK, class SG, class SD>
-static const void *fused_fn()
-{
-    return reinterpret_cast<const void *>(&moe_layer_kernel<XK, SG, SD>);
-}
-
-static const void *fused_kernel_ptr(int x_dt, int pair)
-{
-    if (pair == 0) {
-        if (x_dt == DT_F32) return fused_fn<DT_F32, S3, S3>();
-        if (x_dt == DT_F16) return fused_fn<DT_F16, S3, S3>();
-        return fused_fn<DT_BF16, S3, S3>();
-    }
-    if (x_dt == DT_F32) return fused_fn<DT_F32, S2, S1>();
-    if (x_dt == DT_F16) return fused_fn<DT_F16, S2, S1>();
-    return fused_fn<DT_BF16, S2, S1>();
-}
-
-int fused_layer_grid(const Launch &L, int hidden, int inter, int x_dt, int top_k, int experts)
-{
-    const int pair = fused_shape_pair(hidden, inter);
-    if (pair < 0 || experts > 64 * kFusedRouteR || top_k > kMaxTopK) return 0;
-    const int grid = 2 * L.cus;
-    if ((int64_t)top_k * inter < grid || hidden < grid) return 0;
-    const int lds = fused_layer_lds_bytes(hidden, inter, x_dt, top_k, grid);
-    if (lds > kLdsBudget) return 0;
-    // Resident workgroups per CU, cached per (shape pair, x dtype, LDS bytes).
-    static int cache_key[2][3] = {{-1, -1, -1}, {-1, -1, -1}};
-    static int cache_occ[2][3];
-    const int xi = x_dt == DT_F32 ? 0 : x_dt == DT_F16 ? 1 : 2;
-    int occ = 0;
-    if (cache_key[pair][xi] == lds) {
-        occ = cache_occ[pair][xi];
-    } else {
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fused_kernel_ptr(x_dt, pair), kNT,
-                                                         (size_t)lds) != hipSuccess)
-            return 0;
-        cache_occ[pair][xi] = occ;
-        cache_key[pair][xi] = lds;
-    }
-    return occ * L.cus >= grid ? grid : 0;   // the exchange needs the whole grid resident
-}
-
-hipError_t launch_fused_layer(const Launch &L, int grid, const RouteArgs &route, const void *x,
-                              int x_dt, int hidden, int inter, const Sections &sec, int bias_dt,
-                              uint16_t *act, int act_kind, float limit, float alpha, float *out,
-                              uint16_t *out_bf16, const SyncArgs &sync)
-{
-    const int pair = fused_shape_pair(hidden, inter);
-    if (pair < 0 || route.tokens != 1 || grid <= 0) return hipErrorInvalidValue;
-    const RowShape g = row_shape(hidden / 32), d = row_shape(inter / 32);
-    const int nmax = (hidden + grid - 1) / grid;
-    const size_t lds = (size_t)fused_layer_lds_bytes(hidden, inter, x_dt, route.top_k, grid);
-    auto go = [&](auto xk, auto sg, auto sd) {
-        constexpr int XK = decltype(xk)::value;
-        using SG = decltype(sg);
-        using SD = decltype(sd);
-        GW_LAUNCH((moe_layer_kernel<XK, SG, SD>), dim3(grid), dim3(kNT), lds, L,
-                           route, x, hidden, inter, sec, bias_dt, act, act_kind, limit, alpha,
-                           out, out_bf16, sync, g.chunks, d.chunks, nmax);
-    };
-    using F32c = std::integral_constant<int, DT_F32>;
-    using F16c = std::integral_constant<int, DT_F16>;
-    using B16c = std::integral_constant<int, DT_BF16>;
-    if (pair == 0) {
-        if (x_dt == DT_F32) go(F32c{}, S3{}, S3{});
-        else if (x_dt == DT_F16) go(F16c{}, S3{}, S3{});
-        else go(B16c{}, S3{}, S3{});
-    } else {
-        if (x_dt == DT_F32) go(F32c{}, S2{}, S1{});
-        else if (x_dt == DT_F16) go(F16c{}, S2{}, S1{});
-        else go(B16c{}, S2{}, S1{});
-    }
-    return hipGetLastError();
 }
 
 hipError_t launch_down(const Launch &L, const Plan *plan, int max_tokens, int max_slots,

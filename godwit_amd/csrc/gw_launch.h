@@ -1,12 +1,25 @@
 // gw_launch.h — host-side launchers of the gfx950 kernels (gw_kernels.hip).
 // Internal to libgodwit_hip.so; the public surface is include/godwit_hip.h.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "gw_plan.h"
 
 namespace gw {
+
+// Launches on the Launch's stream; when the Launch carries a start/stop event
+// pair (profiling), they are attached to the kernel's own dispatch, so they
+// time the kernel alone, not the gaps around it.
+#define GW_LAUNCH(KERNEL, GRID, BLOCK, LDS, L, ...)                                          \
+    do {                                                                                      \
+        if ((L).ev_start)                                                                     \
+            hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, (L).stream, (L).ev_start,          \
+                                  (L).ev_stop, 0, __VA_ARGS__);                               \
+        else                                                                                  \
+            hipLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, (L).stream, __VA_ARGS__);            \
+    } while (0)
 
 struct Launch {
     hipStream_t stream;
@@ -64,13 +77,43 @@ constexpr int kFusedRouteExperts = 256;
 hipError_t launch_down(const Launch &L, const Plan *plan, int max_tokens, int max_slots,
                        const uint16_t *act, int hidden, int inter, const Sections &sec,
                        int bias_dt, float *out, uint16_t *out_bf16, int accumulate);
-// Grid of the fused one-token layer kernel for this shape (0 = not available:
-// shape not built, too few rows per workgroup, or the grid cannot be resident).
-int fused_layer_grid(const Launch &L, int hidden, int inter, int x_dt, int top_k, int experts);
-hipError_t launch_fused_layer(const Launch &L, int grid, const RouteArgs &route, const void *x,
-                              int x_dt, int hidden, int inter, const Sections &sec, int bias_dt,
-                              uint16_t *act, int act_kind, float limit, float alpha, float *out,
-                              uint16_t *out_bf16, const SyncArgs &sync);
+// ---- one-token layer in one kernel (gw_decode.hip)
+
+constexpr int kSyncEpochCapacity = 8192;      // per-workgroup epochs a runner keeps
+constexpr int kDecodeLdsMax = 160 * 1024;     // LDS of one gfx950 compute unit
+constexpr int kDecodeMaxGrid = 256;           // workgroups of the one-kernel layer at most
+constexpr int kDecodeXWords = 16;             // 8-byte exchange words per workgroup
+
+struct DecodeArgs {
+    const float *logits;          // [experts] router logits of the token
+    int experts, top_k;
+    const uint8_t *base;          // expert e at base + e * stride
+    int64_t stride;
+    uint32_t base_bytes;          // experts * stride (< 2^31: 32-bit buffer offsets)
+    int32_t *ids_out;             // optional [top_k]
+    float *w_out;                 // optional [top_k]
+    const void *x;                // [hidden] bf16 or fp16
+    int hidden, inter;
+    Sections sec;
+    int bias_dt;                  // -1: none
+    uint64_t *xchg;               // [kDecodeMaxGrid, kDecodeXWords] tagged activations, zeroed
+    int act_kind;
+    float limit, alpha;
+    float *out;                   // [hidden]
+    uint16_t *out_bf16;           // optional bf16 copy of out
+    int accumulate;               // 0 overwrite, 1 add to out, 2 residual: out += sum
+    SyncArgs sync;
+    int nrmax;                    // most down rows a workgroup owns (ceil(hidden / grid))
+};
+struct DecodeLds { int route, xs, actl, dma, as, vals, total; };
+
+// Grid (one workgroup per CU) of the one-kernel layer for this shape, or 0
+// when it is not available (shape, dtype or top-k not built, LDS, or the grid
+// cannot be resident).  Fills args->nrmax / base_bytes and the LDS size.
+int decode_layer_plan(const Launch &L, int hidden, int inter, int x_dt, int top_k, int experts,
+                      int64_t stride, int bias_dt, DecodeArgs *args, size_t *lds_bytes);
+hipError_t launch_decode_layer(const Launch &L, int grid, size_t lds, int x_dt,
+                               const DecodeArgs &a);
 // ---- prefill (batched tokens) on the matrix cores
 
 // One grouped GEMM launch (gate_up or down) over the work items of a grouping.

@@ -30,14 +30,6 @@
 
 namespace gw {
 
-#define GW_LAUNCH(KERNEL, GRID, BLOCK, LDS, L, ...)                                          \
-    do {                                                                                      \
-        if ((L).ev_start)                                                                     \
-            hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, (L).stream, (L).ev_start,          \
-                                  (L).ev_stop, 0, __VA_ARGS__);                               \
-        else                                                                                  \
-            hipLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, (L).stream, __VA_ARGS__);            \
-    } while (0)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));

@@ -359,15 +359,17 @@ typedef struct gw_moe_block_args {
 
 int gw_moe_block_forward(gw_expert_runner *runner, const gw_moe_block_args *args);
 
-/* For one token (the decode step of a single sequence) the layer above can
- * run as ONE kernel whose workgroups exchange the activations through device
- * memory (enabled by GODWIT_FUSED_LAYER=1 in the environment when the runner
- * is created; the default is the two-kernel form, which measures faster on
- * MI355X today).  Its waits are bounded, and a wait that gives up is counted
- * here instead of hanging the device.  No counterpart in the reference (there
- * the command buffer's encoder boundaries order the stages).  Blocks until the
- * runner's stream is idle; *count is the number of failed exchanges since the
- * runner was created (0 when every result is valid). */
+/* For one token (the decode step of a single sequence) with 16-bit x the
+ * layer above runs as ONE kernel, one workgroup per compute unit, whose
+ * workgroups exchange the activations through device memory (shapes with
+ * 65..96- or 25..64-block rows, top-k <= 8, up to 256 experts; other cases,
+ * and GODWIT_DECODE_LAYER=0 in the environment when the runner is created,
+ * use a gate_up and a down kernel).  The exchange's waits are bounded, and a
+ * wait that gives up is counted here instead of hanging the device.  No
+ * counterpart in the reference (there the command buffer's encoder
+ * boundaries order the stages).  Blocks until the runner's stream is idle;
+ * *count is the number of failed exchanges since the runner was created (0
+ * when every result is valid). */
 int gw_expert_runner_sync_errors(gw_expert_runner *runner, uint32_t *count);
 
 /* ---- graphs (replace per-call command buffers with one replayable graph) */

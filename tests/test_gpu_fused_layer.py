@@ -1,11 +1,17 @@
-"""The one-token layer kernel (route -> gate_up -> in-kernel activation exchange ->
-down + combine, one launch) against the two-kernel form of the same layer and
-against the CPU oracle.
+"""The one-token layer kernel (route -> gate_up + down stream into LDS ->
+in-kernel activation exchange -> down + combine, one launch) against the
+two-kernel form of the same layer (GODWIT_DECODE_LAYER=0) and against the CPU
+oracle.
 
-Both forms use the same row shapes and the same summation and combine order, so
-their outputs are required to be bit-identical; the oracle check uses the
+Both forms compute the gate_up rows with the same lane mapping and order, so
+their activations are the same bytes.  The one-kernel form splits a GPT-OSS
+down row over 32 lanes (3 blocks each) where the two-kernel form uses 16 (6
+each), so the fp32 row sums may round differently: the forms are required to
+agree to 1e-5 of the output's peak there, and bit for bit for Qwen3 (same down
+lane mapping in both).  Routing is exact in both.  The oracle check uses the
 reference's expert metric, max|d|/mean|ref| < 1e-3 (GodwitCLI/main.swift:518-532).
-Every test also requires the kernel's bounded waits to have all succeeded.
+Every test also requires the kernel's bounded waits to have all succeeded.  The
+one-kernel form takes 16-bit x; fp32 x stays on the two kernels.
 """
 import numpy as np
 import pytest
@@ -57,9 +63,9 @@ def _kernel_counts(ctx, fn):
 def test_fused_layer_equals_two_kernel_form(ctx, monkeypatch, shape, n_experts, top_k, x_dtype):
     H, F = shape["hidden"], shape["inter"]
     layout, experts, buf = _make_layer(ctx, shape, n_experts, 1200 + n_experts)
-    monkeypatch.setenv("GODWIT_FUSED_LAYER", "1")
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "1")
     fused = gw.ExpertRunner(ctx, H, F, shape["act"])
-    monkeypatch.setenv("GODWIT_FUSED_LAYER", "0")
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "0")
     split = gw.ExpertRunner(ctx, H, F, shape["act"])
     r = rng(1300 + x_dtype)
     xb, xw = _inputs(ctx, r, H, x_dtype)
@@ -71,10 +77,18 @@ def test_fused_layer_equals_two_kernel_form(ctx, monkeypatch, shape, n_experts, 
     for name, runner in (("fused", fused), ("split", split)):
         counts[name] = _kernel_counts(ctx, lambda: got.__setitem__(
             name, _forward(ctx, runner, layout, buf, n_experts, top_k, xb, x_dtype, lb, H)))
-    assert counts["fused"] == {"moe_layer": 1, "gate_up": 0, "down": 0}, counts
-    assert counts["split"] == {"moe_layer": 0, "gate_up": 1, "down": 1}, counts
-    for a, b in zip(got["fused"], got["split"]):
-        assert np.array_equal(a, b)
+    one = {"moe_layer": 1, "gate_up": 0, "down": 0}
+    two = {"moe_layer": 0, "gate_up": 1, "down": 1}
+    assert counts["fused"] == (two if x_dtype == gw.F32 else one), counts
+    assert counts["split"] == two, counts
+    f_out, f16, f_ids, f_w = got["fused"]
+    s_out, s16, s_ids, s_w = got["split"]
+    assert np.array_equal(f_ids, s_ids) and np.array_equal(f_w, s_w)
+    if shape is QWEN3 or x_dtype == gw.F32:
+        assert np.array_equal(f_out, s_out) and np.array_equal(f16, s16)
+    else:
+        assert np.max(np.abs(f_out - s_out)) <= 1e-5 * np.max(np.abs(s_out))
+    assert np.array_equal(f16, oracle.f32_to_bf16_bits(f_out))
     assert fused.sync_errors() == 0
 
     rid, rw = oracle.router_select(logits, top_k)
@@ -98,7 +112,7 @@ def test_fused_layer_graph_chain_replays(ctx, monkeypatch):
     shape = GPTOSS
     H, F, n_experts, layers = shape["hidden"], shape["inter"], 16, 12
     layout, experts, buf = _make_layer(ctx, shape, n_experts, 1400)
-    monkeypatch.setenv("GODWIT_FUSED_LAYER", "1")
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "1")
     runner = gw.ExpertRunner(ctx, H, F, shape["act"])
     r = rng(1401)
     xbits, xw = normal_bf16(r, H)
