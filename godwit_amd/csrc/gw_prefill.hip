@@ -12,13 +12,22 @@
 //      (expert_accumulate, expert.metal:107-116).
 //
 // GEMM numerics.  Weights are widened by v_cvt_scalef32_pk_bf16_fp4 with the
-// block's e8m0 scale folded in: every e2m1 value times a power of two is
-// exact in bf16 (two significant bits; the whole e8m0 range, subnormal
-// scales included, checked exhaustively on gfx950).  Activations enter the
-// bf16 matrix cores as exact sums of bf16 planes: bf16 x is one plane, fp16
-// two (hi = bf16(v), lo = v - hi) and fp32 three.  Every product is then
-// exact in fp32 and v_mfma_f32_32x32x16_bf16 accumulates in fp32, so the
-// results differ from the reference's scalar loop only in summation order.
+// block's e8m0 scale folded in: e2m1 * 2^(b-127) is exact in bf16 (two
+// significant bits) for every byte up to 252, subnormal 2^-127 included, and
+// byte 255 widens to NaN.  The reference multiplies each finite block partial
+// by the scale (referenceMXFP4, DequantGEMVBenchmark.swift:106-116), whereas a
+// folded 2^126 or 2^127 (bytes 253, 254) would overflow bf16 for |code| >= 4
+// and >= 2.  So a row that holds a 253 or 254 byte folds 2^(b-129) into every
+// block and its fp32 accumulator is multiplied by 4 after the K loop (a
+// prologue pass finds such rows and lowers their staged bytes by 2).  The
+// conversion reads a subnormal scale as 2^-127, so in such a row bytes 0 and
+// 1 widen 4x and 2x too large: their products are 2^-250 of a 253/254 block's for activations
+// of like size, and differ from the reference only where every 253/254 block
+// of the row sums to exactly zero.  Activations enter the bf16 matrix cores as
+// exact sums of bf16 planes: bf16 x is one plane, fp16 two (hi = bf16(v), lo =
+// v - hi) and fp32 three.  Every product in the fp32 normal range is then
+// exact and v_mfma_f32_32x32x16_bf16 accumulates in fp32, so the results
+// differ from the reference's scalar loop only in summation order.
 #include <hip/hip_runtime.h>
 #include <hip/hip_ext.h>
 
@@ -282,6 +291,11 @@ __device__ __forceinline__ uint32_t lds_read4(uint32_t addr)
     uint32_t v;
     asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
     return v;
+}
+
+__device__ __forceinline__ void lds_write1(uint32_t addr, uint32_t v)
+{
+    asm volatile("ds_write_b8 %0, %1" : : "v"(addr), "v"(v) : "memory");
 }
 
 __device__ __forceinline__ bf16x8 lds_read16(uint32_t addr)
@@ -658,6 +672,53 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
     wait_vmcnt<kYounger>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
+    // The scales have landed.  A row that holds a 253 or 254 byte (e2m1 *
+    // 2^126 or 2^127 would overflow bf16) has its staged bytes lowered by 2
+    // (255 kept, 0 and 1 to 0) and its accumulator multiplied by 4 after the
+    // K loop.  Lane half h takes the dwords j = h, h + 2, .. of row c's nb
+    // bytes; bit r of rows_lowered is row r of the wave's 32.  Each wave
+    // rewrites only its own rows (unclamped), before its own first read.
+    uint32_t rows_lowered;
+    {
+        const int lo = sshift + (wave * 32 + c) * nb;
+        const int a0 = lo & ~3;
+        const int ndw = (lo + nb - a0 + 3) >> 2;
+        uint32_t big = 0;
+        for (int j = h; j < ndw; j += 8) {
+            uint32_t w4[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                w4[k] = lds_read4(sbase + (uint32_t)(a0 + 4 * min(j + 2 * k, ndw - 1)));
+            lds_wait<0>();
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int idx = a0 + 4 * (j + 2 * k) + i;
+                    const uint32_t b = (w4[k] >> (8 * i)) & 0xFFu;
+                    big |= (uint32_t)(idx >= lo && idx < lo + nb && b - 253u <= 1u);
+                }
+            }
+        }
+        const uint64_t m = __builtin_amdgcn_ballot_w64(big != 0u);
+        rows_lowered = (uint32_t)m | (uint32_t)(m >> 32);
+        if (rows_lowered != 0u) {                       // wave-uniform, and rare
+            if ((rows_lowered >> c) & 1u) {
+                for (int j = h; j < ndw; j += 2) {
+                    const uint32_t w = lds_read4(sbase + (uint32_t)(a0 + 4 * j));
+                    lds_wait<0>();
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int idx = a0 + 4 * j + i;
+                        const uint32_t b = (w >> (8 * i)) & 0xFFu;
+                        if (idx >= lo && idx < lo + nb && b != 255u)
+                            lds_write1(sbase + (uint32_t)idx, b >= 2u ? b - 2u : 0u);
+                    }
+                }
+            }
+            lds_wait<0>();
+        }
+    }
     for (int q = 0; q < nq_pad; q += D)
         Unroll<0, D>::run([&](auto s_const) { step(q + decltype(s_const)::value, s_const); });
     // Every DMA has landed (the padding chunks' too) and, after the barrier,
@@ -665,7 +726,10 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
     wait_vmcnt<0>();
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] += acc1[i];
+    for (int v = 0; v < 16; ++v) {
+        const int rl = 8 * (v >> 2) + 4 * h + (v & 3);
+        acc[v] = (acc[v] + acc1[v]) * ((rows_lowered >> rl) & 1u ? 4.0f : 1.0f);
+    }
 
     // Epilogue: lane holds entry column c, feature rows 8(v/4) + 4h + (v%4)
     // of the wave's 32; bias from the LDS tile.  The tile is written to LDS,

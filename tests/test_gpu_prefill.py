@@ -15,7 +15,7 @@ import pytest
 
 import godwit_amd as gw
 import oracle
-from helpers import expert_metric, layer_check, normal_bf16, rng
+from helpers import ExpertData, expert_metric, layer_check, normal_bf16, rng
 from test_gpu_expert import GPTOSS, QWEN3, SMALL, _make_layer
 
 pytestmark = pytest.mark.gpu
@@ -333,3 +333,86 @@ def test_fused_combine_equals_kernel(ctx, monkeypatch, shape, E, K, T, x_dtype, 
     assert ok, (rel_rms, worst, bound)
     for b in (xb, lb, buf):
         b.free()
+
+
+# Down-projection scale bytes by output row: rows 0..191 take EDGE[r % 6] in
+# every block (a 255 row holds one NaN block among 127s), rows 192.. mix the
+# six bytes at random.
+EDGE = (0, 1, 127, 253, 254, 255)
+
+
+def _edge_scale_layer(ctx, E, seed):
+    """A 256 x 128 GPT-OSS-activation layer without biases whose down scales are
+    the e8m0 edge bytes.  Gate_up scales 2^-14 .. 2^-12 keep the activations near
+    3e-3 (fp16 normal), so every down block partial stays below 0.2 and a row
+    of 253 / 254 blocks sums to under 2^128: finite in the oracle.  Rows with
+    codes 8 (-0) only in block 0 every seventh row."""
+    shape = dict(hidden=256, inter=128, act="gptOssClampedGLU", oact=oracle.ACT_GPTOSS,
+                 bias=False)
+    H, F = shape["hidden"], shape["inter"]
+    layout = gw.ExpertLayout(H, F, E)
+    r = rng(seed)
+    experts = []
+    nbr = F // 32
+    for _ in range(E):
+        e = ExpertData(r, H, F, layout.offsets, layout.stride, with_bias=False)
+        e.gu_scales[:] = r.integers(113, 116, size=e.gu_scales.size, dtype=np.uint8)
+        sc = e.dn_scales.reshape(H, nbr)
+        for row in range(H):
+            if row < 192:
+                b = EDGE[row % 6]
+                sc[row] = 127 if b == 255 else b
+                if b == 255:
+                    sc[row, (row // 6) % nbr] = 255
+            else:
+                sc[row] = r.choice(EDGE, size=nbr)
+        dn = e.dn_packed.reshape(H, F // 2)
+        dn[::7, :16] = 0x88
+        for name, arr in (("gate_up_scales", e.gu_scales), ("down_scales", e.dn_scales),
+                          ("down_blocks", e.dn_packed)):
+            off = layout.offsets[name]
+            e.blob[off:off + arr.nbytes] = arr.view(np.uint8)
+        experts.append(e)
+    buf = ctx.buffer(np.concatenate([e.blob for e in experts]))
+    return shape, layout, experts, buf
+
+
+@pytest.mark.parametrize("T", [8, 40], ids=["self-grouped-t8", "tile-list-t40"])
+def test_prefill_edge_scales(ctx, T):
+    """Every e8m0 edge byte through the grouped GEMMs against referenceMXFP4
+    (DequantGEMVBenchmark.swift:106-116), which multiplies each finite block
+    partial by its scale (MXFP4.decodeScale, MXFP4.swift:37-40): bytes 0 and 1
+    (subnormal scales), 127, 253 and 254 (e2m1 * 2^126 and 2^127 pass the bf16
+    maximum for |code| >= 4 and >= 2), 255 (NaN), and code 8 (-0).  NaN outputs
+    sit exactly where the oracle's are, no output is infinite, and every finite
+    output of feature row r is within 1e-3 of the mean |oracle| of that row
+    over the batch (rows span 2^-127 .. 2^127, so the bound is per row)."""
+    E, K = 4, 2
+    shape, layout, experts, buf = _edge_scale_layer(ctx, E, 3100 + T)
+    H, F = shape["hidden"], shape["inter"]
+    runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+    r = rng(3200 + T)
+    xb, xw = _x(ctx, r, T, H, gw.BF16)
+    logits = r.standard_normal((T, E)).astype(np.float32)
+    lb = ctx.buffer(logits)
+    got, got16, ids, _ = _run(ctx, runner, layout, buf, E, K, xb, gw.BF16, lb, T, H)
+    ref, rids, _ = oracle.moe_layer([e.oracle_expert() for e in experts], K, logits, xw, H, F,
+                                    shape["oact"])
+    assert np.array_equal(ids, rids)
+    nan_ref = np.isnan(ref)
+    assert nan_ref[:, 5:192:6].all() and not nan_ref[:, :192][:, np.arange(192) % 6 != 5].any()
+    assert np.array_equal(np.isnan(got), nan_ref)
+    assert not np.isinf(ref).any() and not np.isinf(got).any()
+    # Row classes reach the range ends: 2^127-scaled rows near 1e37, 2^-127 near 1e-39.
+    assert np.abs(ref[:, 4:192:6]).max() > 1e36 and 0 < np.abs(ref[:, 0:192:6]).max() < 1e-37
+    for row in range(H):
+        fin = ~nan_ref[:, row]      # a mixed row is NaN only for tokens of its NaN experts
+        if not fin.any():
+            continue
+        want = ref[fin, row].astype(np.float64)
+        d = np.abs(got[fin, row].astype(np.float64) - want)
+        assert d.max() <= 1e-3 * np.abs(want).mean(), (row, d.max(), np.abs(want).mean())
+    assert np.array_equal(got16, oracle.f32_to_bf16_bits(got.ravel()))
+    for b in (xb, lb, buf):
+        b.free()
+    runner.close()
