@@ -25,6 +25,7 @@ from typing import Dict, List, Optional, Sequence, Tuple, Union
 import numpy as np
 
 from ._lib import (ACT_GPTOSS_CLAMPED_GLU, ACT_SILU, BF16, F16, F32, SECTION_COUNT,
+                   STATIC_SCRATCH_BYTES,
                    AssignmentC, ExpertLayoutC, ExpertWeightsC, GodwitError, ModelInfoC, MoeBlockArgsC, MoeLayerArgsC,
                    check, lib)
 
@@ -32,7 +33,7 @@ __all__ = [
     "Context", "DeviceBuffer", "ExpertLayout", "ExpertRunner", "Weights", "Assignment",
     "Router", "Decision", "Graph", "GodwitError", "F32", "F16", "BF16", "SECTIONS",
     "mxfp4_dequant", "mxfp4_gemv", "mxfp4_gemv_bias", "expert_activation",
-    "expert_accumulate", "device_count",
+    "expert_accumulate", "device_count", "STATIC_SCRATCH_BYTES",
 ]
 
 SECTIONS = ["gate_up_blocks", "gate_up_scales", "down_blocks", "down_scales",
@@ -454,6 +455,21 @@ class ExpertRunner:
                              router_bias, router_bias_dtype, out_bf16, routing_ids,
                              routing_weights)
         check(lib.gw_moe_prefill_forward(self.handle, ctypes.byref(a)))
+
+    def prefill_forward_static(self, experts_base: int, expert_stride: int, expert_count: int,
+                               top_k: int, x: int, x_dtype: int, tokens: int, out: int,
+                               logits: int = 0, router_weight: int = 0,
+                               router_weight_dtype: int = BF16, router_bias: int = 0,
+                               router_bias_dtype: int = BF16, out_bf16: int = 0,
+                               routing_ids: int = 0, routing_weights: int = 0) -> None:
+        """prefill_forward with its scratch in the library's fixed per-device array
+        (STATIC_SCRATCH_BYTES) instead of the runner's buffer: allocates nothing.
+        Calls that overlap on one device race.  Enqueue only."""
+        a = self._layer_args(experts_base, expert_stride, expert_count, top_k, x, x_dtype,
+                             tokens, out, logits, router_weight, router_weight_dtype,
+                             router_bias, router_bias_dtype, out_bf16, routing_ids,
+                             routing_weights)
+        check(lib.gw_moe_prefill_forward_static(self.handle, ctypes.byref(a)))
 
     def block_forward(self, experts_base: int, expert_stride: int, expert_count: int,
                       top_k: int, tokens: int, stream: int, norm_weight: int,

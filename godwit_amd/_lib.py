@@ -16,6 +16,7 @@ STATUS_NAMES = {0: "GW_OK", 1: "GW_ERR_ARG", 2: "GW_ERR_SHAPE", 3: "GW_ERR_OOM",
 F32, F16, BF16 = 0, 1, 2
 ACT_GPTOSS_CLAMPED_GLU, ACT_SILU = 0, 1
 SECTION_COUNT = 6
+STATIC_SCRATCH_BYTES = 8 << 20   # GW_STATIC_SCRATCH_BYTES
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -106,6 +107,7 @@ SIGNATURES = {
     "gw_expert_apply_assignments_async": (_I, [_P, _P, _I, _P, _I32, _P]),
     "gw_moe_layer_forward": (_I, [_P, ctypes.POINTER(MoeLayerArgsC)]),
     "gw_moe_prefill_forward": (_I, [_P, ctypes.POINTER(MoeLayerArgsC)]),
+    "gw_moe_prefill_forward_static": (_I, [_P, ctypes.POINTER(MoeLayerArgsC)]),
     "gw_moe_block_forward": (_I, [_P, ctypes.POINTER(MoeBlockArgsC)]),
     "gw_model_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "gw_model_close": (_I, [_P]),

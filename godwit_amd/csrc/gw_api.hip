@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -149,6 +150,15 @@ extern "C" int gw_device_count(int *count)
     return GW_OK;
 }
 
+// The allocation-free prefill's scratch (gw_moe_prefill_forward_static): one
+// copy of this array per device.  Host code never uses its name as an
+// address: gw_context_create resolves each device's copy once, with that
+// device current, into g_scratch_ptr.
+static __device__ __align__(256) unsigned char scratch[GW_STATIC_SCRATCH_BYTES];
+static constexpr int kScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kScratchDevices] = {};
+
 extern "C" int gw_context_create(int device, gw_context **out)
 {
     GW_CHECK(out, GW_ERR_ARG, "out is null");
@@ -161,6 +171,14 @@ extern "C" int gw_context_create(int device, gw_context **out)
     GW_HIP(hipSetDevice(device));
     hipDeviceProp_t prop;
     GW_HIP(hipGetDeviceProperties(&prop, device));
+    if (device < kScratchDevices) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (!g_scratch_ptr[device]) {
+            void *p = nullptr;
+            GW_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+            g_scratch_ptr[device] = p;
+        }
+    }
     gw_context *ctx = new gw_context();
     ctx->device = device;
     ctx->cus = prop.multiProcessorCount;
@@ -962,7 +980,8 @@ extern "C" int gw_expert_apply_assignments(gw_expert_runner *r, const void *inpu
 // ---------------------------------------------------------------------------
 
 // out_mode 0: out = MoE output; 2: out += MoE output (the residual add).
-static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int out_mode);
+static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int out_mode,
+                            bool use_static = false);
 
 // A batch of up to kMaxTokens tokens runs either the streaming decode kernels,
 // which read each selected expert once per token group of a workgroup, or the
@@ -1170,7 +1189,10 @@ extern "C" int gw_expert_runner_reserve_prefill(gw_expert_runner *r, int32_t max
     return GW_OK;
 }
 
-static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int out_mode)
+// use_static: scratch carved from the device's static array (exactly T, K, E)
+// instead of the runner's reserved buffer, and no allocation.
+static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int out_mode,
+                            bool use_static)
 {
     GW_CHECK(r && a, GW_ERR_ARG, "null argument");
     GW_CHECK(a->tokens >= 1, GW_ERR_SHAPE, "tokens must be positive (got %d)", a->tokens);
@@ -1188,13 +1210,23 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
              GW_ERR_SHAPE, "prefill needs hidden and intermediate sizes that are multiples of 32 "
              "and at least 128 (got %lld, %lld)", (long long)r->hidden, (long long)r->inter);
     const int T = a->tokens, K = (int)a->top_k, E = (int)a->expert_count;
-    int rc = gw_expert_runner_reserve_prefill(r, T, K, E);
-    if (rc) return rc;
-    PrefillScratch ps;
-    prefill_layout(r, r->pf_tokens, r->pf_topk, r->pf_experts, static_cast<char *>(r->pf_buf),
-                   &ps);
     gw_context *ctx = r->ctx;
     const gw::Launch L = launch_of(ctx);
+    PrefillScratch ps;
+    if (use_static) {
+        void *base = ctx->device < kScratchDevices ? g_scratch_ptr[ctx->device] : nullptr;
+        GW_CHECK(base, GW_ERR_ARG, "no static scratch on device %d", ctx->device);
+        const size_t need = prefill_layout(r, T, K, E, nullptr, nullptr);
+        GW_CHECK(need <= GW_STATIC_SCRATCH_BYTES, GW_ERR_SHAPE,
+                 "%d tokens x top-%d over %d experts need %zu bytes of prefill scratch; the "
+                 "static array holds %zu", T, K, E, need, (size_t)GW_STATIC_SCRATCH_BYTES);
+        prefill_layout(r, T, K, E, static_cast<char *>(base), &ps);
+    } else {
+        int rc = gw_expert_runner_reserve_prefill(r, T, K, E);
+        if (rc) return rc;
+        prefill_layout(r, r->pf_tokens, r->pf_topk, r->pf_experts,
+                       static_cast<char *>(r->pf_buf), &ps);
+    }
     const float *logits = a->logits;
     if (!logits) {
         GW_CHECK(dtype_ok(a->router_weight_dtype), GW_ERR_ARG, "bad router dtype");
@@ -1287,6 +1319,16 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
         g.y_out = ps.y;
         g.y_bytes = (int64_t)sizeof(float) * T * K * r->hidden;
         if (fuse_combine) {
+            if (use_static) {
+                // The array holds the previous call's bytes: the counters
+                // start from zero by a fill kernel (no memset node in a
+                // captured graph).
+                ProfScope p(ctx, "prefill_clear");
+                GW_HIP(gw::launch_fill_u8(p.launch(L), ps.arrive,
+                                          sizeof(uint32_t) * (size_t)T *
+                                              (size_t)((r->hidden + 255) / 256),
+                                          0, 0, 0));
+            }
             g.arrive = ps.arrive;
             g.comb_w = ps.weights;
             g.comb_out = a->out;
@@ -1314,6 +1356,11 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
 extern "C" int gw_moe_prefill_forward(gw_expert_runner *r, const gw_moe_layer_args *a)
 {
     return moe_prefill_impl(r, a, 0);
+}
+
+extern "C" int gw_moe_prefill_forward_static(gw_expert_runner *r, const gw_moe_layer_args *a)
+{
+    return moe_prefill_impl(r, a, 0, true);
 }
 
 // ---------------------------------------------------------------------------

@@ -294,6 +294,22 @@ int gw_expert_runner_reserve_prefill(gw_expert_runner *runner, int32_t max_token
                                      int32_t expert_count);
 int gw_moe_prefill_forward(gw_expert_runner *runner, const gw_moe_layer_args *args);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): gw_moe_prefill_forward with its scratch (routing ids and
+ * weights, the tile list, the split x planes, the bf16 activation planes, the
+ * expert outputs, the combine counters) carved from a fixed per-device array
+ * of GW_STATIC_SCRATCH_BYTES instead of the runner's reserved buffer.  It
+ * calls no allocator (with profiling off).  A batch whose scratch exceeds the
+ * array returns GW_ERR_SHAPE: about 72 tokens of GPT-OSS-120B (2880 x 2880,
+ * top-4) or 78 of Qwen3-30B-A3B fit.  Same arguments and results, byte for
+ * byte, as gw_moe_prefill_forward.  Every call on one device shares that
+ * device's array and leaves its contents behind: calls that overlap on one GPU
+ * (two streams, two runners, two threads) race, and the caller serialises
+ * them.  Enqueue only. */
+#define GW_STATIC_SCRATCH_BYTES ((size_t)8 << 20)
+int gw_moe_prefill_forward_static(gw_expert_runner *runner, const gw_moe_layer_args *args);
+
 /* ---- .gwt installations ---------------------------------------------------
  * A .gwt install is a directory with manifest.json (GodwitManifest,
  * Install/GodwitManifest.swift:8-105) and experts/layer_NN.bin, each
