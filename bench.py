@@ -61,7 +61,7 @@ def gate_up_bytes(lay) -> int:
     return K * per + H * 2 + K * F * 2
 
 
-COUNTER_LAYERS = 4
+COUNTER_LAYERS = L
 # HBM bytes per gate_up_kernel launch (GPT-OSS-120B layer, batch 1): rocprofv3
 # FETCH_SIZE + WRITE_SIZE per dispatch from `bench.py --counter-pass 256`, each
 # scaled by what the counter reads for a 256 MiB device-to-device copy
@@ -71,6 +71,10 @@ GATE_UP_TRAFFIC_BYTES = 35_944_526
 # `bench.py --workload prefill` under rocprofv3 --pmc, the copy scale of the
 # decode run (profiles/prefill_gemm_gptoss_512.md).
 PREFILL_GATE_UP_TRAFFIC_BYTES = 1_294_336_732
+# HBM bytes per decode_layer_kernel launch (the one-kernel layer, GPT-OSS-120B,
+# batch 1), measured as above over the whole 36-layer stack
+# (profiles/decode_layer_traffic.md).
+DECODE_LAYER_TRAFFIC_BYTES = 54_349_808
 
 
 def build_model(ctx, gw, lay, seed: int):
@@ -78,23 +82,30 @@ def build_model(ctx, gw, lay, seed: int):
     return build_model_layers(ctx, gw, lay, seed, L)
 
 
+def fill_layer(ctx, gw, buf, lay, n_experts: int, s: int, biases: bool = True) -> None:
+    """One layer file of synthetic experts in five launches: every packed byte
+    U{0..255} (nibbles U{0..15}), then each section over all experts at once
+    (rows of the expert stride): scales U{119..127}, biases N(0, 0.02) bf16 or
+    zeros."""
+    o, sz = lay.offsets, lay.sizes
+    ctx.fill_uniform_u8(buf, 0, 255, s)
+    for sec, k in (("gate_up_scales", 1), ("down_scales", 2)):
+        ctx.fill_uniform_u8(buf, 119, 127, s * 131 + k, offset=o[sec], count=sz[sec],
+                            rows=n_experts, row_stride=lay.stride)
+    for sec, k in (("gate_up_bias", 3), ("down_bias", 4)):
+        if biases:
+            ctx.fill_normal(buf, gw.BF16, sz[sec] // 2, 0.0, 0.02, s * 131 + k, offset=o[sec],
+                            rows=n_experts, row_stride=lay.stride)
+        else:
+            ctx.fill_uniform_u8(buf, 0, 0, 0, offset=o[sec], count=sz[sec], rows=n_experts,
+                                row_stride=lay.stride)
+
+
 def build_model_layers(ctx, gw, lay, seed: int, n_layers: int):
     bufs = []
-    o, sz = lay.offsets, lay.sizes
     for l in range(n_layers):
         buf = ctx.empty(lay.layer_file_size)
-        s = seed * 1000003 + l * 7919
-        ctx.fill_uniform_u8(buf, 0, 255, s)                       # every nibble U{0..15}
-        for e in range(E):
-            base = e * lay.stride
-            ctx.fill_uniform_u8(buf, 119, 127, s * 131 + 4 * e + 1,
-                                offset=base + o["gate_up_scales"], count=sz["gate_up_scales"])
-            ctx.fill_uniform_u8(buf, 119, 127, s * 131 + 4 * e + 2,
-                                offset=base + o["down_scales"], count=sz["down_scales"])
-            ctx.fill_normal(buf, gw.BF16, 2 * F, 0.0, 0.02, s * 131 + 4 * e + 3,
-                            offset=base + o["gate_up_bias"])
-            ctx.fill_normal(buf, gw.BF16, H, 0.0, 0.02, s * 131 + 4 * e + 4,
-                            offset=base + o["down_bias"])
+        fill_layer(ctx, gw, buf, lay, E, seed * 1000003 + l * 7919)
         bufs.append(buf)
     ctx.synchronize()
     return bufs
@@ -102,13 +113,10 @@ def build_model_layers(ctx, gw, lay, seed: int, n_layers: int):
 
 def counter_pass(gw, args) -> int:
     """The run rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE profiles for the decode
-    kernels: COUNTER_LAYERS GPT-OSS-120B layers resident (fewer than the stack:
-    the profiler does not survive the 36 x 128 x 4 fill dispatches of the full
-    model; per-launch traffic does not depend on how many layers are resident,
-    as no expert is re-read within the L2), --warmup + --steps tokens through
-    them eagerly with fresh N(0,1) logits per layer and token, then three
-    device-to-device copies of --counter-pass MiB, whose known bytes scale the
-    counters."""
+    kernels: the benchmark's own 36-layer GPT-OSS-120B stack (five fill
+    launches per layer), --warmup + --steps tokens through it eagerly with
+    fresh N(0,1) logits per layer and token, then three device-to-device
+    copies of --counter-pass MiB, whose known bytes scale the counters."""
     ctx = gw.Context(0)
     lay = gw.ExpertLayout(H, F, E)
     runner = gw.ExpertRunner(ctx, H, F, "gptOssClampedGLU", 7.0, 1.702)
@@ -237,22 +245,11 @@ def gptoss20b_bench(gw, args) -> int:
     ctx = gw.Context(0)
     lay = gw.ExpertLayout(H, F, E20)
     runner = gw.ExpertRunner(ctx, H, F, "gptOssClampedGLU", 7.0, 1.702)
-    o, sz = lay.offsets, lay.sizes
     layers, routers = [], []
     for l in range(ncopy):
         buf = ctx.empty(lay.layer_file_size)
         sd = args.seed * 1000003 + l * 7919
-        ctx.fill_uniform_u8(buf, 0, 255, sd)
-        for e in range(E20):
-            base = e * lay.stride
-            ctx.fill_uniform_u8(buf, 119, 127, sd * 131 + 4 * e + 1,
-                                offset=base + o["gate_up_scales"], count=sz["gate_up_scales"])
-            ctx.fill_uniform_u8(buf, 119, 127, sd * 131 + 4 * e + 2,
-                                offset=base + o["down_scales"], count=sz["down_scales"])
-            ctx.fill_normal(buf, gw.BF16, 2 * F, 0.0, 0.02, sd * 131 + 4 * e + 3,
-                            offset=base + o["gate_up_bias"])
-            ctx.fill_normal(buf, gw.BF16, H, 0.0, 0.02, sd * 131 + 4 * e + 4,
-                            offset=base + o["down_bias"])
+        fill_layer(ctx, gw, buf, lay, E20, sd)
         rw = ctx.empty(E20 * H * 4)
         ctx.fill_normal(rw, gw.F32, E20 * H, 0.0, 0.02, sd * 17 + 5)
         layers.append(buf)
@@ -333,32 +330,32 @@ def host_threads() -> int:
 def cpu_baseline(seconds: float, threads: int = 1) -> dict:
     """The oracle (scalar C port of the reference CPU path: referenceMXFP4 + bias,
     gptoss activation with fp16 rounding, Router.select, sequential combine) on
-    whole tokens of the same workload until `seconds` have elapsed.  Eight
-    distinct synthetic layer weight sets are cycled so no layer's 53 MB stays
-    in the host caches.  threads > 1 splits each GEMV's rows over that many
-    OpenMP threads (same results)."""
+    whole tokens of the same workload until `seconds` have elapsed: per layer,
+    top-4 of 128 N(0,1) logits, as on the GPU.  The 128 expert slots of a layer
+    point into a pool of 32 distinct synthetic experts (425 MB; slot e of layer l
+    is pool entry (e + 5 l) mod 32), so no selected expert's 13 MB stays in the
+    host caches from one layer to the next.  threads > 1 splits each GEMV's rows
+    over that many OpenMP threads (same results)."""
     import oracle
     oracle.set_threads(threads)
     r = np.random.default_rng(77)
-    sets = []
-    for _ in range(8):
-        experts = []
-        for _ in range(K):
-            experts.append(oracle.Expert(
-                r.integers(0, 256, 2 * F * H // 2, dtype=np.uint8),
-                r.integers(119, 128, 2 * F * H // 32, dtype=np.uint8),
-                r.integers(0, 256, H * F // 2, dtype=np.uint8),
-                r.integers(119, 128, H * F // 32, dtype=np.uint8),
-                oracle.round_to_bf16((r.standard_normal(2 * F) * 0.02).astype(np.float32)),
-                oracle.round_to_bf16((r.standard_normal(H) * 0.02).astype(np.float32))))
-        sets.append(experts)
+    pool = []
+    for _ in range(32):
+        pool.append(oracle.Expert(
+            r.integers(0, 256, 2 * F * H // 2, dtype=np.uint8),
+            r.integers(119, 128, 2 * F * H // 32, dtype=np.uint8),
+            r.integers(0, 256, H * F // 2, dtype=np.uint8),
+            r.integers(119, 128, H * F // 32, dtype=np.uint8),
+            oracle.round_to_bf16((r.standard_normal(2 * F) * 0.02).astype(np.float32)),
+            oracle.round_to_bf16((r.standard_normal(H) * 0.02).astype(np.float32))))
+    slots = [[pool[(e + 5 * l) % 32] for e in range(E)] for l in range(L)]
     x = oracle.round_to_bf16(r.standard_normal(H).astype(np.float32))
     tokens = 0
     t0 = time.perf_counter()
     while True:
         for l in range(L):
-            logits = r.standard_normal((1, K)).astype(np.float32)   # top-4 of the 4 held
-            out, _, _ = oracle.moe_layer(sets[(tokens * L + l) % 8], K, logits, x, H, F)
+            logits = r.standard_normal((1, E)).astype(np.float32)
+            out, _, _ = oracle.moe_layer(slots[l], K, logits, x, H, F)
             x = oracle.round_to_bf16(out[0])
         tokens += 1
         dt = time.perf_counter() - t0
@@ -367,6 +364,32 @@ def cpu_baseline(seconds: float, threads: int = 1) -> dict:
     oracle.set_threads(1)
     return {"tokens": tokens, "seconds": dt, "us_per_token": dt / tokens * 1e6,
             "threads": threads}
+
+
+def timed_rounds(steps: int, run_step, sync, window: int = 20):
+    """The reference's timing protocol (DequantGEMVBenchmark.swift:290-322: 7 rounds,
+    median reported): the `steps` timed steps run as max(1, steps // window)
+    consecutive rounds of about `window` steps, each bracketed by a device
+    synchronisation.  Returns (per-step seconds of each round, total seconds)."""
+    n_rounds = max(1, steps // window)
+    bounds = [steps * i // n_rounds for i in range(n_rounds + 1)]
+    per_step = []
+    sync()
+    t0 = time.perf_counter()
+    for i in range(n_rounds):
+        tr = time.perf_counter()
+        for j in range(bounds[i], bounds[i + 1]):
+            run_step(j)
+        sync()
+        per_step.append((time.perf_counter() - tr) / (bounds[i + 1] - bounds[i]))
+    return per_step, time.perf_counter() - t0
+
+
+def round_stats(per_step, scale: float) -> dict:
+    """rounds / median / min / max of the per-step times, times `scale`."""
+    v = sorted(x * scale for x in per_step)
+    return {"rounds": len(v), "median": round(v[len(v) // 2], 3), "min": round(v[0], 3),
+            "max": round(v[-1], 3)}
 
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 matrix peak
@@ -494,20 +517,10 @@ def qwen3_bench(gw, args, batch: int) -> int:
     # A batch may take the grouped GEMMs (GODWIT_PREFILL_ABOVE below the
     # batch): their scratch has to exist before the step is captured.
     runner.reserve_prefill(batch, Kq, Eq)
-    o, sz = lay.offsets, lay.sizes
     layers = []
     for l in range(Lq):
         buf = ctx.empty(lay.layer_file_size)
-        s = args.seed * 1000003 + l * 7919
-        ctx.fill_uniform_u8(buf, 0, 255, s)
-        for e in range(Eq):
-            base = e * lay.stride
-            ctx.fill_uniform_u8(buf, 119, 127, s * 131 + 4 * e + 1,
-                                offset=base + o["gate_up_scales"], count=sz["gate_up_scales"])
-            ctx.fill_uniform_u8(buf, 119, 127, s * 131 + 4 * e + 2,
-                                offset=base + o["down_scales"], count=sz["down_scales"])
-            for sec in ("gate_up_bias", "down_bias"):
-                ctx.fill_uniform_u8(buf, 0, 0, 0, offset=base + o[sec], count=sz[sec])
+        fill_layer(ctx, gw, buf, lay, Eq, args.seed * 1000003 + l * 7919, biases=False)
         layers.append(buf)
     ctx.synchronize()
     log(f"resident experts: {Lq} x {Eq} x {lay.stride} B = {Lq * lay.layer_file_size / 1e9:.2f} GB")
@@ -537,13 +550,11 @@ def qwen3_bench(gw, args, batch: int) -> int:
 
     for i in range(args.warmup):
         step(i)
-    ctx.synchronize()
     uniq = []
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(args.warmup + i)
-    ctx.synchronize()
-    dt = (time.perf_counter() - t0) / args.steps
+    per_step, elapsed = timed_rounds(args.steps, lambda j: step(args.warmup + j),
+                                     ctx.synchronize)
+    stats = round_stats(per_step, 1e6 / batch)
+    dt = stats["median"] * 1e-6 * batch
     # distinct experts per layer, from the routing of the steps just timed
     lg = logits_all.download(np.float32, total * Lq * batch * Eq).reshape(total, Lq, batch, Eq)
     for i in range(args.warmup, total):
@@ -590,6 +601,8 @@ def qwen3_bench(gw, args, batch: int) -> int:
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
         "us_per_token": round(dt * 1e6 / batch, 2), "hbm_frac_of_peak": round(value / PEAK_HBM_GBS, 4),
+        "us_per_token_mean": round(elapsed / args.steps * 1e6 / batch, 2),
+        **stats, "rounds_unit": "us/token",
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "compute": "e2m1 weights (MXFP4, exact) x bf16 activations, fp32 products and sums",
         "data": "synthetic (seeded MXFP4, zero bias sections, logits N(0,1) per token and layer)",
@@ -605,7 +618,8 @@ def qwen3_bench(gw, args, batch: int) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=140,
+                    help="timed steps, run as rounds of 20 (the median round is reported)")
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -681,13 +695,10 @@ def main() -> int:
 
     for i in range(args.warmup):
         step(i)
-    ctx.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(args.warmup + i)
-    ctx.synchronize()
-    elapsed = time.perf_counter() - t0
-    s_per_token = elapsed / args.steps
+    per_step, elapsed = timed_rounds(args.steps, lambda j: step(args.warmup + j),
+                                     ctx.synchronize)
+    stats = round_stats(per_step, 1e6)
+    s_per_token = stats["median"] * 1e-6
 
     # routing sanity: the last token's experts are distinct and in range
     last = ids.download(np.int32, L * K).reshape(L, K)
@@ -695,7 +706,8 @@ def main() -> int:
 
     bytes_token = L * (K * expert_bytes(lay) + E * 4 + H * 2 + H * 4 + H * 2)
     value = bytes_token / s_per_token / 1e9
-    log(f"{args.steps} tokens in {elapsed * 1e3:.2f} ms: {s_per_token * 1e6:.1f} us/token, "
+    log(f"{args.steps} tokens in {elapsed * 1e3:.2f} ms ({stats['rounds']} rounds): median "
+        f"{stats['median']:.1f} us/token (min {stats['min']:.1f}, max {stats['max']:.1f}), "
         f"{value:.0f} GB/s ({value / PEAK_HBM_GBS * 100:.1f}% of {PEAK_HBM_GBS:.0f})")
 
     roofline = None
@@ -716,7 +728,7 @@ def main() -> int:
         ctx.set_profiling(False)
         if "moe_layer" in kernels:
             dom, nbytes = "moe_layer", bytes_token // L
-            desc = ("moe_layer_kernel (one launch per layer: route + MXFP4 gate_up GEMV + "
+            desc = ("decode_layer_kernel (one launch per layer: route + MXFP4 gate_up GEMV + "
                     "SwiGLU + down GEMV + weighted combine)")
         else:
             dom, nbytes = "gate_up", gate_up_bytes(lay)
@@ -725,7 +737,8 @@ def main() -> int:
         achieved = nbytes / (k_us * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                    "traffic": GATE_UP_TRAFFIC_BYTES if dom == "gate_up" else None,
+                    "traffic": (GATE_UP_TRAFFIC_BYTES if dom == "gate_up"
+                                else DECODE_LAYER_TRAFFIC_BYTES),
                     "kernel": desc, "bytes_per_launch": nbytes, "avg_launch_us": round(k_us, 3)}
         log("kernels: " + ", ".join(f"{k} {v['avg_us']:.2f} us x{v['launches']}"
                                     for k, v in kernels.items()))
@@ -735,9 +748,9 @@ def main() -> int:
         c = cpu_baseline(args.cpu_seconds)
         cpu = {"value": round(bytes_token / (c["us_per_token"] * 1e-6) / 1e9, 4), "unit": "GB/s",
                "us_per_token": round(c["us_per_token"], 1), "cores": 1, "kind": "port",
-               "sample": f"{c['tokens']} token(s) x {L} GPT-OSS-120B-shaped MoE layers (top-4, "
-                         f"2880x2880 experts, 8 distinct synthetic layer weight sets cycled), "
-                         f"scalar C oracle, 1 thread, {c['seconds']:.1f} s",
+               "sample": f"{c['tokens']} token(s) x {L} GPT-OSS-120B-shaped MoE layers (top-4 "
+                         f"of 128 N(0,1) logits, 2880x2880 experts drawn from a pool of 32 "
+                         f"synthetic ones), scalar C oracle, 1 thread, {c['seconds']:.1f} s",
                "cpu": platform.processor() or platform.machine()}
         try:
             with open("/proc/cpuinfo") as f:
@@ -767,6 +780,8 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": round(s_per_token * 1e3, 4),
         "us_per_token": round(s_per_token * 1e6, 2),
+        "us_per_token_mean": round(elapsed / args.steps * 1e6, 2),
+        **stats, "rounds_unit": "us/token",
         "hbm_frac_of_peak": round(value / PEAK_HBM_GBS, 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -27,6 +27,7 @@ import numpy as np
 from ._lib import (ACT_GPTOSS_CLAMPED_GLU, ACT_SILU, BF16, F16, F32, SECTION_COUNT,
                    STATIC_SCRATCH_BYTES,
                    AssignmentC, ExpertLayoutC, ExpertWeightsC, GodwitError, ModelInfoC, MoeBlockArgsC, MoeLayerArgsC,
+                   PrefillViewC,
                    check, lib)
 
 __all__ = [
@@ -137,13 +138,23 @@ class Context:
         check(lib.gw_memcpy_dtod_async(self.handle, dst, src, nbytes))
 
     def fill_uniform_u8(self, buf: DeviceBuffer, lo: int, hi: int, seed: int,
-                        offset: int = 0, count: Optional[int] = None) -> None:
+                        offset: int = 0, count: Optional[int] = None, rows: int = 1,
+                        row_stride: int = 0) -> None:
+        """Seeded bytes uniform over [lo, hi]; with rows > 1, `rows` runs of `count`
+        bytes starting row_stride bytes apart, in one launch."""
         n = buf.nbytes - offset if count is None else count
-        check(lib.gw_fill_uniform_u8(self.handle, buf.address(offset), n, lo, hi, seed))
+        if rows > 1:
+            assert offset + (rows - 1) * row_stride + n <= buf.nbytes
+        check(lib.gw_fill_uniform_u8(self.handle, buf.address(offset), n, rows, row_stride, lo,
+                                     hi, seed))
 
     def fill_normal(self, buf: DeviceBuffer, dtype: int, count: int, mean: float, std: float,
-                    seed: int, offset: int = 0) -> None:
-        check(lib.gw_fill_normal(self.handle, buf.address(offset), dtype, count, mean, std, seed))
+                    seed: int, offset: int = 0, rows: int = 1, row_stride: int = 0) -> None:
+        """Seeded normal(mean, std) values; rows as in fill_uniform_u8."""
+        esz = 4 if dtype == F32 else 2
+        assert offset + (rows - 1) * row_stride + count * esz <= buf.nbytes
+        check(lib.gw_fill_normal(self.handle, buf.address(offset), dtype, count, rows, row_stride,
+                                 mean, std, seed))
 
     # Profiler (Profiler.swift:11-98): per-kernel-family GPU time from hipEvents.
     def set_profiling(self, on: bool) -> None:
@@ -491,6 +502,16 @@ class ExpertRunner:
         b.norm_weight_dtype = norm_weight_dtype
         b.epsilon = epsilon
         check(lib.gw_moe_block_forward(self.handle, ctypes.byref(b)))
+
+    def prefill_view(self) -> dict:
+        """Device addresses of the last grouped batch's routing, activations (two
+        bf16 planes whose sum is the fp16 activation) and per-entry expert outputs
+        in this runner's prefill scratch; valid until its next batch."""
+        v = PrefillViewC()
+        check(lib.gw_expert_runner_prefill_view(self.handle, ctypes.byref(v)))
+        return {"routing_ids": v.routing_ids, "routing_weights": v.routing_weights,
+                "activations": v.activations, "activation_plane": v.activation_plane,
+                "expert_outputs": v.expert_outputs, "tokens": v.tokens, "top_k": v.top_k}
 
     def reserve_prefill(self, max_tokens: int, top_k: int, expert_count: int) -> None:
         """Sizes the prefill scratch up front (required before capturing a graph)."""

@@ -40,6 +40,12 @@ class AssignmentC(ctypes.Structure):
     _fields_ = [("weights", ExpertWeightsC), ("token", _I32), ("routing_weight", _F)]
 
 
+class PrefillViewC(ctypes.Structure):
+    _fields_ = [("routing_ids", _P), ("routing_weights", _P), ("activations", _P),
+                ("activation_plane", ctypes.c_int64), ("expert_outputs", _P),
+                ("tokens", ctypes.c_int32), ("top_k", ctypes.c_int32)]
+
+
 class MoeLayerArgsC(ctypes.Structure):
     _fields_ = [("experts_base", _P), ("expert_stride", _I64), ("expert_count", _I64),
                 ("top_k", _I64), ("logits", _P), ("router_weight", _P),
@@ -85,8 +91,8 @@ SIGNATURES = {
     "gw_memcpy_dtod": (_I, [_P, _P, _P, _SZ]),
     "gw_memset_zero": (_I, [_P, _P, _SZ]),
     "gw_memcpy_dtod_async": (_I, [_P, _P, _P, _SZ]),
-    "gw_fill_uniform_u8": (_I, [_P, _P, _SZ, _I, _I, ctypes.c_uint64]),
-    "gw_fill_normal": (_I, [_P, _P, _I, _SZ, _F, _F, ctypes.c_uint64]),
+    "gw_fill_uniform_u8": (_I, [_P, _P, _SZ, _SZ, _SZ, _I, _I, ctypes.c_uint64]),
+    "gw_fill_normal": (_I, [_P, _P, _I, _SZ, _SZ, _SZ, _F, _F, ctypes.c_uint64]),
     "gw_expert_layout_init": (_I, [_I64, _I64, _I64, ctypes.POINTER(ExpertLayoutC)]),
     "gw_mxfp4_dequant": (_I, [_P, _P, _P, _I64, _P]),
     "gw_mxfp4_gemv": (_I, [_P, _P, _P, _P, _I, _P, _I64, _I64]),
@@ -108,6 +114,7 @@ SIGNATURES = {
     "gw_moe_layer_forward": (_I, [_P, ctypes.POINTER(MoeLayerArgsC)]),
     "gw_moe_prefill_forward": (_I, [_P, ctypes.POINTER(MoeLayerArgsC)]),
     "gw_moe_prefill_forward_static": (_I, [_P, ctypes.POINTER(MoeLayerArgsC)]),
+    "gw_expert_runner_prefill_view": (_I, [_P, ctypes.POINTER(PrefillViewC)]),
     "gw_moe_block_forward": (_I, [_P, ctypes.POINTER(MoeBlockArgsC)]),
     "gw_model_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "gw_model_close": (_I, [_P]),

@@ -354,25 +354,35 @@ extern "C" int gw_memset_zero(gw_context *ctx, void *dst, size_t bytes)
     return GW_OK;
 }
 
-extern "C" int gw_fill_uniform_u8(gw_context *ctx, void *dst, size_t count, int lo, int hi,
-                                  uint64_t seed)
+extern "C" int gw_fill_uniform_u8(gw_context *ctx, void *dst, size_t count, size_t rows,
+                                  size_t row_stride, int lo, int hi, uint64_t seed)
 {
     GW_CHECK(ctx, GW_ERR_ARG, "context is null");
-    GW_CHECK(count == 0 || dst, GW_ERR_ARG, "null pointer");
+    GW_CHECK(count == 0 || rows == 0 || dst, GW_ERR_ARG, "null pointer");
+    GW_CHECK(rows <= 65535 && (rows <= 1 || row_stride >= count), GW_ERR_ARG,
+             "rows %zu (at most 65535) of %zu bytes need a stride of at least that (got %zu)",
+             rows, count, row_stride);
     GW_CHECK(lo >= 0 && hi <= 255 && lo <= hi, GW_ERR_ARG, "bad range [%d, %d]", lo, hi);
     ProfScope ps(ctx, "fill");
-    GW_HIP(gw::launch_fill_u8(ps.launch(launch_of(ctx)), dst, count, lo, hi, seed));
+    GW_HIP(gw::launch_fill_u8(ps.launch(launch_of(ctx)), dst, count, rows, row_stride, lo, hi,
+                              seed));
     return GW_OK;
 }
 
 extern "C" int gw_fill_normal(gw_context *ctx, void *dst, gw_dtype dtype, size_t count,
-                              float mean, float stddev, uint64_t seed)
+                              size_t rows, size_t row_stride, float mean, float stddev,
+                              uint64_t seed)
 {
     GW_CHECK(ctx, GW_ERR_ARG, "context is null");
-    GW_CHECK(count == 0 || dst, GW_ERR_ARG, "null pointer");
+    GW_CHECK(count == 0 || rows == 0 || dst, GW_ERR_ARG, "null pointer");
     GW_CHECK(dtype_ok(dtype), GW_ERR_ARG, "bad dtype %d", (int)dtype);
+    const size_t esz = dtype == GW_F32 ? 4 : 2;
+    GW_CHECK(rows <= 65535 && (rows <= 1 || (row_stride >= count * esz && row_stride % esz == 0)),
+             GW_ERR_ARG, "rows %zu (at most 65535) of %zu elements need a stride of at least "
+             "that many bytes, a multiple of the element size (got %zu)", rows, count, row_stride);
     ProfScope ps(ctx, "fill");
-    GW_HIP(gw::launch_fill_normal(ps.launch(launch_of(ctx)), dst, dtype, count, mean, stddev, seed));
+    GW_HIP(gw::launch_fill_normal(ps.launch(launch_of(ctx)), dst, dtype, count, rows, row_stride,
+                                  mean, stddev, seed));
     return GW_OK;
 }
 
@@ -580,6 +590,7 @@ struct gw_expert_runner {
     uint64_t *xchg_buf = nullptr;    // one-kernel layer: tagged activation words (zeroed once)
     // prefill scratch, sized for pf_tokens tokens x pf_topk ranks x pf_experts
     int pf_tokens = 0, pf_topk = 0, pf_experts = 0;
+    int pf_last_tokens = 0, pf_last_topk = 0;   // of the last batch in pf_buf
     void *pf_buf = nullptr;
     bool decode_layer = true;        // one-token layers in one kernel (GODWIT_DECODE_LAYER=0: two)
     int prefill_above = 1;           // batches larger than this run the grouped GEMMs
@@ -1327,7 +1338,7 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
                 GW_HIP(gw::launch_fill_u8(p.launch(L), ps.arrive,
                                           sizeof(uint32_t) * (size_t)T *
                                               (size_t)((r->hidden + 255) / 256),
-                                          0, 0, 0));
+                                          1, 0, 0, 0, 0));
             }
             g.arrive = ps.arrive;
             g.comb_w = ps.weights;
@@ -1350,12 +1361,34 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
     if (a->routing_weights)
         GW_HIP(hipMemcpyAsync(a->routing_weights, ps.weights, sizeof(float) * T * K,
                               hipMemcpyDeviceToDevice, ctx->stream));
+    if (!use_static) {
+        r->pf_last_tokens = T;
+        r->pf_last_topk = K;
+    }
     return GW_OK;
 }
 
 extern "C" int gw_moe_prefill_forward(gw_expert_runner *r, const gw_moe_layer_args *a)
 {
     return moe_prefill_impl(r, a, 0);
+}
+
+extern "C" int gw_expert_runner_prefill_view(gw_expert_runner *r, gw_prefill_view *v)
+{
+    GW_CHECK(r && v, GW_ERR_ARG, "null argument");
+    GW_CHECK(r->pf_buf && r->pf_last_tokens > 0, GW_ERR_ARG,
+             "no batch has run through this runner's prefill scratch");
+    PrefillScratch ps;
+    prefill_layout(r, r->pf_tokens, r->pf_topk, r->pf_experts, static_cast<char *>(r->pf_buf),
+                   &ps);
+    v->routing_ids = ps.ids;
+    v->routing_weights = ps.weights;
+    v->activations = ps.act;
+    v->activation_plane = (int64_t)r->pf_last_tokens * r->pf_last_topk * r->inter;
+    v->expert_outputs = ps.y;
+    v->tokens = r->pf_last_tokens;
+    v->top_k = r->pf_last_topk;
+    return GW_OK;
 }
 
 extern "C" int gw_moe_prefill_forward_static(gw_expert_runner *r, const gw_moe_layer_args *a)

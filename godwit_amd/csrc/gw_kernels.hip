@@ -741,15 +741,20 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z)
     return z ^ (z >> 31);
 }
 
+// Row blockIdx.y of rows spaced row_stride bytes apart; value i of the fill
+// (row * count + element; 8-byte units for bytes) depends only on (seed, i),
+// so one row is the plain contiguous fill.
 __global__ __launch_bounds__(256) void fill_u8_kernel(uint8_t *__restrict__ dst, int64_t count,
-                                                      uint32_t lo, uint32_t range,
-                                                      uint64_t seed)
+                                                      int64_t row_stride, uint32_t lo,
+                                                      uint32_t range, uint64_t seed)
 {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // 8 bytes each
     const int64_t b0 = i * 8;
     if (b0 >= count) return;
-    const uint64_t h0 = mix64(seed ^ mix64((uint64_t)i * 2));
-    const uint64_t h1 = mix64(seed ^ mix64((uint64_t)i * 2 + 1));
+    const int64_t unit = (int64_t)blockIdx.y * ((count + 7) / 8) + i;
+    uint8_t *row = dst + (int64_t)blockIdx.y * row_stride;
+    const uint64_t h0 = mix64(seed ^ mix64((uint64_t)unit * 2));
+    const uint64_t h1 = mix64(seed ^ mix64((uint64_t)unit * 2 + 1));
     uint64_t word = 0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -757,27 +762,30 @@ __global__ __launch_bounds__(256) void fill_u8_kernel(uint8_t *__restrict__ dst,
         const uint32_t v = lo + ((r16 * range) >> 16);
         word |= (uint64_t)(v & 0xFFu) << (8 * k);
     }
-    if (b0 + 8 <= count && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
-        *reinterpret_cast<uint64_t *>(dst + b0) = word;
+    if (b0 + 8 <= count && (reinterpret_cast<uintptr_t>(row) & 7) == 0) {
+        *reinterpret_cast<uint64_t *>(row + b0) = word;
     } else {
-        for (int k = 0; k < 8 && b0 + k < count; ++k) dst[b0 + k] = (uint8_t)(word >> (8 * k));
+        for (int k = 0; k < 8 && b0 + k < count; ++k) row[b0 + k] = (uint8_t)(word >> (8 * k));
     }
 }
 
 __global__ __launch_bounds__(256) void fill_normal_kernel(void *__restrict__ dst, int dt,
-                                                          int64_t count, float mean,
-                                                          float stddev, uint64_t seed)
+                                                          int64_t count, int64_t row_stride,
+                                                          float mean, float stddev,
+                                                          uint64_t seed)
 {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= count) return;
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= count) return;
+    const int64_t i = (int64_t)blockIdx.y * count + e;
+    void *row = static_cast<uint8_t *>(dst) + (int64_t)blockIdx.y * row_stride;
     const uint64_t h = mix64(seed ^ mix64((uint64_t)i));
     const float u1 = ((float)(h >> 40) + 1.0f) * (1.0f / 16777216.0f);        // (0, 1]
     const float u2 = (float)((h >> 16) & 0xFFFFFFull) * (1.0f / 16777216.0f);  // [0, 1)
     const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
     const float v = mean + stddev * z;
-    if (dt == DT_F32) static_cast<float *>(dst)[i] = v;
-    else if (dt == DT_BF16) static_cast<uint16_t *>(dst)[i] = f32_to_bf16_bits(v);
-    else static_cast<uint16_t *>(dst)[i] = f32_to_f16_bits(v);
+    if (dt == DT_F32) static_cast<float *>(row)[e] = v;
+    else if (dt == DT_BF16) static_cast<uint16_t *>(row)[e] = f32_to_bf16_bits(v);
+    else static_cast<uint16_t *>(row)[e] = f32_to_f16_bits(v);
 }
 
 // ---------------------------------------------------------------------------
@@ -990,23 +998,24 @@ hipError_t launch_route(const Launch &L, const RouteArgs &route, Plan *plan)
     return hipGetLastError();
 }
 
-hipError_t launch_fill_u8(const Launch &L, void *dst, size_t count, int lo, int hi,
-                          uint64_t seed)
+hipError_t launch_fill_u8(const Launch &L, void *dst, size_t count, size_t rows,
+                          size_t row_stride, int lo, int hi, uint64_t seed)
 {
-    if (count == 0) return hipSuccess;
+    if (count == 0 || rows == 0) return hipSuccess;
     const int64_t threads = ((int64_t)count + 7) / 8;
     const uint32_t range = (uint32_t)(hi - lo + 1);
-    GW_LAUNCH(fill_u8_kernel, dim3(div_up(threads, 256)), dim3(256), 0, L,
-              static_cast<uint8_t *>(dst), (int64_t)count, (uint32_t)lo, range, seed);
+    GW_LAUNCH(fill_u8_kernel, dim3(div_up(threads, 256), (unsigned)rows), dim3(256), 0, L,
+              static_cast<uint8_t *>(dst), (int64_t)count, (int64_t)row_stride, (uint32_t)lo,
+              range, seed);
     return hipGetLastError();
 }
 
-hipError_t launch_fill_normal(const Launch &L, void *dst, int dt, size_t count, float mean,
-                              float stddev, uint64_t seed)
+hipError_t launch_fill_normal(const Launch &L, void *dst, int dt, size_t count, size_t rows,
+                              size_t row_stride, float mean, float stddev, uint64_t seed)
 {
-    if (count == 0) return hipSuccess;
-    GW_LAUNCH(fill_normal_kernel, dim3(div_up((int64_t)count, 256)), dim3(256), 0, L, dst, dt,
-              (int64_t)count, mean, stddev, seed);
+    if (count == 0 || rows == 0) return hipSuccess;
+    GW_LAUNCH(fill_normal_kernel, dim3(div_up((int64_t)count, 256), (unsigned)rows), dim3(256), 0,
+              L, dst, dt, (int64_t)count, (int64_t)row_stride, mean, stddev, seed);
     return hipGetLastError();
 }
 

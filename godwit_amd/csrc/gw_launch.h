@@ -181,10 +181,10 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
 hipError_t launch_prefill_combine(const Launch &L, const float *y, const float *w, int T, int K,
                                   int H, float *out, uint16_t *out_bf16, int residual);
 
-hipError_t launch_fill_u8(const Launch &L, void *dst, size_t count, int lo, int hi,
-                          uint64_t seed);
-hipError_t launch_fill_normal(const Launch &L, void *dst, int dt, size_t count, float mean,
-                              float stddev, uint64_t seed);
+hipError_t launch_fill_u8(const Launch &L, void *dst, size_t count, size_t rows,
+                          size_t row_stride, int lo, int hi, uint64_t seed);
+hipError_t launch_fill_normal(const Launch &L, void *dst, int dt, size_t count, size_t rows,
+                              size_t row_stride, float mean, float stddev, uint64_t seed);
 
 // LDS bytes the down kernel needs per slot of staged activations and the
 // fixed part; used by the host to bound slots per chunk.

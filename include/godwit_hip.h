@@ -103,13 +103,16 @@ int gw_memcpy_dtod_async(gw_context *ctx, void *dst, const void *src, size_t byt
 
 /* Seeded synthetic data on the device (counter-based: element i depends only
  * on (seed, i)).  Replaces the xorshift inputs of
- * DequantGEMVBenchmark.swift:35-54 for the large configurations.
+ * DequantGEMVBenchmark.swift:35-54 for the large configurations.  One launch
+ * fills `rows` runs of `count` elements whose starts are `row_stride` bytes
+ * apart (one section of every expert of a layer, say); element i is
+ * row * count + position, so rows == 1 is the plain contiguous fill.
  *  - bytes uniform over [lo, hi] inclusive;
  *  - normal(mean, std) written as f32, f16 or bf16 (RNE). */
-int gw_fill_uniform_u8(gw_context *ctx, void *dst, size_t count, int lo, int hi,
-                       uint64_t seed);
-int gw_fill_normal(gw_context *ctx, void *dst, gw_dtype dtype, size_t count, float mean,
-                   float std, uint64_t seed);
+int gw_fill_uniform_u8(gw_context *ctx, void *dst, size_t count, size_t rows,
+                       size_t row_stride, int lo, int hi, uint64_t seed);
+int gw_fill_normal(gw_context *ctx, void *dst, gw_dtype dtype, size_t count, size_t rows,
+                   size_t row_stride, float mean, float std, uint64_t seed);
 
 /* ---- expert weight layout (ExpertLayout, Install/InstallLayout.swift:14-121) */
 
@@ -293,6 +296,26 @@ int gw_moe_layer_forward(gw_expert_runner *runner, const gw_moe_layer_args *args
 int gw_expert_runner_reserve_prefill(gw_expert_runner *runner, int32_t max_tokens, int32_t top_k,
                                      int32_t expert_count);
 int gw_moe_prefill_forward(gw_expert_runner *runner, const gw_moe_layer_args *args);
+
+/* Inspection, no counterpart in the reference (the Metal runner exposes its
+ * intermediate buffers to its own tests the same way): device pointers into
+ * this runner's prefill scratch as the last batch through it left them
+ * (gw_moe_prefill_forward, or gw_moe_layer_forward / gw_moe_block_forward on
+ * the grouped GEMMs), valid until the next such call.  Entry j = token *
+ * top_k + rank.  activations: two bf16 planes [2][tokens * top_k][intermediate]
+ * (plane 1 at activations + activation_plane) whose sum is the entry's fp16
+ * activation exactly; expert_outputs: [tokens * top_k][hidden] fp32, down
+ * projection plus bias, before the weighted combine.  Returns GW_ERR_ARG
+ * before the first batch. */
+typedef struct gw_prefill_view {
+    const int32_t *routing_ids;        /* [tokens * top_k] */
+    const float *routing_weights;      /* [tokens * top_k] */
+    const uint16_t *activations;
+    int64_t activation_plane;          /* elements between the two planes */
+    const float *expert_outputs;
+    int32_t tokens, top_k;
+} gw_prefill_view;
+int gw_expert_runner_prefill_view(gw_expert_runner *runner, gw_prefill_view *view);
 
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

@@ -87,3 +87,33 @@ class ExpertData:
     def oracle_expert(self):
         return oracle.Expert(self.gu_packed, self.gu_scales, self.dn_packed, self.dn_scales,
                              self.gu_bias, self.dn_bias)
+
+
+def fill_layer_device(ctx, buf, layout, n_experts, seed, biases=True):
+    """A layer file of synthetic experts filled on the device in five launches:
+    packed bytes U{0..255}, each scale section U{119..127} over all experts at
+    once (rows of the expert stride), biases N(0, 0.02) bf16 or zeros."""
+    import godwit_amd as gw
+    o, sz = layout.offsets, layout.sizes
+    ctx.fill_uniform_u8(buf, 0, 255, seed)
+    for sec, k in (("gate_up_scales", 1), ("down_scales", 2)):
+        ctx.fill_uniform_u8(buf, 119, 127, seed * 131 + k, offset=o[sec], count=sz[sec],
+                            rows=n_experts, row_stride=layout.stride)
+    for sec, k in (("gate_up_bias", 3), ("down_bias", 4)):
+        if biases:
+            ctx.fill_normal(buf, gw.BF16, sz[sec] // 2, 0.0, 0.02, seed * 131 + k, offset=o[sec],
+                            rows=n_experts, row_stride=layout.stride)
+        else:
+            ctx.fill_uniform_u8(buf, 0, 0, 0, offset=o[sec], count=sz[sec], rows=n_experts,
+                                row_stride=layout.stride)
+
+
+def expert_from_blob(blob, layout):
+    """oracle.Expert over one expert's bytes in the .gwt stride layout (bf16 biases
+    widened to fp32)."""
+    o, sz = layout.offsets, layout.sizes
+    sec = {k: blob[o[k]:o[k] + sz[k]] for k in o}
+    return oracle.Expert(sec["gate_up_blocks"], sec["gate_up_scales"], sec["down_blocks"],
+                         sec["down_scales"],
+                         oracle.bf16_bits_to_f32(sec["gate_up_bias"].view(np.uint16)),
+                         oracle.bf16_bits_to_f32(sec["down_bias"].view(np.uint16)))

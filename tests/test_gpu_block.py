@@ -4,8 +4,9 @@ composition: oracle.rmsnorm_f16 (TransformerLayer.normalise, :265-285), the
 oracle layer on those fp16 rows, then the fp32 residual add.
 
 Tolerance: the expert metric max|d|/mean|moe| < 1e-3 (GodwitCLI/main.swift:
-518-532) on the change the block makes to the stream (prefill: the 5e-3 per
-token / 1e-4 median rule of the prefill tests); routing ids exact.  The GPU's
+518-532) on the change the block makes to the stream (prefill: every token
+below 1e-3, the median below 1e-4, as in the prefill tests); routing ids
+exact.  The GPU's
 sum of squares is a tree, so a normalised value can differ from the oracle's by
 one fp16 ulp, well inside that bound.
 """
@@ -115,7 +116,7 @@ def test_block_prefill_matches_oracle(ctx, T):
     ref, moe, rid, _ = _oracle_block(experts, shape, K, logits, stream, wbits, eps)
     assert np.array_equal(gid, rid.reshape(T, K))
     m = np.array([expert_metric(got[t] - stream[t], moe[t]) for t in range(T)])
-    assert m.max() < 5e-3 and np.median(m) < 1e-4, (m.max(), np.median(m))
+    assert m.max() < 1e-3 and np.median(m) < 1e-4, (m.max(), np.median(m))
     buf.free()
     runner.close()
 

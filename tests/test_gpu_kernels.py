@@ -254,3 +254,34 @@ def test_router_logits(ctx):
     assert d.experts == list(ids) and np.allclose(d.weights, w, rtol=0, atol=0)
     wb.free()
     bb.free()
+
+
+def test_fill_rows_equal_contiguous(ctx):
+    """One strided fill launch over `rows` runs (one section of every expert of a
+    layer, as the benchmark fills its weights) equals the contiguous fill of
+    rows * count values cut into rows, and leaves the bytes between runs alone."""
+    rows, count, stride = 5, 40, 72            # bytes: 8-byte units, rows not 8-aligned
+    buf = ctx.buffer(np.full(rows * stride, 0xA5, np.uint8))
+    ctx.fill_uniform_u8(buf, 3, 200, 99, count=count, rows=rows, row_stride=stride)
+    ref = ctx.empty(rows * count)
+    ctx.fill_uniform_u8(ref, 3, 200, 99, count=rows * count)
+    ctx.synchronize()
+    got = buf.download(np.uint8).reshape(rows, stride)
+    want = ref.download(np.uint8).reshape(rows, count)
+    assert np.array_equal(got[:, :count], want)
+    assert (got[:, count:] == 0xA5).all()
+    assert want.min() >= 3 and want.max() <= 200
+    n, stride2 = 37, 100                       # bf16 normals, 2-byte aligned rows
+    buf2 = ctx.buffer(np.full(3 * stride2, 0x5A, np.uint8))
+    ctx.fill_normal(buf2, gw.BF16, n, 0.0, 1.0, 7, offset=2, rows=3, row_stride=stride2)
+    ref2 = ctx.empty(3 * n * 2)
+    ctx.fill_normal(ref2, gw.BF16, 3 * n, 0.0, 1.0, 7)
+    ctx.synchronize()
+    raw = buf2.download(np.uint8)
+    want2 = ref2.download(np.uint16).reshape(3, n)
+    for r in range(3):
+        row = raw[r * stride2 + 2:r * stride2 + 2 + 2 * n].view(np.uint16)
+        assert np.array_equal(row, want2[r]), r
+        assert (raw[r * stride2 + 2 + 2 * n:(r + 1) * stride2 + 2][:stride2 - 2 * n] == 0x5A).all()
+    for b in (buf, ref, buf2, ref2):
+        b.free()

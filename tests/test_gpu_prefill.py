@@ -3,8 +3,8 @@ against the decode path.
 
 The oracle is the reference's layer: route each token (Router.select), run
 every selected expert (referenceMXFP4 GEMVs + activation with fp16 rounding)
-and combine in router order (layer_reference.py).  Tolerance: the reference's
-expert metric max|d|/mean|ref| per token (GodwitCLI/main.swift:518-532), see
+and combine in router order.  Tolerance: the reference's expert metric
+max|d|/mean|ref| per token (GodwitCLI/main.swift:518-532) below 1e-3, see
 _close_batch; routing ids exact, weights to 1e-6.  Shapes cover one, two and three bf16
 activation planes (bf16, fp16, fp32 x), partial feature tiles, K dimensions
 that are not a multiple of the 256-element staging chunk, experts with no
@@ -22,15 +22,14 @@ pytestmark = pytest.mark.gpu
 
 
 def _close_batch(got, ref):
-    """Per-token expert metric.  A gate_up sum whose last fp32 bits differ from the
-    oracle's can round its fp16 activation one ulp the other way (the reference
-    rounds the activation to fp16, expert.metal:101), which moves a token's down
-    output by up to ~1e-3 of its mean magnitude; with many (token, expert) pairs a
-    few such flips are expected.  So: every token within the reference's own
-    check-expert tolerance (5e-3, GodwitCLI/main.swift:518-532) and the median
-    token within 1e-4 (the accumulation itself is exact to fp32 rounding)."""
+    """Per-token expert metric (GodwitCLI/main.swift:518-532) below 1e-3, the
+    north-star tolerance, and the median token below 1e-4.  A gate_up sum whose
+    last fp32 bits differ from the oracle's can round its fp16 activation one ulp
+    the other way (the reference rounds the activation to fp16, expert.metal:101);
+    test_gpu_config4 takes the 512-token layer apart stage by stage and finds
+    exactly such flips, plus fp32 summation differences within their bound."""
     m = np.array([expert_metric(got[t], ref[t]) for t in range(len(ref))])
-    assert m.max() < 5e-3, (m.max(), np.argmax(m))
+    assert m.max() < 1e-3, (m.max(), np.argmax(m))
     assert np.median(m) < 1e-4, np.median(m)
 
 

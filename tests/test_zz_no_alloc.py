@@ -38,7 +38,7 @@ def test_static_scratch_prefill_equals_reserved(ctx):
                                         xw, H, F, shape["oact"])
         assert np.array_equal(got[2], rids)
         m = max(expert_metric(got[0][t], ref[t]) for t in range(T))
-        assert m < 5e-3, (T, m)
+        assert m < 1e-3, (T, m)
         for b in (xb, lb):
             b.free()
     # 2880 x 2880, top-4: about 116 KiB of scratch per token, so 256 tokens cannot fit
