@@ -192,12 +192,15 @@ class Graph:
     @staticmethod
     def capture(ctx: Context, body) -> "Graph":
         check(lib.gw_graph_begin_capture(ctx.handle))
+        h = ctypes.c_void_p()
         try:
             body()
-        finally:
-            h = ctypes.c_void_p()
-            rc = lib.gw_graph_end_capture(ctx.handle, ctypes.byref(h))
-        check(rc)
+        except BaseException:
+            # end the capture and drop the partial graph, then re-raise
+            if lib.gw_graph_end_capture(ctx.handle, ctypes.byref(h)) == 0 and h.value:
+                lib.gw_graph_destroy(h.value)
+            raise
+        check(lib.gw_graph_end_capture(ctx.handle, ctypes.byref(h)))
         return Graph(ctx, h.value)
 
     def launch(self) -> None:
@@ -358,7 +361,12 @@ class ExpertRunner:
                                           ctypes.byref(h)))
         self.handle = h.value
         if bias_dtype != BF16:
-            check(lib.gw_expert_runner_set_bias_dtype(self.handle, bias_dtype))
+            rc = lib.gw_expert_runner_set_bias_dtype(self.handle, bias_dtype)
+            if rc != 0:
+                err = GodwitError(rc, (lib.gw_last_error() or b"").decode())
+                lib.gw_expert_runner_destroy(self.handle)
+                self.handle = None
+                raise err
         self._x: Optional[DeviceBuffer] = None
         self._y: Optional[DeviceBuffer] = None
 

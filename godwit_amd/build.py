@@ -23,6 +23,10 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["gw_kernels.hip", "gw_decode.hip", "gw_prefill.hip", "gw_model.hip", "gw_api.hip"]
+# Host-only C++ (no HIP), compiled by the host compiler.
+HOST_SOURCES = ["gw_host.cpp"]
+CXX = os.environ.get("CXX", "g++")
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-fvisibility=hidden"]
 OBJDIR = os.path.join(HERE, "_build")
 
 FLAGS = [
@@ -39,15 +43,19 @@ FLAGS = [
 
 
 def build(verbose: bool = True) -> str:
-    """Compiles the sources in parallel (one hipcc per file), then links."""
+    """Compiles the sources in parallel (hipcc per HIP file, the host compiler for
+    the host-only C++), then links."""
     os.makedirs(OBJDIR, exist_ok=True)
     inc = ["-I", os.path.join(HERE, "..", "include")]
     t0 = time.time()
     procs = []
-    for src in SOURCES:
-        obj = os.path.join(OBJDIR, src.replace(".hip", ".o"))
-        cmd = [HIPCC, *[f for f in FLAGS if f != "-shared"], *inc, "-c", "-o", obj,
-               os.path.join(CSRC, src)]
+    for src in SOURCES + HOST_SOURCES:
+        obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
+        if src.endswith(".hip"):
+            cmd = [HIPCC, *[f for f in FLAGS if f != "-shared"], *inc, "-c", "-o", obj,
+                   os.path.join(CSRC, src)]
+        else:
+            cmd = [CXX, *HOST_FLAGS, *inc, "-c", "-o", obj, os.path.join(CSRC, src)]
         procs.append((src, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE,
                                                  stderr=subprocess.STDOUT, text=True)))
     objs, failed, noise = [], False, []

@@ -19,27 +19,17 @@
 
 #include "../../include/godwit_hip.h"
 #include "gw_error.h"
+#include "gw_host.h"
 #include "gw_launch.h"
 #include "gw_plan.h"
 
+using gw::HostPlan;
 using gw::Plan;
+using gw::plan_add;
 
 // ---------------------------------------------------------------------------
 // errors
 // ---------------------------------------------------------------------------
-
-static thread_local std::string g_error;
-
-int gw::set_error(int code, const char *fmt, ...)
-{
-    char buf[512];
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(buf, sizeof(buf), fmt, ap);
-    va_end(ap);
-    g_error = buf;
-    return code;
-}
 
 #define fail gw::set_error
 
@@ -56,7 +46,6 @@ int gw::set_error(int code, const char *fmt, ...)
         if (!(cond)) return fail(code, __VA_ARGS__); \
     } while (0)
 
-extern "C" const char *gw_last_error(void) { return g_error.c_str(); }
 extern "C" const char *gw_version(void) { return "godwit_hip 0.1 (gfx950)"; }
 
 static bool dtype_ok(int dt) { return dt == GW_F32 || dt == GW_F16 || dt == GW_BF16; }
@@ -82,6 +71,16 @@ struct gw_context {
     std::vector<hipEvent_t> event_pool;  // reusable events
     std::vector<std::pair<std::string, std::pair<double, int64_t>>> totals;
 };
+
+// True while the context's stream is being captured, by gw_graph_begin_capture
+// or by a caller's own capture of that stream.
+static bool is_capturing(const gw_context *ctx)
+{
+    if (ctx->capturing) return true;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(ctx->stream, &st) == hipSuccess &&
+           st == hipStreamCaptureStatusActive;
+}
 
 static gw::Launch launch_of(gw_context *ctx)
 {
@@ -117,7 +116,7 @@ struct ProfScope {
     ProfScope(gw_context *c, const char *n) : ctx(c), name(n) {}
     gw::Launch launch(gw::Launch L)
     {
-        if (ctx->profiling && !ctx->capturing && !start) {
+        if (ctx->profiling && !is_capturing(ctx) && !start) {
             start = take_event(ctx);
             end = start ? take_event(ctx) : nullptr;
             if (start && end) {
@@ -217,7 +216,7 @@ extern "C" int gw_context_destroy(gw_context *ctx)
 extern "C" int gw_context_synchronize(gw_context *ctx)
 {
     GW_CHECK(ctx, GW_ERR_ARG, "context is null");
-    GW_CHECK(!ctx->capturing, GW_ERR_ARG, "synchronize during graph capture");
+    GW_CHECK(!is_capturing(ctx), GW_ERR_ARG, "synchronize during graph capture");
     GW_HIP(hipStreamSynchronize(ctx->stream));
     return GW_OK;
 }
@@ -293,6 +292,16 @@ extern "C" int gw_context_profile_reset(gw_context *ctx)
 // memory
 // ---------------------------------------------------------------------------
 
+// A failed allocation: the status (GW_ERR_OOM for out-of-memory), and the
+// runtime's last-error record cleared, so that the next launch's
+// hipGetLastError does not report this failure again.
+static int alloc_failed(hipError_t e, const char *what, size_t bytes)
+{
+    (void)hipGetLastError();
+    return fail(e == hipErrorOutOfMemory ? GW_ERR_OOM : GW_ERR_HIP, "%s(%zu): %s", what, bytes,
+                hipGetErrorString(e));
+}
+
 extern "C" int gw_malloc(gw_context *ctx, size_t bytes, void **out)
 {
     GW_CHECK(ctx && out, GW_ERR_ARG, "null argument");
@@ -302,8 +311,7 @@ extern "C" int gw_malloc(gw_context *ctx, size_t bytes, void **out)
     hipError_t e = hipMalloc(out, bytes);
     if (e != hipSuccess) {
         *out = nullptr;
-        return fail(e == hipErrorOutOfMemory ? GW_ERR_OOM : GW_ERR_HIP,
-                    "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        return alloc_failed(e, "hipMalloc", bytes);
     }
     return GW_OK;
 }
@@ -321,7 +329,7 @@ static int copy(gw_context *ctx, void *dst, const void *src, size_t n, hipMemcpy
     GW_CHECK(ctx, GW_ERR_ARG, "context is null");
     if (n == 0) return GW_OK;
     GW_CHECK(dst && src, GW_ERR_ARG, "null pointer");
-    GW_CHECK(!ctx->capturing, GW_ERR_ARG, "blocking copy during graph capture");
+    GW_CHECK(!is_capturing(ctx), GW_ERR_ARG, "blocking copy during graph capture");
     GW_HIP(hipMemcpyAsync(dst, src, n, kind, ctx->stream));
     GW_HIP(hipStreamSynchronize(ctx->stream));
     return GW_OK;
@@ -348,7 +356,7 @@ extern "C" int gw_memset_zero(gw_context *ctx, void *dst, size_t bytes)
     GW_CHECK(ctx, GW_ERR_ARG, "context is null");
     if (bytes == 0) return GW_OK;
     GW_CHECK(dst, GW_ERR_ARG, "null pointer");
-    GW_CHECK(!ctx->capturing, GW_ERR_ARG, "memset during graph capture");
+    GW_CHECK(!is_capturing(ctx), GW_ERR_ARG, "memset during graph capture");
     GW_HIP(hipMemsetAsync(dst, 0, bytes, ctx->stream));
     GW_HIP(hipStreamSynchronize(ctx->stream));
     return GW_OK;
@@ -469,8 +477,11 @@ extern "C" int gw_mxfp4_gemv_bias(gw_context *ctx, const uint8_t *packed, const 
     GW_CHECK(!bias || dtype_ok(bias_dtype), GW_ERR_ARG, "bad bias dtype %d", (int)bias_dtype);
     if (rows == 0) return GW_OK;
     if (cols == 0) {
+        // y = 0: a fill kernel rather than a memset, so that the call can be
+        // captured into a graph (no memset node).
         GW_CHECK(!bias, GW_ERR_UNSUPPORTED, "cols == 0 with bias");
-        GW_HIP(hipMemsetAsync(y, 0, rows * 4, ctx->stream));
+        ProfScope ps(ctx, "fill");
+        GW_HIP(gw::launch_fill_u8(ps.launch(launch_of(ctx)), y, (size_t)rows * 4, 1, 0, 0, 0, 0));
         return GW_OK;
     }
     ProfScope ps(ctx, "gemv");
@@ -672,8 +683,7 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         gw_expert_runner_destroy(r);
-        return fail(e == hipErrorOutOfMemory ? GW_ERR_OOM : GW_ERR_HIP, "runner scratch: %s",
-                    hipGetErrorString(e));
+        return alloc_failed(e, "runner scratch", 0);
     }
     r->decode_layer = get_env_int("GODWIT_DECODE_LAYER", 1) != 0;
     const int pa = get_env_int("GODWIT_PREFILL_ABOVE", 1);
@@ -708,6 +718,22 @@ extern "C" int gw_expert_runner_set_bias_dtype(gw_expert_runner *r, gw_dtype bia
 {
     GW_CHECK(r, GW_ERR_ARG, "runner is null");
     GW_CHECK(bias_dtype == GW_BF16 || bias_dtype == GW_F32, GW_ERR_ARG, "bad bias dtype");
+    if (bias_dtype == GW_F32) {
+        // The .gwt layout sizes the bias sections for bf16; fp32 values need
+        // twice the bytes, which must still end before the next section (the
+        // gate_up bias) or the expert stride (the down bias).
+        gw_expert_layout lay;
+        int rc = gw_expert_layout_init(r->hidden, r->inter, 1, &lay);
+        if (rc) return rc;
+        const int64_t gu_end = r->offsets[GW_SECTION_GATE_UP_BIAS] + 4 * 2 * r->inter;
+        const int64_t dn_end = r->offsets[GW_SECTION_DOWN_BIAS] + 4 * r->hidden;
+        GW_CHECK(gu_end <= r->offsets[GW_SECTION_DOWN_BIAS] && dn_end <= lay.stride, GW_ERR_SHAPE,
+                 "fp32 biases of %lld + %lld rows overflow their sections in the expert layout "
+                 "(gate_up bias ends at %lld, down bias at %lld; limits %lld and %lld)",
+                 (long long)(2 * r->inter), (long long)r->hidden, (long long)gu_end,
+                 (long long)dn_end, (long long)r->offsets[GW_SECTION_DOWN_BIAS],
+                 (long long)lay.stride);
+    }
     r->bias_dt = bias_dtype;
     return GW_OK;
 }
@@ -732,26 +758,6 @@ static gw::Sections sections_of(const int64_t off[GW_SECTION_COUNT])
     return s;
 }
 
-// A host-built plan: expert-major groups over assignments, in order.
-struct HostPlan {
-    Plan p;
-    const gw_expert_weights *group_w[gw::kMaxSlots];
-    int max_group_tokens = 0;
-    void clear()
-    {
-        memset(&p, 0, sizeof(p));
-        max_group_tokens = 0;
-    }
-};
-
-static bool same_weights(const gw_expert_weights *a, const gw_expert_weights *b)
-{
-    if (a->buffer != b->buffer) return false;
-    for (int s = 0; s < GW_SECTION_COUNT; ++s)
-        if (a->offsets[s] != b->offsets[s]) return false;
-    return true;
-}
-
 // Runs one plan: upload, fused gate_up + activation, fused down + combine.
 // All groups of a plan share one set of section offsets (the runner launches
 // a separate plan per distinct offset set).
@@ -759,29 +765,8 @@ static int run_plan(gw_expert_runner *r, HostPlan &hp, const int64_t offsets[GW_
                     const void *inputs, int x_dt, float *outputs, int accumulate)
 {
     gw_context *ctx = r->ctx;
-    // Regroup slots group-major (the kernels' convention): slots were appended
-    // in assignment order; renumber so each group's slots are contiguous.
-    Plan &p = hp.p;
-    Plan q = p;
-    int next = 0;
-    int remap[gw::kMaxSlots];
-    for (int g = 0; g < p.ngroups; ++g) {
-        q.group_slot0[g] = next;
-        int k = 0;
-        for (int s = 0; s < p.nslots; ++s) {
-            if (p.slot_group[s] != g) continue;
-            remap[s] = next;
-            q.slot_token[next] = p.slot_token[s];
-            q.slot_group[next] = g;
-            q.slot_weight[next] = p.slot_weight[s];
-            ++next;
-            ++k;
-        }
-        q.group_ntok[g] = k;
-    }
-    for (int t = 0; t < p.ntokens; ++t)
-        for (int k = 0; k < p.tok_nslots[t]; ++k) q.tok_slots[t][k] = remap[p.tok_slots[t][k]];
-    for (int g = 0; g < p.ngroups; ++g) q.group_base[g] = hp.group_w[g]->buffer;
+    Plan q;
+    gw::plan_regroup(hp, q);
 
     if (r->ring_used == kPlanRing) {   // staging slots are reused only after their copies ran
         GW_HIP(hipStreamSynchronize(ctx->stream));
@@ -816,49 +801,6 @@ static int run_plan(gw_expert_runner *r, HostPlan &hp, const int64_t offsets[GW_
     return GW_OK;
 }
 
-// Adds (weights, token, w) to the plan being built; returns false if it does
-// not fit (the caller flushes and retries on an empty plan).
-static bool plan_add(HostPlan &hp, const gw_expert_weights *w, int32_t token, float weight,
-                     bool merge)
-{
-    Plan &p = hp.p;
-    if (p.nslots >= gw::kMaxSlots) return false;
-    int local = -1;
-    for (int t = 0; t < p.ntokens; ++t)
-        if (p.tok_global[t] == token) local = t;
-    if (local < 0) {
-        if (p.ntokens >= gw::kMaxTokens) return false;
-        local = p.ntokens;
-        p.tok_global[local] = token;
-        p.tok_nslots[local] = 0;
-        p.ntokens += 1;
-    }
-    if (p.tok_nslots[local] >= gw::kMaxTopK) return false;
-    int g = -1;
-    if (merge) {
-        for (int k = 0; k < p.ngroups; ++k) {
-            if (!same_weights(hp.group_w[k], w)) continue;
-            bool has = false;   // a group holds each token at most once
-            for (int s = 0; s < p.nslots; ++s)
-                if (p.slot_group[s] == k && p.slot_token[s] == local) has = true;
-            if (!has) { g = k; break; }
-        }
-    }
-    if (g < 0) {
-        g = p.ngroups++;
-        hp.group_w[g] = w;
-        p.group_ntok[g] = 0;
-    }
-    const int s = p.nslots++;
-    p.slot_token[s] = local;
-    p.slot_group[s] = g;
-    p.slot_weight[s] = weight;
-    p.group_ntok[g] += 1;
-    if (p.group_ntok[g] > hp.max_group_tokens) hp.max_group_tokens = p.group_ntok[g];
-    p.tok_slots[local][p.tok_nslots[local]++] = s;
-    return true;
-}
-
 static bool same_offsets(const gw_expert_weights *a, const gw_expert_weights *b)
 {
     for (int s = 0; s < GW_SECTION_COUNT; ++s)
@@ -890,7 +832,7 @@ static int run_assignments(gw_expert_runner *r, const void *inputs, int x_dt,
     GW_CHECK(inputs && outputs, GW_ERR_ARG, "null pointer");
     GW_CHECK((reinterpret_cast<uintptr_t>(inputs) & 3u) == 0, GW_ERR_ARG,
              "inputs must be 4-byte aligned");
-    GW_CHECK(!r->ctx->capturing, GW_ERR_ARG, "host-planned calls cannot be captured");
+    GW_CHECK(!is_capturing(r->ctx), GW_ERR_ARG, "host-planned calls cannot be captured");
     for (int32_t i = 0; i < n; ++i) {
         int rc = check_weights(r, &a[i].weights);
         if (rc) return rc;
@@ -947,7 +889,7 @@ extern "C" int gw_expert_apply_batch(gw_expert_runner *r, const void *x, gw_dtyp
     GW_CHECK(count == 0 || (experts && routing_weights), GW_ERR_ARG, "null pointer");
     GW_CHECK(out, GW_ERR_ARG, "out is null");
     if (count == 0) {   // the reference returns zeros (ExpertRunner.swift:195)
-        GW_CHECK(!r->ctx->capturing, GW_ERR_ARG, "cannot capture");
+        GW_CHECK(!is_capturing(r->ctx), GW_ERR_ARG, "cannot capture");
         GW_HIP(hipMemsetAsync(out, 0, sizeof(float) * r->hidden, r->ctx->stream));
         GW_HIP(hipStreamSynchronize(r->ctx->stream));
         return GW_OK;
@@ -1008,7 +950,7 @@ static bool batch_takes_grouped_gemm(const gw_expert_runner *r, const gw_moe_lay
     if (a->expert_count < 1 || a->expert_count > 256 || !aligned16(a->x) ||
         !aligned16(a->experts_base) || a->expert_stride % 16)
         return false;
-    if (r->ctx->capturing &&
+    if (is_capturing(r->ctx) &&
         !(r->pf_buf && a->tokens <= r->pf_tokens && a->top_k <= r->pf_topk &&
           a->expert_count <= r->pf_experts))
         return false;
@@ -1178,7 +1120,7 @@ extern "C" int gw_expert_runner_reserve_prefill(gw_expert_runner *r, int32_t max
     if (r->pf_buf && max_tokens <= r->pf_tokens && top_k <= r->pf_topk &&
         expert_count <= r->pf_experts)
         return GW_OK;
-    GW_CHECK(!r->ctx->capturing, GW_ERR_ARG,
+    GW_CHECK(!is_capturing(r->ctx), GW_ERR_ARG,
              "prefill scratch must be reserved before graph capture");
     const int T = max_tokens > r->pf_tokens ? max_tokens : r->pf_tokens;
     const int K = top_k > r->pf_topk ? top_k : r->pf_topk;
@@ -1188,7 +1130,10 @@ extern "C" int gw_expert_runner_reserve_prefill(gw_expert_runner *r, int32_t max
     (void)hipFree(r->pf_buf);
     r->pf_buf = nullptr;
     r->pf_tokens = r->pf_topk = r->pf_experts = 0;
-    GW_HIP(hipMalloc(&r->pf_buf, bytes));
+    if (hipError_t e = hipMalloc(&r->pf_buf, bytes); e != hipSuccess) {
+        r->pf_buf = nullptr;
+        return alloc_failed(e, "prefill scratch hipMalloc", bytes);
+    }
     PrefillScratch ps;
     prefill_layout(r, T, K, E, static_cast<char *>(r->pf_buf), &ps);
     GW_HIP(hipMemsetAsync(ps.arrive, 0, sizeof(uint32_t) * (size_t)T * ((r->hidden + 255) / 256),

@@ -49,7 +49,6 @@ constexpr int kDW = kDT / 64;     // waves per workgroup
 constexpr int kDmaWaves = kDW;   // waves issuing the down stream's LDS-DMA
 constexpr int kChunk = 1024;      // bytes one wave-wide 16-byte LDS-DMA moves
 constexpr int kRsrcWord3 = 0x00020000;   // raw (untyped) buffer access
-constexpr int kSc1 = 16;                 // buffer cache policy: device-coherent (sc1)
 constexpr uint32_t kOutOfRange = 0x80000000u;   // buffer offset past any layer (reads zero)
 constexpr int kXWords = kDecodeXWords;   // exchange words per workgroup (3 activations each)
 constexpr unsigned kSpinLimit = 1u << 18;
@@ -144,7 +143,7 @@ template <int XK, class GS, int NSG, class DS, int NDMA>
 __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
 {
     constexpr int TPG = GS::TPR, MG = GS::M, SEGG = 64 / TPG, RGW = kDW * SEGG;
-    constexpr int TPD = DS::TPR, MD = DS::M, SEGD = 64 / TPD, RGD = kDW * SEGD;
+    constexpr int TPD = DS::TPR, MD = DS::M, SEGD = 64 / TPD;
     constexpr int BD = XL<XK>::kBlockDw;
     constexpr int BDA = XL<DT_F16>::kBlockDw;
     extern __shared__ __align__(16) uint32_t lds[];

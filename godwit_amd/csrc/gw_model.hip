@@ -21,169 +21,8 @@
 
 #include "../../include/godwit_hip.h"
 #include "gw_error.h"
+#include "gw_host.h"
 
-namespace {
-
-// ---------------------------------------------------------------------------
-// A small JSON reader: enough for manifest.json (objects, arrays, strings,
-// numbers, true/false/null; \uXXXX escapes kept as '?').
-// ---------------------------------------------------------------------------
-
-struct Json {
-    enum Kind { Null, Bool, Num, Str, Arr, Obj } kind = Null;
-    bool b = false;
-    double num = 0.0;
-    std::string str;
-    std::vector<Json> arr;
-    std::vector<std::pair<std::string, Json>> obj;
-
-    const Json *get(const char *key) const
-    {
-        if (kind != Obj) return nullptr;
-        for (const auto &kv : obj)
-            if (kv.first == key) return &kv.second;
-        return nullptr;
-    }
-};
-
-class JsonParser {
-  public:
-    JsonParser(const char *p, const char *end) : p_(p), end_(end) {}
-
-    bool parse(Json &out)
-    {
-        if (!value(out, 0)) return false;
-        ws();
-        return p_ == end_;
-    }
-    const char *where() const { return p_; }
-
-  private:
-    const char *p_, *end_;
-
-    void ws()
-    {
-        while (p_ < end_ && (*p_ == ' ' || *p_ == '\n' || *p_ == '\r' || *p_ == '\t')) ++p_;
-    }
-    bool lit(const char *s)
-    {
-        const size_t n = strlen(s);
-        if ((size_t)(end_ - p_) < n || strncmp(p_, s, n) != 0) return false;
-        p_ += n;
-        return true;
-    }
-    bool string(std::string &out)
-    {
-        if (p_ >= end_ || *p_ != '"') return false;
-        ++p_;
-        while (p_ < end_ && *p_ != '"') {
-            if (*p_ == '\\') {
-                if (++p_ >= end_) return false;
-                const char c = *p_++;
-                switch (c) {
-                case 'n': out += '\n'; break;
-                case 't': out += '\t'; break;
-                case 'r': out += '\r'; break;
-                case 'b': out += '\b'; break;
-                case 'f': out += '\f'; break;
-                case 'u':
-                    if (end_ - p_ < 4) return false;
-                    p_ += 4;
-                    out += '?';
-                    break;
-                default: out += c; break;   // \" \\ \/
-                }
-            } else {
-                out += *p_++;
-            }
-        }
-        if (p_ >= end_) return false;
-        ++p_;
-        return true;
-    }
-    bool value(Json &v, int depth)
-    {
-        if (depth > 64) return false;
-        ws();
-        if (p_ >= end_) return false;
-        const char c = *p_;
-        if (c == '{') {
-            v.kind = Json::Obj;
-            ++p_;
-            ws();
-            if (p_ < end_ && *p_ == '}') { ++p_; return true; }
-            for (;;) {
-                ws();
-                std::string key;
-                if (!string(key)) return false;
-                ws();
-                if (p_ >= end_ || *p_ != ':') return false;
-                ++p_;
-                Json child;
-                if (!value(child, depth + 1)) return false;
-                v.obj.emplace_back(std::move(key), std::move(child));
-                ws();
-                if (p_ < end_ && *p_ == ',') { ++p_; continue; }
-                if (p_ < end_ && *p_ == '}') { ++p_; return true; }
-                return false;
-            }
-        }
-        if (c == '[') {
-            v.kind = Json::Arr;
-            ++p_;
-            ws();
-            if (p_ < end_ && *p_ == ']') { ++p_; return true; }
-            for (;;) {
-                Json child;
-                if (!value(child, depth + 1)) return false;
-                v.arr.push_back(std::move(child));
-                ws();
-                if (p_ < end_ && *p_ == ',') { ++p_; continue; }
-                if (p_ < end_ && *p_ == ']') { ++p_; return true; }
-                return false;
-            }
-        }
-        if (c == '"') { v.kind = Json::Str; return string(v.str); }
-        if (lit("true")) { v.kind = Json::Bool; v.b = true; return true; }
-        if (lit("false")) { v.kind = Json::Bool; v.b = false; return true; }
-        if (lit("null")) { v.kind = Json::Null; return true; }
-        char *stop = nullptr;
-        const std::string tok(p_, (size_t)std::min<ptrdiff_t>(end_ - p_, 64));
-        v.num = strtod(tok.c_str(), &stop);
-        if (stop == tok.c_str()) return false;
-        v.kind = Json::Num;
-        p_ += stop - tok.c_str();
-        return true;
-    }
-};
-
-const char *const kSectionNames[GW_SECTION_COUNT] = {"gate_up_blocks", "gate_up_scales",
-                                                     "down_blocks",    "down_scales",
-                                                     "gate_up_bias",   "down_bias"};
-
-bool number_of(const Json &o, const char *key, double &out)
-{
-    const Json *v = o.get(key);
-    if (!v || v->kind != Json::Num) return false;
-    out = v->num;
-    return true;
-}
-
-bool integer_of(const Json &o, const char *key, int64_t &out)
-{
-    double d;
-    if (!number_of(o, key, d) || d != std::floor(d) || d < 0 || d > 9.0e15) return false;
-    out = (int64_t)d;
-    return true;
-}
-
-bool bool_or(const Json &o, const char *key, bool dflt)
-{
-    const Json *v = o.get(key);
-    return v && v->kind == Json::Bool ? v->b : dflt;
-}
-
-}  // namespace
 
 struct gw_model {
     std::string dir;
@@ -201,73 +40,6 @@ static std::string layer_path(const gw_model *m, int layer)
     char name[32];
     snprintf(name, sizeof(name), "layer_%02d.bin", layer);
     return m->dir + "/experts/" + name;
-}
-
-// Parses manifest.json (GodwitManifest, decoded as ModelReader.init does,
-// ModelReader.swift:17-37): format version 2, layer/expert counts, the expert
-// stride and sections, and the spec fields the MoE path needs (with the
-// decoder's defaults for fields older installs lack, ArchitectureSpec.swift:
-// 176-205).
-static int parse_manifest(const std::string &text, gw_model_info &info)
-{
-    Json root;
-    JsonParser parser(text.data(), text.data() + text.size());
-    if (!parser.parse(root) || root.kind != Json::Obj)
-        return gw::set_error(GW_ERR_ARG, "manifest.json is not valid JSON (near byte %ld)",
-                             (long)(parser.where() - text.data()));
-    memset(&info, 0, sizeof(info));
-    if (!integer_of(root, "formatVersion", info.format_version))
-        return gw::set_error(GW_ERR_ARG, "manifest.json has no formatVersion");
-    if (info.format_version != GW_GWT_FORMAT_VERSION)
-        return gw::set_error(GW_ERR_ARG, "format v%lld, runtime expects v%d",
-                             (long long)info.format_version, GW_GWT_FORMAT_VERSION);
-    if (!integer_of(root, "layerCount", info.layer_count) ||
-        !integer_of(root, "expertCount", info.expert_count) ||
-        !integer_of(root, "expertStride", info.expert_stride) || info.expert_stride <= 0)
-        return gw::set_error(GW_ERR_ARG,
-                             "manifest.json lacks layerCount, expertCount or expertStride");
-    const Json *secs = root.get("expertSections");
-    if (!secs || secs->kind != Json::Obj)
-        return gw::set_error(GW_ERR_ARG, "manifest.json has no expertSections");
-    for (int s = 0; s < GW_SECTION_COUNT; ++s) {
-        const Json *span = secs->get(kSectionNames[s]);
-        if (!span || !integer_of(*span, "offset", info.section_offset[s]) ||
-            !integer_of(*span, "length", info.section_length[s]))
-            return gw::set_error(GW_ERR_ARG, "manifest has no section '%s'", kSectionNames[s]);
-        if (info.section_offset[s] + info.section_length[s] > info.expert_stride)
-            return gw::set_error(GW_ERR_ARG, "section '%s' ends past the expert stride",
-                                 kSectionNames[s]);
-    }
-    const Json *spec = root.get("spec");
-    if (!spec || spec->kind != Json::Obj)
-        return gw::set_error(GW_ERR_ARG, "manifest.json has no spec");
-    double eps = 0.0;
-    if (!integer_of(*spec, "hiddenSize", info.hidden_size) ||
-        !integer_of(*spec, "intermediateSize", info.intermediate_size) ||
-        !number_of(*spec, "rmsNormEpsilon", eps))
-        return gw::set_error(GW_ERR_ARG, "spec lacks hiddenSize, intermediateSize or rmsNormEpsilon");
-    info.rms_norm_epsilon = (float)eps;
-    const Json *act = spec->get("activation");
-    if (!act || act->kind != Json::Str)
-        return gw::set_error(GW_ERR_ARG, "spec has no activation");
-    if (act->str == "gptOssClampedGLU") info.activation = GW_ACT_GPTOSS_CLAMPED_GLU;
-    else if (act->str == "silu") info.activation = GW_ACT_SILU;
-    else return gw::set_error(GW_ERR_SHAPE, "expert activation '%s' is not supported", act->str.c_str());
-    double lim = 7.0, alpha = 1.702;
-    number_of(*spec, "activationLimit", lim);
-    number_of(*spec, "activationAlpha", alpha);
-    info.activation_limit = (float)lim;
-    info.activation_alpha = (float)alpha;
-    info.expert_bias = bool_or(*spec, "expertBias", false) ? 1 : 0;
-    info.router_bias = bool_or(*spec, "routerBias", false) ? 1 : 0;
-    info.experts_per_token = 0;
-    if (const Json *layers = spec->get("layers"); layers && layers->kind == Json::Arr)
-        for (const Json &l : layers->arr) {
-            int64_t k = 0;
-            if (integer_of(l, "expertsPerToken", k) && k > info.experts_per_token)
-                info.experts_per_token = k;
-        }
-    return GW_OK;
 }
 
 extern "C" int gw_model_open(const char *directory, gw_model **out)
@@ -293,7 +65,7 @@ extern "C" int gw_model_open(const char *directory, gw_model **out)
     fclose(f);
     gw_model *m = new gw_model;
     m->dir = dir;
-    const int rc = parse_manifest(text, m->info);
+    const int rc = gw::parse_manifest(text, m->info);
     if (rc != GW_OK) {
         delete m;
         return rc;

@@ -97,6 +97,8 @@ int gw_free(gw_context *ctx, void *ptr);
 int gw_memcpy_htod(gw_context *ctx, void *dst, const void *src, size_t bytes);
 int gw_memcpy_dtoh(gw_context *ctx, void *dst, const void *src, size_t bytes);
 int gw_memcpy_dtod(gw_context *ctx, void *dst, const void *src, size_t bytes);
+/* Blocking zero fill; GW_ERR_ARG while the context's stream is being captured
+ * (a memset node would be recorded). */
 int gw_memset_zero(gw_context *ctx, void *dst, size_t bytes);
 /* Enqueue-only device-to-device copy on the context stream (no wait). */
 int gw_memcpy_dtod_async(gw_context *ctx, void *dst, const void *src, size_t bytes);
@@ -205,7 +207,11 @@ typedef struct gw_expert_runner gw_expert_runner;
 /* ExpertRunner.init(context:reader:swigluLimit:swigluAlpha:) (:37-47).
  * limit/alpha are the model's activationLimit/activationAlpha (7.0 / 1.702 for
  * GPT-OSS, ArchitectureSpec.swift:102-104).  Bias sections are bf16 as written
- * by the installer; gw_expert_runner_set_bias_dtype switches to f32 sections. */
+ * by the installer; gw_expert_runner_set_bias_dtype switches to f32 sections,
+ * and returns GW_ERR_SHAPE where the layout's bias pages cannot hold fp32
+ * values (a gate_up bias of 2 x intermediate fp32 values must end before the
+ * down bias section, the down bias before the expert stride: GPT-OSS's 5760
+ * gate_up biases do not fit). */
 int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size, int64_t intermediate_size,
                             gw_activation activation, float swiglu_limit, float swiglu_alpha,
                             gw_expert_runner **out);

@@ -14,7 +14,7 @@
  * Pinning (what checks each function independently of this file):
  *   codec            known answers of Tests/GodwitTests/MXFP4Tests.swift and
  *                    MXFP4EncodeTests.swift, plus an exhaustive 16x256 table
- *                    built from the closed form with numpy (tests/test_oracle_codec.py)
+ *                    built from the closed form with numpy (tests/test_oracle.py:59-77)
  *   f16 / bf16       numpy's float16 cast (RNE) and the bit identities of
  *                    Int8Affine.swift:86-93
  *   GEMV             DequantGEMVTests.swift:64-77 hand case, fp64 brute force
