@@ -281,7 +281,7 @@ def gptoss20b_bench(gw, args) -> int:
         for _ in range(args.steps):
             step()
         ctx.synchronize()
-        for name in ("router", "gate_up", "down"):
+        for name in ("router", "moe_layer", "gate_up", "down"):
             ms, n = ctx.profile(name)
             if n:
                 kernels[name] = {"launches": n, "avg_us": ms / n * 1e3}
@@ -292,7 +292,14 @@ def gptoss20b_bench(gw, args) -> int:
     log(f"gpt-oss-20b layer: {dt * 1e6:.2f} us per layer, {value:.0f} GB/s "
         f"({value / PEAK_HBM_GBS * 100:.1f}% of {PEAK_HBM_GBS:.0f})")
     roof = None
-    if "gate_up" in kernels:
+    if "moe_layer" in kernels:
+        lb = K * expert_bytes(lay) + E20 * 4 + H * 2 + H * 4 + H * 2
+        ach = lb / (kernels["moe_layer"]["avg_us"] * 1e-6) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": "decode_layer_kernel (route + gate_up + SwiGLU + down + combine)",
+                "bytes_per_launch": lb, "avg_launch_us": round(kernels["moe_layer"]["avg_us"], 3)}
+    elif "gate_up" in kernels:
         ach = gate_up_bytes(lay) / (kernels["gate_up"]["avg_us"] * 1e-6) / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
@@ -575,8 +582,8 @@ def qwen3_bench(gw, args, batch: int) -> int:
                            step_logits)
             token()
         ctx.synchronize()
-        for name in ("gate_up", "down", "prefill_route", "prefill_group", "prefill_gate_up",
-                     "prefill_down", "prefill_combine"):
+        for name in ("moe_layer", "gate_up", "down", "prefill_route", "prefill_group",
+                     "prefill_gate_up", "prefill_down", "prefill_combine"):
             ms, n = ctx.profile(name)
             if n:
                 kernels[name] = {"launches": n, "avg_us": ms / n * 1e3}
@@ -585,7 +592,15 @@ def qwen3_bench(gw, args, batch: int) -> int:
                                     for k, v in kernels.items()))
     roof = None
     gu = "gate_up" if "gate_up" in kernels else "prefill_gate_up"
-    if gu in kernels:
+    if "moe_layer" in kernels:
+        lb = (float(np.mean(uniq)) / Lq) * per_expert + batch * (Eq * 4 + Hq * 2 + Hq * 4 + Hq * 2)
+        ach = lb / (kernels["moe_layer"]["avg_us"] * 1e-6) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": "decode_layer_kernel (route + gate_up + SiLU-GLU + down + combine)",
+                "bytes_per_launch": int(lb),
+                "avg_launch_us": round(kernels["moe_layer"]["avg_us"], 3)}
+    elif gu in kernels:
         gu_bytes = (float(np.mean(uniq)) / Lq) * (lay.sizes["gate_up_blocks"] +
                                                   lay.sizes["gate_up_scales"] +
                                                   lay.sizes["gate_up_bias"])

@@ -10,19 +10,20 @@
 // At batch 1 the layer is two dependent streams of weights: k experts' gate_up
 // rows (4 x 8.8 MB for GPT-OSS), then their down rows (4 x 4.4 MB), which
 // need every activation of their expert.  The down rows' addresses are known
-// as soon as the routing is, so a workgroup issues its whole share of both
-// right after routing: its gate_up rows into a ring of registers (consumed as
-// they land) and, behind them, its down rows with their scales and biases
-// straight into LDS by buffer LDS-DMA (no registers held).  Loads of a wave
-// complete in issue order, so the gate_up rows land first; the activations
-// are exchanged across the grid while the down rows are still streaming in,
-// and the down products are computed from LDS once both are there.  The two
-// streams thus share one ramp, and the exchange waits behind the down stream
-// instead of adding to it.
+// as soon as the routing is.  Each SIMD runs one gate_up wave and one DMA
+// wave: the gate_up waves stream their rows through a ring of register stages
+// and widen and dot them as they land; the DMA waves, released once the last
+// gate_up stage is queued, copy the workgroup's down rows with their scales
+// and biases straight into LDS by buffer LDS-DMA (no registers held).  A SIMD
+// lets its older wave issue first, so the gate_up rows are queued ahead of
+// the down stream.  The activations are exchanged across the grid while the
+// down rows are still streaming in, and the down products are computed from
+// LDS once both are there.
 //
 // The exchange: a workgroup stores its activations with their launch tag in
-// 8-byte words (device-coherent stores, no wait); every workgroup polls all
-// words until each carries the current tag (a bounded spin: a wait that gives
+// 8-byte words (device-coherent stores, no wait); the gate_up waves of every
+// workgroup, which hold no down stream of their own, poll all words until
+// each carries the current tag (a bounded spin: a wait that gives
 // up sets an error word, read by gw_expert_runner_sync_errors, so no
 // workgroup ever waits unboundedly) and stages the activations in LDS.  The
 // grid must be co-resident (one workgroup per CU; the host checks occupancy).
@@ -46,11 +47,16 @@ namespace {
 
 constexpr int kDT = 512;          // threads per workgroup
 constexpr int kDW = kDT / 64;     // waves per workgroup
-constexpr int kDmaWaves = kDW;   // waves issuing the down stream's LDS-DMA
+// Waves 0..kGuWaves-1 (one per SIMD) stream and compute the gate_up rows and
+// then poll the exchange; the others issue the down stream's LDS-DMA.
+constexpr int kGuWaves = 4;
+constexpr int kDmaWaves = kDW - kGuWaves;
 constexpr int kChunk = 1024;      // bytes one wave-wide 16-byte LDS-DMA moves
 constexpr int kRsrcWord3 = 0x00020000;   // raw (untyped) buffer access
+constexpr int kNt = 2;                   // buffer cache policy: non-temporal (streamed once)
 constexpr uint32_t kOutOfRange = 0x80000000u;   // buffer offset past any layer (reads zero)
-constexpr int kXWords = kDecodeXWords;   // exchange words per workgroup (3 activations each)
+constexpr int kXWords = 16;              // exchange words per workgroup (3 activations each)
+static_assert(kDecodeMaxGrid * kXWords * 8 <= kDecodeXchgBytes, "exchange buffer");
 constexpr unsigned kSpinLimit = 1u << 18;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -72,8 +78,8 @@ __host__ __device__ inline DecodeLds decode_lds(int hidden, int inter, int top_k
 {
     DecodeLds l;
     const int hb = hidden / 32, fb = inter / 32;
-    l.route = 0;                                   // int32 ids[8], float w[8]
-    l.xs = 64;                                     // x, 20 dwords per block
+    l.route = 0;                                   // int32 ids[8], float w[8], done count
+    l.xs = 128;                                    // x, 20 dwords per block
     l.actl = l.xs + hb * 80;                       // this workgroup's fp16 activations
     l.dma = (l.actl + rows_per_wg + 255) & ~255;   // the down stream (+ one spare chunk)
     const int dma_bytes = (top_k * sw_total + kChunk - 1) / kChunk * kChunk + kChunk;
@@ -142,7 +148,7 @@ template <int TPR> __device__ __forceinline__ float next_segment(float v)
 template <int XK, class GS, int NSG, class DS, int NDMA>
 __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
 {
-    constexpr int TPG = GS::TPR, MG = GS::M, SEGG = 64 / TPG, RGW = kDW * SEGG;
+    constexpr int TPG = GS::TPR, MG = GS::M, SEGG = 64 / TPG, RGW = kGuWaves * SEGG;
     constexpr int TPD = DS::TPR, MD = DS::M, SEGD = 64 / TPD;
     constexpr int BD = XL<XK>::kBlockDw;
     constexpr int BDA = XL<DT_F16>::kBlockDw;
@@ -165,6 +171,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     const DecodeLds L = decode_lds(H, F, K, a.nrmax, swt, RGW * NSG);
     int32_t *eid = reinterpret_cast<int32_t *>(lds8 + L.route);
     float *ew = reinterpret_cast<float *>(lds8 + L.route + 32);
+    unsigned *gu_done = reinterpret_cast<unsigned *>(lds8 + L.route + 64);   // gate_up waves done
     uint32_t *xs = reinterpret_cast<uint32_t *>(lds8 + L.xs);
     uint16_t *actl = reinterpret_cast<uint16_t *>(lds8 + L.actl);
     uint32_t *as = reinterpret_cast<uint32_t *>(lds8 + L.as);
@@ -174,6 +181,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
 
     // ---- 1. route (wave 0) while waves 1.. stage x -------------------------
     if (wave == 0) {
+        if (lane == 0) *gu_done = 0u;
         int sid;
         float w;
         if (a.experts <= 128) select_one<2>(a.logits, a.experts, K, sid, w);
@@ -190,153 +198,176 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     __syncthreads();
 
     const int segg = lane / TPG, tlg = lane % TPG;
-
-    // ---- 3. issue: every gate_up stage, then (waves 1..) the down stream ----
     const int nrows = 2 * (p1 - p0);
     const int two_f = 2 * F;
     const float inv_two_f = 1.0f / (float)two_f;
     const int64_t rbg = (int64_t)hb * 16;
-    u32x4 W[NSG][MG];
-    uint32_t SC[NSG][MG];
-    uint32_t BW[NSG];
-    int BSH[NSG];
-#pragma unroll
-    for (int s = 0; s < NSG; ++s) {
-        const int i = s * RGW + wave * SEGG + segg;
-        const int rg = 2 * p0 + (i < nrows ? i : 0);
-        int k, r;
-        divmod_small(rg, two_f, inv_two_f, k, r);
-        const uint8_t *ebase = a.base + (int64_t)eid[k] * a.stride;
-        const uint8_t *row = ebase + a.sec.gu_blocks + r * rbg;
-        const uint8_t *srow = ebase + a.sec.gu_scales + (int64_t)r * hb;
-#pragma unroll
-        for (int m = 0; m < MG; ++m) {
-            const int cb = min(tlg + m * TPG, hb - 1);
-            W[s][m] = __builtin_nontemporal_load((g_u32x4 *)row + cb);
-            SC[s][m] = ((g_u8 *)srow)[cb];
-        }
-        const uintptr_t ba = a.bias_dt >= 0
-                                 ? reinterpret_cast<uintptr_t>(ebase + a.sec.gu_bias + (int64_t)r * bsz)
-                                 : reinterpret_cast<uintptr_t>(srow);
-        BSH[s] = (int)(ba & 2u) * 8;
-        BW[s] = *(g_u32 *)(ba & ~(uintptr_t)3);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // The down stream's DMA pieces, issued just before the last gate_up stage
-    // is consumed: the earlier gate_up loads are in by then and the rest are
-    // queued, so every gate_up row lands ahead of the down stream and the
-    // exchange can complete while the down rows are still arriving.  Piece c
-    // of wave w is packed position (w + kDmaWaves*c) KiB of the per-expert
-    // windows [rows | scale bytes | biases] x top_k.  Every wave issues NDMA
-    // pieces (those past the end read zeros into the spare chunk without a
-    // memory access), so the compiler's load counts are the same on every
-    // path.  The pieces' experts are read from LDS before the first of them
-    // is issued (the compiler makes any LDS read after an LDS-DMA wait for
-    // every load in flight).
-    // This lane's activation blocks into registers, read with ds_read_b128
-    // written out: the compiler would make an LDS read after the LDS-DMA wait
-    // for every load in flight; x was stored before the barrier above.
-    uint4 X[MG][4];
-    {
-        const uint32_t xa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)xs;
-        u32x4 xv[MG][4];
-#pragma unroll
-        for (int m = 0; m < MG; ++m) {
-            const int cb = tlg + m * TPG;
-            const uint32_t addr = xa + (uint32_t)((cb < hb ? cb : 0) * BD * 4);
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(xv[m][q]) : "v"(addr), "i"(q * 16));
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int m = 0; m < MG; ++m)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                u32x4 v = xv[m][q];
-                asm volatile("" : "+v"(v));
-                X[m][q] = make_uint4(v.x, v.y, v.z, v.w);
-            }
-    }
+    const __amdgpu_buffer_rsrc_t lr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(a.base), (short)0, (int)a.base_bytes, kRsrcWord3);
 
-    // ---- 4. gate_up: consume the stages as they land -----------------------
-    static_assert(NSG >= 2, "the down stream is issued before the last gate_up stage");
-#pragma unroll
-    for (int s = 0; s < NSG; ++s) {
-        if (s == NSG - 1) {
-            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint8_t *>(a.base), (short)0, (int)a.base_bytes, kRsrcWord3);
-            const int total = K * swt;
-            const int nchunks = (total + kChunk - 1) / kChunk;
-            const int rbd = fb * 16;
-            const int s0 = r0 * fb, b0 = r0 * bsz;
-            const int s0a = s0 & ~15, b0a = b0 & ~15;
-            const int lim_w = nr * rbd, lim_s = (s0 - s0a) + nr * fb;
-            const int lim_b = a.bias_dt >= 0 ? (b0 - b0a) + nr * bsz : 0;
-            const uint32_t rel_w = (uint32_t)(a.sec.dn_blocks + (int64_t)r0 * rbd);
-            const uint32_t rel_s = (uint32_t)(a.sec.dn_scales + s0a) - (uint32_t)sww;
-            const uint32_t rel_b = (uint32_t)(a.sec.dn_bias + b0a) - (uint32_t)(sww + sws);
-            const float inv_swt = 1.0f / (float)swt;
-            uint32_t eo_c[NDMA];
-#pragma unroll
-            for (int c = 0; c < NDMA; ++c) {
-                const int pos = (wave + kDmaWaves * c) * kChunk + lane * 16;
-                int k, o;
-                divmod_small(pos, swt, inv_swt, k, o);
-                eo_c[c] = (uint32_t)eid[min(k, K - 1)] * (uint32_t)a.stride;
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int c = 0; c < NDMA; ++c) {
-                const int chunk = wave + kDmaWaves * c;
-                const int pos = chunk * kChunk + lane * 16;
-                int k, o;
-                divmod_small(pos, swt, inv_swt, k, o);
-                const bool is_w = o < sww, is_s = !is_w && o < sww + sws;
-                const int lim = is_w ? lim_w : is_s ? lim_s + sww : lim_b + sww + sws;
-                const uint32_t rel = is_w ? rel_w : is_s ? rel_s : rel_b;
-                const bool ok = pos < total && o < lim;
-                const uint32_t voff = ok ? eo_c[c] + rel + (uint32_t)o : kOutOfRange;
-                uint8_t *dst = lds8 + L.dma + (chunk < nchunks ? chunk : nchunks) * kChunk;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (l_void *)dst, 16, voff, 0, 0, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        const int i = s * RGW + wave * SEGG + segg;
-        const bool valid = i < nrows;
-        float acc = 0.0f;
-#pragma unroll
-        for (int m = 0; m < MG; ++m) {
-            const int cb = tlg + m * TPG;
-            const bool use = valid && cb < hb;
-            WBlock<XK> wb;
-            widen_v(W[s][m], wb);
-            const float d = block_dot_r<XK>(wb, X[m]) * decode_scale(SC[s][m]);
-            acc += use ? d : 0.0f;
-        }
-        acc = seg_sum<TPG>(acc);
-        const float up = next_segment<TPG>(acc);
-        const float b_own = bias_of(BW[s], BSH[s], a.bias_dt);
-        const float b_next = next_segment<TPG>(b_own);
-        if (valid && (segg & 1) == 0 && tlg == 0) {
-            const float v = apply_activation(a.act_kind, acc + b_own, up + b_next, a.limit, a.alpha);
-            actl[i >> 1] = f32_to_f16_bits(v);
-        }
+    if (wave >= kGuWaves) {
+        // ---- 3a. the down stream (waves kGuWaves..): the workgroup's down
+        // rows, their scale bytes and biases straight into LDS by LDS-DMA.
+        // Piece c of DMA wave d is packed position (d + kDmaWaves*c) KiB of
+        // the per-expert windows [rows | scale bytes | biases] x top_k; pieces
+        // past the end read zeros into the spare chunk without a memory
+        // access.  These waves share each SIMD with a gate_up wave, which
+        // takes precedence in issuing, so the gate_up rows are queued first.
+        const int d = wave - kGuWaves;
+        const int total = K * swt;
+        const int nchunks = (total + kChunk - 1) / kChunk;
+        const int rbd = fb * 16;
+        const int s0 = r0 * fb, b0 = r0 * bsz;
+        const int s0a = s0 & ~15, b0a = b0 & ~15;
+        const int lim_w = nr * rbd, lim_s = (s0 - s0a) + nr * fb;
+        const int lim_b = a.bias_dt >= 0 ? (b0 - b0a) + nr * bsz : 0;
+        const uint32_t rel_w = (uint32_t)(a.sec.dn_blocks + (int64_t)r0 * rbd);
+        const uint32_t rel_s = (uint32_t)(a.sec.dn_scales + s0a) - (uint32_t)sww;
+        const uint32_t rel_b = (uint32_t)(a.sec.dn_bias + b0a) - (uint32_t)(sww + sws);
+        const float inv_swt = 1.0f / (float)swt;
+        // Wait until the gate_up waves have queued their last stage.
         __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < NDMA; ++c) {
+            const int chunk = d + kDmaWaves * c;
+            const int pos = chunk * kChunk + lane * 16;
+            int k, o;
+            divmod_small(pos, swt, inv_swt, k, o);
+            const uint32_t eo = (uint32_t)eid[min(k, K - 1)] * (uint32_t)a.stride;
+            const bool is_w = o < sww, is_s = !is_w && o < sww + sws;
+            const int lim = is_w ? lim_w : is_s ? lim_s + sww : lim_b + sww + sws;
+            const uint32_t rel = is_w ? rel_w : is_s ? rel_s : rel_b;
+            const bool ok = pos < total && o < lim;
+            const uint32_t voff = ok ? eo + rel + (uint32_t)o : kOutOfRange;
+            uint8_t *dst = lds8 + L.dma + (chunk < nchunks ? chunk : nchunks) * kChunk;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(lr, (l_void *)dst, 16, voff, 0, 0, 0);
+        }
+    } else {
+        // ---- 3b. gate_up (waves 0..kGuWaves-1, one per SIMD): RGW rows a
+        // stage, a ring of D stages in flight (stage s + D issued once stage s
+        // is consumed), widened and dotted as they land.  Rows past the share
+        // read zeros without a memory access (buffer loads over the layer).
+        constexpr int D = NSG < 2 ? NSG : 2;
+        u32x4 W[D][MG];
+        uint32_t SC[D][MG];
+        uint32_t BW[D];
+        int BSH[D];
+#define GW_ISSUE_STAGE(S)                                                                       \
+    do {                                                                                        \
+        constexpr int q_ = (S) % D;                                                             \
+        const int i_ = (S) * RGW + wave * SEGG + segg;                                          \
+        const bool live_ = i_ < nrows;                                                          \
+        int k_, r_;                                                                             \
+        divmod_small(2 * p0 + (live_ ? i_ : 0), two_f, inv_two_f, k_, r_);                     \
+        const uint32_t eo_ = (uint32_t)eid[k_] * (uint32_t)a.stride;                            \
+        const uint32_t row_ = eo_ + (uint32_t)a.sec.gu_blocks + (uint32_t)(r_ * rbg);           \
+        const uint32_t srow_ = eo_ + (uint32_t)a.sec.gu_scales + (uint32_t)(r_ * hb);           \
+        _Pragma("unroll") for (int m_ = 0; m_ < MG; ++m_) {                                     \
+            const int cb_ = min(tlg + m_ * TPG, hb - 1);                                        \
+            W[q_][m_] = __builtin_bit_cast(                                                     \
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(                                   \
+                           lr, live_ ? row_ + (uint32_t)cb_ * 16 : kOutOfRange, 0, kNt));       \
+            SC[q_][m_] = __builtin_amdgcn_raw_buffer_load_b8(                                   \
+                lr, live_ ? srow_ + (uint32_t)cb_ : kOutOfRange, 0, 0);                         \
+        }                                                                                       \
+        const uint32_t ba_ = a.bias_dt >= 0                                                     \
+                                 ? eo_ + (uint32_t)a.sec.gu_bias + (uint32_t)(r_ * bsz)         \
+                                 : srow_;                                                       \
+        BSH[q_] = (int)(ba_ & 2u) * 8;                                                          \
+        BW[q_] = __builtin_amdgcn_raw_buffer_load_b32(lr, live_ ? (ba_ & ~3u) : kOutOfRange,   \
+                                                      0, 0);                                    \
+    } while (0)
+        Unroll<0, D>::run([&](auto sc) { GW_ISSUE_STAGE(decltype(sc)::value); });
+        // This lane's activation blocks into registers, read with ds_read_b128
+        // written out: the compiler would make an LDS read after an LDS-DMA
+        // wait for every load in flight; x was stored before the barrier above.
+        uint4 X[MG][4];
+        {
+            const uint32_t xa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)xs;
+            u32x4 xv[MG][4];
+#pragma unroll
+            for (int m = 0; m < MG; ++m) {
+                const int cb = tlg + m * TPG;
+                const uint32_t addr = xa + (uint32_t)((cb < hb ? cb : 0) * BD * 4);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(xv[m][q]) : "v"(addr), "i"(q * 16));
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int m = 0; m < MG; ++m)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    u32x4 v = xv[m][q];
+                    asm volatile("" : "+v"(v));
+                    X[m][q] = make_uint4(v.x, v.y, v.z, v.w);
+                }
+        }
+        Unroll<0, NSG>::run([&](auto sc) {
+            constexpr int s = decltype(sc)::value, q = s % D;
+            const int i = s * RGW + wave * SEGG + segg;
+            const bool valid = i < nrows;
+            float acc = 0.0f;
+#pragma unroll
+            for (int m = 0; m < MG; ++m) {
+                const int cb = tlg + m * TPG;
+                const bool use = valid && cb < hb;
+                WBlock<XK> wb;
+                widen_v(W[q][m], wb);
+                float dd = block_dot_r<XK>(wb, X[m]);
+                dd *= decode_scale(SC[q][m]);
+                acc += use ? dd : 0.0f;
+            }
+            acc = seg_sum<TPG>(acc);
+            const float up = next_segment<TPG>(acc);
+            const float b_own = bias_of(BW[q], BSH[q], a.bias_dt);
+            const float b_next = next_segment<TPG>(b_own);
+            if (valid && (segg & 1) == 0 && tlg == 0) {
+                const float v = apply_activation(a.act_kind, acc + b_own, up + b_next, a.limit,
+                                                 a.alpha);
+                actl[i >> 1] = f32_to_f16_bits(v);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (s + D < NSG) {
+                GW_ISSUE_STAGE(s + D);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (s == (NSG > D ? NSG - 1 - D : 0)) {
+                // the last stage is queued (or all were up front): the DMA
+                // waves may queue the down stream behind it
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        });
+#undef GW_ISSUE_STAGE
     }
-    // A bare barrier: __syncthreads' fence would wait for the down stream too.
-    // Only this workgroup's LDS writes (the activations) must be visible.
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
+    // The gate_up waves count themselves done in LDS (their activations are
+    // written first); the publishing wave waits for the count instead of a
+    // barrier, which would also wait for the DMA waves still queuing the
+    // down stream.
+    if (wave < kGuWaves) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane == 0) __hip_atomic_fetch_add(gu_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (wave == 0) {
+            while (__hip_atomic_load(gu_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
+                   (unsigned)kGuWaves)
+                __builtin_amdgcn_s_sleep(1);
+        }
+    }
 
     // ---- 5. exchange ---------------------------------------------------------
     // Workgroup b publishes its activations as kXWords 8-byte words, three
     // fp16 values and the 16-bit launch tag each, with device-coherent stores;
     // an aligned 8-byte store is seen whole or not at all, so the tag marks
-    // the word valid and no separate flag, wait or counter is needed.  Every
-    // workgroup then reads all words, keeping those carrying this launch's
-    // tag and polling the rest (a bounded spin), and places the activations
-    // in LDS.  Every workgroup completes every launch, so all agree on the tag.
+    // the word valid and no separate flag, wait or counter is needed.  The
+    // gate_up waves (no down stream of their own, so their loads are not
+    // queued behind it) then read all words, keeping those carrying this
+    // launch's tag and polling the rest (a bounded spin), and place the
+    // activations in LDS while the down stream still lands; the DMA waves
+    // wait for their part of it.  Every workgroup completes every launch, so
+    // all agree on the tag.
     const int G = gridDim.x;
     const int npair = K * F;
     const unsigned pq = (unsigned)npair / (unsigned)G, pr = (unsigned)npair - pq * (unsigned)G;
@@ -351,14 +382,17 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         }
         __hip_atomic_store(xw + b * kXWords + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_s_waitcnt(0);                // this wave's part of the down stream is in LDS
-    {
-        constexpr int WPT = 8;                    // words per thread (G * kXWords <= WPT * kDT)
-        const float inv_f = 1.0f / (float)F;
+    if (wave >= kGuWaves) {
+        __builtin_amdgcn_s_waitcnt(0);            // this wave's part of the down stream is in LDS
+    } else {
+        constexpr int kPollT = kGuWaves * 64;
+        constexpr int WPT = kDecodeMaxGrid * kXWords / kPollT;   // words per thread
+        static_assert(WPT <= 32, "pending mask");
+        const int t = (int)threadIdx.x;
         uint32_t pending = 0;
 #pragma unroll
         for (int u = 0; u < WPT; ++u) {
-            const int idx = (int)threadIdx.x + u * kDT;
+            const int idx = t + u * kPollT;
             const int pb = idx / kXWords, j = idx % kXWords;
             const int np = (int)pq + (pb < (int)pr ? 1 : 0);
             if (pb < G && 3 * j < np) pending |= 1u << u;
@@ -369,23 +403,24 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
 #pragma unroll
             for (int u = 0; u < WPT; ++u)
                 v[u] = (pending >> u) & 1u
-                           ? __hip_atomic_load(xw + (int)threadIdx.x + u * kDT, __ATOMIC_RELAXED,
+                           ? __hip_atomic_load(xw + t + u * kPollT, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT)
                            : 0ull;
 #pragma unroll
             for (int u = 0; u < WPT; ++u) {
                 if (((pending >> u) & 1u) && (v[u] >> 48) == tag) {
                     pending &= ~(1u << u);
-                    const int idx = (int)threadIdx.x + u * kDT;
+                    const int idx = t + u * kPollT;
                     const int pb = idx / kXWords, j = idx % kXWords;
                     const int np = (int)pq + (pb < (int)pr ? 1 : 0);
                     const int pbase = pb * (int)pq + min(pb, (int)pr);
 #pragma unroll
                     for (int e = 0; e < 3; ++e) {
                         if (3 * j + e < np) {
-                            int k, f;
-                            divmod_small(pbase + 3 * j + e, F, inv_f, k, f);
-                            reinterpret_cast<uint16_t *>(as + k * fb * BDA + (f >> 5) * BDA)[f & 31] =
+                            // pair p = k * F + f sits in block p / 32 of the
+                            // expert-major block layout, element p % 32
+                            const int pp = pbase + 3 * j + e;
+                            reinterpret_cast<uint16_t *>(as + (pp >> 5) * BDA)[pp & 31] =
                                 (uint16_t)(v[u] >> (16 * e));
                         }
                     }
@@ -487,9 +522,9 @@ namespace {
 // top-4: 90 gate_up rows a workgroup on 256 CUs, three 32-row stages) and
 // Qwen3-30B-A3B (2048 / 768: 64- and 24-block rows, up to top-8).
 enum { kShapeGptOss = 0, kShapeQwen3 = 1 };
-constexpr int kNdma[2] = {10, 5};
-constexpr int kStagesG[2] = {3, 2};
-constexpr int kRowsPerStage[2] = {kDW * 64 / 16, kDW * 64 / 16};
+constexpr int kNdma[2] = {20, 10};   // 1 KiB pieces per DMA wave
+constexpr int kStagesG[2] = {6, 3};
+constexpr int kRowsPerStage[2] = {kGuWaves * 64 / 16, kGuWaves * 64 / 16};
 
 int shape_of(int hidden, int inter)
 {
@@ -504,11 +539,11 @@ int shape_of(int hidden, int inter)
 template <class F> void with_kernel(int shape, int x_dt, F &&f)
 {
     if (shape == kShapeGptOss) {
-        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 6>, 3, DShape<32, 3>, kNdma[kShapeGptOss]>);
-        else f(decode_layer_kernel<DT_F16, DShape<16, 6>, 3, DShape<32, 3>, kNdma[kShapeGptOss]>);
+        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 6>, kStagesG[kShapeGptOss], DShape<32, 3>, kNdma[kShapeGptOss]>);
+        else f(decode_layer_kernel<DT_F16, DShape<16, 6>, kStagesG[kShapeGptOss], DShape<32, 3>, kNdma[kShapeGptOss]>);
     } else {
-        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 4>, 2, DShape<8, 3>, kNdma[kShapeQwen3]>);
-        else f(decode_layer_kernel<DT_F16, DShape<16, 4>, 2, DShape<8, 3>, kNdma[kShapeQwen3]>);
+        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 4>, kStagesG[kShapeQwen3], DShape<8, 3>, kNdma[kShapeQwen3]>);
+        else f(decode_layer_kernel<DT_F16, DShape<16, 4>, kStagesG[kShapeQwen3], DShape<8, 3>, kNdma[kShapeQwen3]>);
     }
 }
 

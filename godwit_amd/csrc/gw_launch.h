@@ -82,7 +82,7 @@ hipError_t launch_down(const Launch &L, const Plan *plan, int max_tokens, int ma
 constexpr int kSyncEpochCapacity = 8192;      // per-workgroup epochs a runner keeps
 constexpr int kDecodeLdsMax = 160 * 1024;     // LDS of one gfx950 compute unit
 constexpr int kDecodeMaxGrid = 256;           // workgroups of the one-kernel layer at most
-constexpr int kDecodeXWords = 16;             // 8-byte exchange words per workgroup
+constexpr int kDecodeXchgBytes = 32768;       // one-kernel layer's exchange buffer
 
 struct DecodeArgs {
     const float *logits;          // [experts] router logits of the token
@@ -96,7 +96,7 @@ struct DecodeArgs {
     int hidden, inter;
     Sections sec;
     int bias_dt;                  // -1: none
-    uint64_t *xchg;               // [kDecodeMaxGrid, kDecodeXWords] tagged activations, zeroed
+    uint64_t *xchg;               // kDecodeXchgBytes: probes, then fp16 activations; zeroed once
     int act_kind;
     float limit, alpha;
     float *out;                   // [hidden]

@@ -235,17 +235,6 @@ constexpr int kSelfGroupTokens = kPT;
 
 
 // Calls f(integral_constant<int, S>) for S = B .. E-1 in order.
-template <int B, int E> struct Unroll {
-    template <class F> __device__ __forceinline__ static void run(F &&f)
-    {
-        f(std::integral_constant<int, B>{});
-        Unroll<B + 1, E>::run(f);
-    }
-};
-template <int E> struct Unroll<E, E> {
-    template <class F> __device__ __forceinline__ static void run(F &&) {}
-};
-
 constexpr int kRowBytes = kKC * 32 * 2;       // one staged chunk row: 256 bf16
 constexpr int kPlaneBytes = kPT * kRowBytes;  // one staged plane of a chunk
 constexpr int kPrefillLdsMax = 160 * 1024;

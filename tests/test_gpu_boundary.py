@@ -34,11 +34,16 @@ def _f32_bias_layer(ctx, shape, E, seed):
     return layout, experts, ctx.buffer(np.concatenate([e.blob for e in experts]))
 
 
-def test_f32_bias_through_every_path(ctx):
+WIDE = dict(hidden=2880, inter=1024, act="gptOssClampedGLU", oact=oracle.ACT_GPTOSS, bias=True)
+
+
+@pytest.mark.parametrize("shape", [SMALL, WIDE], ids=["small", "h2880-f1024"])
+def test_f32_bias_through_every_path(ctx, shape):
     """set_bias_dtype(GW_F32): apply (ExpertRunner.apply), the one-token layer, a
     4-token decode batch and a 40-token grouped prefill all read fp32 biases and
-    match the oracle fed the same fp32 values."""
-    shape, E, K = SMALL, 8, 2
+    match the oracle fed the same fp32 values; also at GPT-OSS's 2880 width with
+    an intermediate size whose fp32 gate_up bias still fits its page."""
+    E, K = 8, 2
     H, F = shape["hidden"], shape["inter"]
     layout, experts, buf = _f32_bias_layer(ctx, shape, E, 5100)
     runner = gw.ExpertRunner(ctx, H, F, shape["act"], bias_dtype=gw.F32)
