@@ -453,10 +453,24 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         const int g0 = wave * gpw, g1 = min(g0 + gpw, ngroups);
         int kx = -1;
         uint4 A[MD][4];
+        // (k, group within expert) advanced per group: no division in the loop
+        int k = g0 / gpk, qg = g0 - k * gpk;
         for (int g = g0; g < g1; ++g) {
-            const int k = g / gpk;
-            const int q = (g - k * gpk) * RPW + segd;
+            const int q = qg * RPW + segd;
             const bool valid = q < nr;
+            const int qc = valid ? q : 0;
+            const uint8_t *wrow = lds8 + L.dma + k * swt + qc * rbd;
+            const uint8_t *srow = lds8 + L.dma + k * swt + sww + shs + qc * fb;
+            // this group's weight blocks and scale bytes, all read before use
+            u32x4 wv[MD];
+            uint32_t sv[MD];
+#pragma unroll
+            for (int m = 0; m < MD; ++m) {
+                const int cb = tld + m * TPD;
+                const int cbc = valid && cb < fb ? cb : 0;
+                wv[m] = *reinterpret_cast<const u32x4 *>(wrow + cbc * 16);
+                sv[m] = srow[cbc];
+            }
             if (k != kx) {                                // wave-uniform
                 const uint32_t *xk = as + k * fb * BDA;
 #pragma unroll
@@ -468,19 +482,14 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
                 }
                 kx = k;
             }
-            const int qc = valid ? q : 0;
-            const uint8_t *wrow = lds8 + L.dma + k * swt + qc * rbd;
-            const uint8_t *srow = lds8 + L.dma + k * swt + sww + shs + qc * fb;
             float acc = 0.0f;
 #pragma unroll
             for (int m = 0; m < MD; ++m) {
                 const int cb = tld + m * TPD;
                 const bool use = valid && cb < fb;
-                const int cbc = use ? cb : 0;
-                const u32x4 wv = *reinterpret_cast<const u32x4 *>(wrow + cbc * 16);
                 WBlock<DT_F16> wb;
-                widen_v(wv, wb);
-                const float d = block_dot_r<DT_F16>(wb, A[m]) * decode_scale(srow[cbc]);
+                widen_v(wv[m], wb);
+                const float d = block_dot_r<DT_F16>(wb, A[m]) * decode_scale(sv[m]);
                 acc += use ? d : 0.0f;
             }
             acc = seg_sum<TPD>(acc);
@@ -492,6 +501,10 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
                                                : load_as_f32(bp, a.bias_dt, 0);
                 }
                 vals[k * a.nrmax + q] = acc + bias;
+            }
+            if (++qg == gpk) {
+                qg = 0;
+                ++k;
             }
         }
     }
