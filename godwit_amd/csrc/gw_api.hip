@@ -598,7 +598,7 @@ struct gw_expert_runner {
     float *logits = nullptr;         // [kMaxTokens, kMaxExperts]
     Plan *staging = nullptr;         // pinned host mirror of `plans`
     unsigned *sync_buf = nullptr;    // fused layer exchange: counters | epochs | error word
-    uint64_t *xchg_buf = nullptr;    // one-kernel layer: probes + activations (zeroed once)
+    uint64_t *xchg_buf = nullptr;    // one-kernel layer: tagged activation words (zeroed once)
     // prefill scratch, sized for pf_tokens tokens x pf_topk ranks x pf_experts
     int pf_tokens = 0, pf_topk = 0, pf_experts = 0;
     int pf_last_tokens = 0, pf_last_topk = 0;   // of the last batch in pf_buf
@@ -677,7 +677,10 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     const size_t sync_bytes = sizeof(unsigned) * (gw::kSyncWords + kSyncEpochWords + 64);
     if (e == hipSuccess) e = hipMalloc((void **)&r->sync_buf, sync_bytes);
     if (e == hipSuccess) e = hipMemset(r->sync_buf, 0, sync_bytes);
-    const size_t xchg_bytes = gw::kDecodeXchgBytes;
+    // the exchange ring gets a 2 MiB block of its own, the large-page granule, so
+    // every compute unit's polls share one translation (measured faster than a
+    // block of the ring's own size)
+    const size_t xchg_bytes = std::max<size_t>(gw::kDecodeXchgBytes, 2u << 20);
     if (e == hipSuccess) e = hipMalloc((void **)&r->xchg_buf, xchg_bytes);
     if (e == hipSuccess) e = hipMemset(r->xchg_buf, 0, xchg_bytes);
     if (e == hipSuccess) e = hipDeviceSynchronize();

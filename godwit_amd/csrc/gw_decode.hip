@@ -56,7 +56,8 @@ constexpr int kRsrcWord3 = 0x00020000;   // raw (untyped) buffer access
 constexpr int kNt = 2;                   // buffer cache policy: non-temporal (streamed once)
 constexpr uint32_t kOutOfRange = 0x80000000u;   // buffer offset past any layer (reads zero)
 constexpr int kXWords = 16;              // exchange words per workgroup (3 activations each)
-static_assert(kDecodeMaxGrid * kXWords * 8 <= kDecodeXchgBytes, "exchange buffer");
+constexpr int kXSlotWords = kDecodeMaxGrid * kXWords;   // one launch's words
+static_assert(kXSlotWords * 8 * kDecodeXchgSlots <= kDecodeXchgBytes, "exchange buffer");
 constexpr unsigned kSpinLimit = 1u << 18;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -78,13 +79,14 @@ __host__ __device__ inline DecodeLds decode_lds(int hidden, int inter, int top_k
 {
     DecodeLds l;
     const int hb = hidden / 32, fb = inter / 32;
-    l.route = 0;                                   // int32 ids[8], float w[8], done count
+    l.route = 0;                                   // int32 ids[8], float w[8], done count, rank counts
     l.xs = 128;                                    // x, 20 dwords per block
     l.actl = l.xs + hb * 80;                       // this workgroup's fp16 activations
     l.dma = (l.actl + rows_per_wg + 255) & ~255;   // the down stream (+ one spare chunk)
     const int dma_bytes = (top_k * sw_total + kChunk - 1) / kChunk * kChunk + kChunk;
-    l.as = l.dma + dma_bytes;                      // all activations, 20 dwords per block
-    l.vals = l.as + top_k * fb * 80;               // down outputs [top_k][nrmax]
+    l.as = l.dma + dma_bytes;                      // all activations, fp16 [top_k][inter]
+    // (the routing keys and logits, 1 KiB, use the same area before the exchange)
+    l.vals = l.as + max(top_k * fb * 64, 1024);    // down outputs [top_k][nrmax]
     l.total = l.vals + top_k * nrmax * 4;
     return l;
 }
@@ -142,16 +144,16 @@ template <int TPR> __device__ __forceinline__ float next_segment(float v)
 }  // namespace
 
 // XK: x dtype (bf16 or fp16).  GS / DS: row shapes of gate_up (hidden wide)
-// and down (intermediate wide) rows.  NSG: gate_up stages (of kDW * 64 / TPR
-// rows) a workgroup's share fills; they are all in flight at once.  NDMA:
-// 1 KiB LDS-DMA pieces each of waves 1.. issues for the down stream.
-template <int XK, class GS, int NSG, class DS, int NDMA>
+// and down (intermediate wide) rows.  NSG: gate_up stages (of kGuWaves * 64 /
+// TPR rows) a workgroup's share fills.  NDMA: 1 KiB LDS-DMA pieces each DMA
+// wave issues for the down stream.  PD: ticks of the 100 MHz real-time
+// counter between publishing and the first poll of the exchange.
+template <int XK, class GS, int NSG, class DS, int NDMA, int PD>
 __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
 {
     constexpr int TPG = GS::TPR, MG = GS::M, SEGG = 64 / TPG, RGW = kGuWaves * SEGG;
     constexpr int TPD = DS::TPR, MD = DS::M, SEGD = 64 / TPD;
     constexpr int BD = XL<XK>::kBlockDw;
-    constexpr int BDA = XL<DT_F16>::kBlockDw;
     extern __shared__ __align__(16) uint32_t lds[];
     uint8_t *lds8 = reinterpret_cast<uint8_t *>(lds);
 
@@ -179,23 +181,99 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     // Launches this workgroup has completed (written back at the end).
     const unsigned epoch1 = a.sync.epochs[b] + 1;
 
-    // ---- 1. route (wave 0) while waves 1.. stage x -------------------------
+    // ---- 1. route while waves 1.. stage x -----------------------------------
+    // Up to 128 experts: wave 0 writes the logits' order keys to LDS (0 for
+    // NaN and for no expert), then every thread counts, for expert t / 4,
+    // the keys greater than its own in quarter t % 4 of them.  When no logit
+    // is NaN and no two experts share a selected rank's key, expert e's count
+    // is its position in Router.select's result (the selection sort picks
+    // the K largest in descending order whatever its permutation holds);
+    // otherwise wave 0 runs the exact selection.  The softmax over the
+    // selected logits is computed by a DMA wave, off the gate_up path.  More
+    // experts: wave 0 routes alone (select_one).
+    const bool by_rank = a.experts <= 128;
+    uint32_t *rkey = reinterpret_cast<uint32_t *>(lds8 + L.as);   // keys [128]; the
+    float *rlogit = reinterpret_cast<float *>(lds8 + L.as + 512);  // exchange area is free
+    unsigned *rcount = reinterpret_cast<unsigned *>(lds8 + L.route + 68);   // [kMaxTopK + 1]
     if (wave == 0) {
-        if (lane == 0) *gu_done = 0u;
-        int sid;
-        float w;
-        if (a.experts <= 128) select_one<2>(a.logits, a.experts, K, sid, w);
-        else select_one<4>(a.logits, a.experts, K, sid, w);
-        if (lane < K) {
-            eid[lane] = sid;
-            ew[lane] = w;
-            if (b == 0 && a.ids_out) a.ids_out[lane] = sid;
-            if (b == 0 && a.w_out) a.w_out[lane] = w;
+        if (by_rank) {
+            bool nan = false;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int i = lane + 64 * r;
+                const float v = a.logits[min(i, a.experts - 1)];
+                const bool in = i < a.experts, isn = in && __builtin_isnan(v);
+                nan |= isn;
+                rkey[i] = in && !isn ? order_key(v) : 0u;
+                rlogit[i] = v;
+            }
+            // rcount[0..K) count the experts placed at each rank; rcount[K]
+            // flags a NaN
+            const bool any_nan = __ballot(nan) != 0ull;
+            if (lane <= K) rcount[lane] = lane == K && any_nan ? 1u : 0u;
+            if (lane == 0) *gu_done = 0u;
+        } else {
+            if (lane == 0) *gu_done = 0u;
+            int sid;
+            float w;
+            select_one<4>(a.logits, a.experts, K, sid, w);
+            if (lane < K) {
+                eid[lane] = sid;
+                ew[lane] = w;
+                if (b == 0 && a.ids_out) a.ids_out[lane] = sid;
+                if (b == 0 && a.w_out) a.w_out[lane] = w;
+            }
         }
     } else {
         stage_vector<XK>(xs, a.x, H, threadIdx.x - 64, kDT - 64);
     }
     __syncthreads();
+    if (by_rank) {
+        const int ie = threadIdx.x >> 2, qe = threadIdx.x & 3;
+        const uint32_t mk = rkey[ie];
+        const uint4 *kq = reinterpret_cast<const uint4 *>(rkey + 32 * qe);
+        int gt0 = 0, gt1 = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const uint4 k4 = kq[c];
+            gt0 += (k4.x > mk ? 1 : 0) + (k4.y > mk ? 1 : 0);
+            gt1 += (k4.z > mk ? 1 : 0) + (k4.w > mk ? 1 : 0);
+        }
+        int gt = gt0 + gt1;
+        gt += __builtin_amdgcn_mov_dpp(gt, 0xB1, 0xF, 0xF, true);   // the element's 4 lanes
+        gt += __builtin_amdgcn_mov_dpp(gt, 0x4E, 0xF, 0xF, true);
+        if (qe == 0 && mk != 0u && gt < K) {
+            eid[gt] = ie;
+            ew[gt] = rlogit[ie];                  // the logit until the softmax below
+            atomicAdd(rcount + gt, 1u);
+        }
+        __syncthreads();
+        bool exact = rcount[K] != 0u;
+        for (int r = 0; r < K; ++r) exact |= rcount[r] != 1u;
+        if (exact) {                              // uniform: NaN or a tie
+            if (wave == 0) {
+                int sid;
+                float w;
+                select_one<2>(a.logits, a.experts, K, sid, w);
+                if (lane < K) {
+                    eid[lane] = sid;
+                    ew[lane] = w;
+                    if (b == 0 && a.ids_out) a.ids_out[lane] = sid;
+                    if (b == 0 && a.w_out) a.w_out[lane] = w;
+                }
+            }
+            __syncthreads();
+        } else if (wave == kGuWaves) {
+            // ew is read at the combine, after the barriers that follow
+            const float sv = ew[min(lane, K - 1)];
+            const float w = softmax_ranked(sv, K);
+            if (lane < K) {
+                ew[lane] = w;
+                if (b == 0 && a.ids_out) a.ids_out[lane] = eid[lane];
+                if (b == 0 && a.w_out) a.w_out[lane] = w;
+            }
+        }
+    }
 
     const int segg = lane / TPG, tlg = lane % TPG;
     const int nrows = 2 * (p1 - p0);
@@ -372,7 +450,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     const int npair = K * F;
     const unsigned pq = (unsigned)npair / (unsigned)G, pr = (unsigned)npair - pq * (unsigned)G;
     const uint64_t tag = (uint64_t)(epoch1 & 0xFFFFu);
-    uint64_t *xw = a.xchg;
+    uint64_t *xw = a.xchg + (epoch1 % kDecodeXchgSlots) * kXSlotWords;
     if (wave == 0 && 3 * lane < p1 - p0) {
         uint64_t v = tag << 48;
 #pragma unroll
@@ -385,54 +463,70 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     if (wave >= kGuWaves) {
         __builtin_amdgcn_s_waitcnt(0);            // this wave's part of the down stream is in LDS
     } else {
+        // Thread t reads word j = t % kXWords of workgroups t / kXWords +
+        // u * kPbStep.  The first round's loads are all issued before any
+        // LDS address is formed, so that work overlaps their latency.
         constexpr int kPollT = kGuWaves * 64;
         constexpr int WPT = kDecodeMaxGrid * kXWords / kPollT;   // words per thread
+        constexpr int kPbStep = kPollT / kXWords;
         static_assert(WPT <= 32, "pending mask");
         const int t = (int)threadIdx.x;
+        const int j = t % kXWords, pb0 = t / kXWords;
         uint32_t pending = 0;
 #pragma unroll
         for (int u = 0; u < WPT; ++u) {
-            const int idx = t + u * kPollT;
-            const int pb = idx / kXWords, j = idx % kXWords;
+            const int pb = pb0 + u * kPbStep;
             const int np = (int)pq + (pb < (int)pr ? 1 : 0);
-            if (pb < G && 3 * j < np) pending |= 1u << u;
+            pending |= (uint32_t)((pb < G) & (3 * j < np)) << u;
         }
+        {
+            const uint64_t t_pub = wall_clock64();
+            while (wall_clock64() - t_pub < (uint64_t)PD) __builtin_amdgcn_s_sleep(2);
+        }
+        // The first round may be served by this chip's L2 (the first of its
+        // compute units to read a line fetches it once for all); a word
+        // found stale there is read again past the L2.
+        uint64_t v[WPT];
+#pragma unroll
+        for (int u = 0; u < WPT; ++u)
+            v[u] = (pending >> u) & 1u
+                       ? __hip_atomic_load(xw + t + u * kPollT, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WAVEFRONT)
+                       : 0ull;
+        __builtin_amdgcn_sched_barrier(0);
+        // Word (pb, j) holds pairs pb * pq + min(pb, pr) + 3j .. +2 of the
+        // linear fp16 [top_k][inter] layout; they are written with ds_write
+        // written out, which waits only for this word's load.
+        const uint32_t as_addr = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)(lds8 + L.as);
         unsigned spins = 0;
-        while (pending) {
-            uint64_t v[WPT];
+        for (;;) {
+#pragma unroll
+            for (int u = 0; u < WPT; ++u) {
+                if (((pending >> u) & 1u) && (v[u] >> 48) == tag) {
+                    pending &= ~(1u << u);
+                    const int pb = pb0 + u * kPbStep;
+                    const int nv = (int)pq + (pb < (int)pr ? 1 : 0) - 3 * j;   // >= 1
+                    const uint32_t pair = __umul24((uint32_t)pb, pq) + (uint32_t)min(pb, (int)pr) +
+                                          (uint32_t)(3 * j);
+                    const uint32_t addr = as_addr + 2 * pair;
+                    const uint32_t lo = (uint32_t)v[u], hi = (uint32_t)(v[u] >> 32);
+                    asm volatile("ds_write_b16 %0, %1" ::"v"(addr), "v"(lo) : "memory");
+                    if (nv > 1) asm volatile("ds_write_b16_d16_hi %0, %1 offset:2" ::"v"(addr), "v"(lo) : "memory");
+                    if (nv > 2) asm volatile("ds_write_b16 %0, %1 offset:4" ::"v"(addr), "v"(hi) : "memory");
+                }
+            }
+            if (!pending) break;
+            if (++spins > kSpinLimit) {
+                atomicOr(a.sync.err, 1u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
 #pragma unroll
             for (int u = 0; u < WPT; ++u)
                 v[u] = (pending >> u) & 1u
                            ? __hip_atomic_load(xw + t + u * kPollT, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT)
                            : 0ull;
-#pragma unroll
-            for (int u = 0; u < WPT; ++u) {
-                if (((pending >> u) & 1u) && (v[u] >> 48) == tag) {
-                    pending &= ~(1u << u);
-                    const int idx = t + u * kPollT;
-                    const int pb = idx / kXWords, j = idx % kXWords;
-                    const int np = (int)pq + (pb < (int)pr ? 1 : 0);
-                    const int pbase = pb * (int)pq + min(pb, (int)pr);
-#pragma unroll
-                    for (int e = 0; e < 3; ++e) {
-                        if (3 * j + e < np) {
-                            // pair p = k * F + f sits in block p / 32 of the
-                            // expert-major block layout, element p % 32
-                            const int pp = pbase + 3 * j + e;
-                            reinterpret_cast<uint16_t *>(as + (pp >> 5) * BDA)[pp & 31] =
-                                (uint16_t)(v[u] >> (16 * e));
-                        }
-                    }
-                }
-            }
-            if (pending) {
-                if (++spins > kSpinLimit) {
-                    atomicOr(a.sync.err, 1u);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
         }
     }
     __syncthreads();
@@ -472,11 +566,11 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
                 sv[m] = srow[cbc];
             }
             if (k != kx) {                                // wave-uniform
-                const uint32_t *xk = as + k * fb * BDA;
+                const uint32_t *xk = as + k * fb * 16;
 #pragma unroll
                 for (int m = 0; m < MD; ++m) {
                     const int cb = tld + m * TPD;
-                    const uint4 *xv = reinterpret_cast<const uint4 *>(xk + (cb < fb ? cb : 0) * BDA);
+                    const uint4 *xv = reinterpret_cast<const uint4 *>(xk + (cb < fb ? cb : 0) * 16);
 #pragma unroll
                     for (int qq = 0; qq < 4; ++qq) A[m][qq] = xv[qq];
                 }
@@ -536,6 +630,12 @@ namespace {
 // Qwen3-30B-A3B (2048 / 768: 64- and 24-block rows, up to top-8).
 enum { kShapeGptOss = 0, kShapeQwen3 = 1 };
 constexpr int kNdma[2] = {20, 10};   // 1 KiB pieces per DMA wave
+// The first poll of the exchange waits this many ticks (10 ns) after the
+// workgroup published, measured best on MI355X: about the spread of the
+// grid's publish times (a round that comes too early costs a second memory
+// round trip), and for GPT-OSS also the time its own down stream, queued
+// ahead of the poll's loads, still takes to land.
+constexpr int kPollDelay[2] = {140, 40};
 constexpr int kStagesG[2] = {6, 3};
 constexpr int kRowsPerStage[2] = {kGuWaves * 64 / 16, kGuWaves * 64 / 16};
 
@@ -552,11 +652,11 @@ int shape_of(int hidden, int inter)
 template <class F> void with_kernel(int shape, int x_dt, F &&f)
 {
     if (shape == kShapeGptOss) {
-        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 6>, kStagesG[kShapeGptOss], DShape<32, 3>, kNdma[kShapeGptOss]>);
-        else f(decode_layer_kernel<DT_F16, DShape<16, 6>, kStagesG[kShapeGptOss], DShape<32, 3>, kNdma[kShapeGptOss]>);
+        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 6>, kStagesG[kShapeGptOss], DShape<32, 3>, kNdma[kShapeGptOss], kPollDelay[kShapeGptOss]>);
+        else f(decode_layer_kernel<DT_F16, DShape<16, 6>, kStagesG[kShapeGptOss], DShape<32, 3>, kNdma[kShapeGptOss], kPollDelay[kShapeGptOss]>);
     } else {
-        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 4>, kStagesG[kShapeQwen3], DShape<8, 3>, kNdma[kShapeQwen3]>);
-        else f(decode_layer_kernel<DT_F16, DShape<16, 4>, kStagesG[kShapeQwen3], DShape<8, 3>, kNdma[kShapeQwen3]>);
+        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 4>, kStagesG[kShapeQwen3], DShape<8, 3>, kNdma[kShapeQwen3], kPollDelay[kShapeQwen3]>);
+        else f(decode_layer_kernel<DT_F16, DShape<16, 4>, kStagesG[kShapeQwen3], DShape<8, 3>, kNdma[kShapeQwen3], kPollDelay[kShapeQwen3]>);
     }
 }
 

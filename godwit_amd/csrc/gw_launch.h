@@ -82,7 +82,8 @@ hipError_t launch_down(const Launch &L, const Plan *plan, int max_tokens, int ma
 constexpr int kSyncEpochCapacity = 8192;      // per-workgroup epochs a runner keeps
 constexpr int kDecodeLdsMax = 160 * 1024;     // LDS of one gfx950 compute unit
 constexpr int kDecodeMaxGrid = 256;           // workgroups of the one-kernel layer at most
-constexpr int kDecodeXchgBytes = 32768;       // one-kernel layer's exchange buffer
+constexpr int kDecodeXchgSlots = 4;           // one-kernel layer's exchange: launches rotate
+constexpr int kDecodeXchgBytes = 32768 * kDecodeXchgSlots;   // over this many slots
 
 struct DecodeArgs {
     const float *logits;          // [experts] router logits of the token
@@ -96,7 +97,7 @@ struct DecodeArgs {
     int hidden, inter;
     Sections sec;
     int bias_dt;                  // -1: none
-    uint64_t *xchg;               // kDecodeXchgBytes: probes, then fp16 activations; zeroed once
+    uint64_t *xchg;               // kDecodeXchgBytes of tagged activation words; zeroed once
     int act_kind;
     float limit, alpha;
     float *out;                   // [hidden]

@@ -204,6 +204,22 @@ __device__ __forceinline__ bool select_fast(const float *__restrict__ logits, in
     return true;
 }
 
+// Softmax over the K selected logits held by lanes 0..K-1 in rank order
+// (Router.swift:92-96): the peak subtracted, exponentials summed in rank
+// order.  Returns lane k's weight (lanes >= K: unspecified).
+__device__ __forceinline__ float softmax_ranked(float sv, int K)
+{
+    float peak = lane_value(sv, 0);
+    for (int i = 1; i < K; ++i) {
+        const float x = lane_value(sv, i);
+        peak = x > peak ? x : peak;
+    }
+    const float ex = expf(sv - peak);
+    float total = 0.0f;
+    for (int i = 0; i < K; ++i) total += lane_value(ex, i);
+    return ex / total;
+}
+
 // Top-K of one token's logits by one wave, then the softmax over the K
 // selected (Router.select, Router.swift:78-98).  On return lane k < K holds
 // the expert of rank k in sid_out and its softmax weight in w_out (lanes >= K
@@ -215,17 +231,8 @@ __device__ __forceinline__ void select_one(const float *__restrict__ logits, int
     int sid;
     float sv;
     if (!select_fast<R>(logits, E, K, sid, sv)) select_exact<R>(logits, E, K, sid, sv);
-    // Softmax over the K selected logits (peak subtracted, summed in rank order).
-    float peak = lane_value(sv, 0);
-    for (int i = 1; i < K; ++i) {
-        const float x = lane_value(sv, i);
-        peak = x > peak ? x : peak;
-    }
-    const float ex = expf(sv - peak);
-    float total = 0.0f;
-    for (int i = 0; i < K; ++i) total += lane_value(ex, i);
     sid_out = sid;
-    w_out = ex / total;
+    w_out = softmax_ranked(sv, K);
 }
 
 // Routing of T tokens by one wave (select_one per token) and the demand map

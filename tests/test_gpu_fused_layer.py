@@ -145,3 +145,56 @@ def test_fused_layer_graph_chain_replays(ctx, monkeypatch):
     for b in xs + outs + [lb, buf]:
         b.free()
     runner.close()
+
+
+@pytest.mark.parametrize("shape,n_experts,top_k", [(GPTOSS, 32, 4), (GPTOSS, 128, 4),
+                                                   (GPTOSS, 144, 4), (QWEN3, 128, 8),
+                                                   (QWEN3, 60, 8)],
+                         ids=["gptoss-32", "gptoss-128", "gptoss-144", "qwen3-128", "qwen3-60"])
+@pytest.mark.parametrize("case", ["distinct", "ties_below", "tie_inside", "signed_zero",
+                                  "nan_rest", "nan_first", "all_equal"])
+def test_fused_layer_routing_exact(ctx, monkeypatch, shape, n_experts, top_k, case):
+    """The one-kernel layer's routing equals Router.select (Router.swift:78-98)
+    on every selection path: up to 128 experts the rank count over all
+    threads (distinct keys, ties below the top k), its hand-over to the exact
+    selection sort (a tie inside the top k, -0 against +0, a NaN anywhere, all
+    logits equal), and above 128 experts the one-wave selection.  Weights are
+    the same bits as the two-kernel form's, and so is the layer's output to
+    the two-kernel form's tolerance."""
+    from helpers import fill_layer_device
+    from test_gpu_expert import _routing_logits
+    H, F = shape["hidden"], shape["inter"]
+    layout = gw.ExpertLayout(H, F, n_experts)
+    buf = ctx.empty(layout.stride * n_experts)
+    fill_layer_device(ctx, buf, layout, n_experts, 17 + n_experts, biases=shape["bias"])
+    if case == "all_equal":
+        logits = np.full((1, n_experts), 0.25, np.float32)
+    else:
+        logits = _routing_logits(case, 1, n_experts)
+    lb = ctx.buffer(logits)
+    xb, _ = _inputs(ctx, rng(1400 + n_experts), H, gw.BF16)
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "1")
+    fused = gw.ExpertRunner(ctx, H, F, shape["act"])
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "0")
+    split = gw.ExpertRunner(ctx, H, F, shape["act"])
+    got = {}
+    counts = _kernel_counts(ctx, lambda: got.__setitem__(
+        "fused", _forward(ctx, fused, layout, buf, n_experts, top_k, xb, gw.BF16, lb, H)))
+    assert counts == {"moe_layer": 1, "gate_up": 0, "down": 0}, counts
+    got["split"] = _forward(ctx, split, layout, buf, n_experts, top_k, xb, gw.BF16, lb, H)
+    f_out, _, f_ids, f_w = got["fused"]
+    s_out, _, s_ids, s_w = got["split"]
+    rid, rw = oracle.router_select(logits[0], top_k)
+    assert list(f_ids) == list(rid), (case, list(f_ids), list(rid))
+    assert np.allclose(f_w, rw, rtol=1e-6, atol=1e-7, equal_nan=True), (case, f_w, rw)
+    assert np.array_equal(f_ids, s_ids)
+    assert np.array_equal(f_w.view(np.uint32), s_w.view(np.uint32))
+    if np.all(np.isfinite(s_out)):
+        assert np.max(np.abs(f_out - s_out)) <= 1e-5 * np.max(np.abs(s_out))
+    else:
+        assert np.array_equal(np.isnan(f_out), np.isnan(s_out))
+    assert fused.sync_errors() == 0
+    for b in (xb, lb, buf):
+        b.free()
+    fused.close()
+    split.close()
