@@ -677,9 +677,8 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     const size_t sync_bytes = sizeof(unsigned) * (gw::kSyncWords + kSyncEpochWords + 64);
     if (e == hipSuccess) e = hipMalloc((void **)&r->sync_buf, sync_bytes);
     if (e == hipSuccess) e = hipMemset(r->sync_buf, 0, sync_bytes);
-    // the exchange ring gets a 2 MiB block of its own, the large-page granule, so
-    // every compute unit's polls share one translation (measured faster than a
-    // block of the ring's own size)
+    // the exchange ring gets a 2 MiB block of its own: a block of the ring's own
+    // size measured 1-2% slower per layer on the same box
     const size_t xchg_bytes = std::max<size_t>(gw::kDecodeXchgBytes, 2u << 20);
     if (e == hipSuccess) e = hipMalloc((void **)&r->xchg_buf, xchg_bytes);
     if (e == hipSuccess) e = hipMemset(r->xchg_buf, 0, xchg_bytes);
