@@ -55,7 +55,7 @@ constexpr int kChunk = 1024;      // bytes one wave-wide 16-byte LDS-DMA moves
 constexpr int kRsrcWord3 = 0x00020000;   // raw (untyped) buffer access
 constexpr int kNt = 2;                   // buffer cache policy: non-temporal (streamed once)
 constexpr uint32_t kOutOfRange = 0x80000000u;   // buffer offset past any layer (reads zero)
-constexpr int kXWords = 16;              // exchange words per workgroup (3 activations each)
+constexpr int kXWords = 16;              // exchange words per workgroup at most (3 activations each)
 constexpr int kXSlotWords = kDecodeMaxGrid * kXWords;   // one launch's words
 static_assert(kXSlotWords * 8 * kDecodeXchgSlots <= kDecodeXchgBytes, "exchange buffer");
 constexpr unsigned kSpinLimit = 1u << 18;
@@ -147,8 +147,9 @@ template <int TPR> __device__ __forceinline__ float next_segment(float v)
 // and down (intermediate wide) rows.  NSG: gate_up stages (of kGuWaves * 64 /
 // TPR rows) a workgroup's share fills.  NDMA: 1 KiB LDS-DMA pieces each DMA
 // wave issues for the down stream.  PD: ticks of the 100 MHz real-time
-// counter between publishing and the first poll of the exchange.
-template <int XK, class GS, int NSG, class DS, int NDMA, int PD>
+// counter between publishing and the first poll of the exchange.  XW: words
+// of a workgroup's exchange slot (a power of two, at most kXWords).
+template <int XK, class GS, int NSG, class DS, int NDMA, int PD, int XW>
 __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
 {
     constexpr int TPG = GS::TPR, MG = GS::M, SEGG = 64 / TPG, RGW = kGuWaves * SEGG;
@@ -436,7 +437,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     }
 
     // ---- 5. exchange ---------------------------------------------------------
-    // Workgroup b publishes its activations as kXWords 8-byte words, three
+    // Workgroup b publishes its activations as XW 8-byte words, three
     // fp16 values and the 16-bit launch tag each, with device-coherent stores;
     // an aligned 8-byte store is seen whole or not at all, so the tag marks
     // the word valid and no separate flag, wait or counter is needed.  The
@@ -458,20 +459,21 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             const int j = 3 * lane + e;
             v |= (uint64_t)(j < p1 - p0 ? actl[j] : 0) << (16 * e);
         }
-        __hip_atomic_store(xw + b * kXWords + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(xw + b * XW + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (wave >= kGuWaves) {
         __builtin_amdgcn_s_waitcnt(0);            // this wave's part of the down stream is in LDS
     } else {
-        // Thread t reads word j = t % kXWords of workgroups t / kXWords +
+        // Thread t reads word j = t % XW of workgroups t / XW +
         // u * kPbStep.  The first round's loads are all issued before any
         // LDS address is formed, so that work overlaps their latency.
         constexpr int kPollT = kGuWaves * 64;
-        constexpr int WPT = kDecodeMaxGrid * kXWords / kPollT;   // words per thread
-        constexpr int kPbStep = kPollT / kXWords;
+        static_assert(XW <= kXWords && (XW & (XW - 1)) == 0, "slot words");
+        constexpr int WPT = kDecodeMaxGrid * XW / kPollT;        // words per thread
+        constexpr int kPbStep = kPollT / XW;
         static_assert(WPT <= 32, "pending mask");
         const int t = (int)threadIdx.x;
-        const int j = t % kXWords, pb0 = t / kXWords;
+        const int j = t % XW, pb0 = t / XW;
         uint32_t pending = 0;
 #pragma unroll
         for (int u = 0; u < WPT; ++u) {
@@ -636,6 +638,11 @@ constexpr int kNdma[2] = {20, 10};   // 1 KiB pieces per DMA wave
 // round trip), and for GPT-OSS also the time its own down stream, queued
 // ahead of the poll's loads, still takes to land.
 constexpr int kPollDelay[2] = {140, 40};
+// Words of a workgroup's exchange slot: GPT-OSS publishes up to 15 (45
+// activations at top-4 on 256 CUs), Qwen3 8 (24 at top-8), so two Qwen3
+// slots share a 128-byte line.  A poll's time follows the lines each compute
+// unit reads, so the slots are packed to the power of two that holds them.
+constexpr int kSlotWords[2] = {16, 8};
 constexpr int kStagesG[2] = {6, 3};
 constexpr int kRowsPerStage[2] = {kGuWaves * 64 / 16, kGuWaves * 64 / 16};
 
@@ -652,11 +659,11 @@ int shape_of(int hidden, int inter)
 template <class F> void with_kernel(int shape, int x_dt, F &&f)
 {
     if (shape == kShapeGptOss) {
-        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 6>, kStagesG[kShapeGptOss], DShape<32, 3>, kNdma[kShapeGptOss], kPollDelay[kShapeGptOss]>);
-        else f(decode_layer_kernel<DT_F16, DShape<16, 6>, kStagesG[kShapeGptOss], DShape<32, 3>, kNdma[kShapeGptOss], kPollDelay[kShapeGptOss]>);
+        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 6>, kStagesG[kShapeGptOss], DShape<32, 3>, kNdma[kShapeGptOss], kPollDelay[kShapeGptOss], kSlotWords[kShapeGptOss]>);
+        else f(decode_layer_kernel<DT_F16, DShape<16, 6>, kStagesG[kShapeGptOss], DShape<32, 3>, kNdma[kShapeGptOss], kPollDelay[kShapeGptOss], kSlotWords[kShapeGptOss]>);
     } else {
-        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 4>, kStagesG[kShapeQwen3], DShape<8, 3>, kNdma[kShapeQwen3], kPollDelay[kShapeQwen3]>);
-        else f(decode_layer_kernel<DT_F16, DShape<16, 4>, kStagesG[kShapeQwen3], DShape<8, 3>, kNdma[kShapeQwen3], kPollDelay[kShapeQwen3]>);
+        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 4>, kStagesG[kShapeQwen3], DShape<8, 3>, kNdma[kShapeQwen3], kPollDelay[kShapeQwen3], kSlotWords[kShapeQwen3]>);
+        else f(decode_layer_kernel<DT_F16, DShape<16, 4>, kStagesG[kShapeQwen3], DShape<8, 3>, kNdma[kShapeQwen3], kPollDelay[kShapeQwen3], kSlotWords[kShapeQwen3]>);
     }
 }
 
@@ -671,8 +678,8 @@ int decode_layer_plan(const Launch &L, int hidden, int inter, int x_dt, int top_
     if ((int64_t)experts * stride >= (int64_t)kOutOfRange) return 0;   // 32-bit buffer offsets
     const int G = L.cus;
     if (G <= 0 || G > kDecodeMaxGrid) return 0;
-    // Each workgroup publishes at most 3 * kXWords activations.
-    if (((int64_t)top_k * inter + G - 1) / G > 3 * kXWords) return 0;
+    // Each workgroup publishes at most 3 * XW activations.
+    if (((int64_t)top_k * inter + G - 1) / G > 3 * kSlotWords[shape]) return 0;
     // Every workgroup's gate_up share must fit the register stages.
     const int rows_g = 2 * (int)(((int64_t)top_k * inter + G - 1) / G);
     if (rows_g > kStagesG[shape] * kRowsPerStage[shape]) return 0;
