@@ -61,9 +61,6 @@ static_assert(kXSlotWords * 8 * kDecodeXchgSlots <= kDecodeXchgBytes, "exchange 
 constexpr unsigned kSpinLimit = 1u << 18;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef const __attribute__((address_space(1))) u32x4 g_u32x4;
-typedef const __attribute__((address_space(1))) uint8_t g_u8;
-typedef const __attribute__((address_space(1))) uint32_t g_u32;
 typedef __attribute__((address_space(3))) void l_void;
 
 template <int TPR_, int M_> struct DShape {
@@ -104,11 +101,6 @@ __host__ __device__ inline void decode_windows(int hidden, int inter, int nrmax,
 }
 
 namespace {
-
-__device__ __forceinline__ void store_coherent_u16(uint16_t *p, uint16_t v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // The bias element of a gate_up row is read with the stage as the aligned
 // dword containing it (one load whatever the dtype).

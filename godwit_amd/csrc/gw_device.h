@@ -143,39 +143,6 @@ template <> __device__ __forceinline__ float block_dot_r<DT_F16>(const WBlock<DT
     return a0 + a1;
 }
 
-// Two blocks' dots in four interleaved chains (two per block); each partial
-// sums its block in the same order as block_dot_r, so the values are equal.
-template <int XK> __device__ __forceinline__ void block_dot2_r(const WBlock<XK> &wa,
-                                                              const uint4 (&xa)[4],
-                                                              const WBlock<XK> &wb,
-                                                              const uint4 (&xb)[4], float &da,
-                                                              float &db)
-{
-    static_assert(XK == DT_BF16 || XK == DT_F16, "16-bit activations");
-    float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint4 x = xa[q], y = xb[q];
-        if constexpr (XK == DT_BF16) {
-#define GW_D(acc, w, v) acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, v), acc, false)
-            GW_D(a0, wa.v[4 * q + 0], x.x); GW_D(b0, wb.v[4 * q + 0], y.x);
-            GW_D(a1, wa.v[4 * q + 1], x.y); GW_D(b1, wb.v[4 * q + 1], y.y);
-            GW_D(a0, wa.v[4 * q + 2], x.z); GW_D(b0, wb.v[4 * q + 2], y.z);
-            GW_D(a1, wa.v[4 * q + 3], x.w); GW_D(b1, wb.v[4 * q + 3], y.w);
-#undef GW_D
-        } else {
-#define GW_D(acc, w, v) acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, v), acc, false)
-            GW_D(a0, wa.v[4 * q + 0], x.x); GW_D(b0, wb.v[4 * q + 0], y.x);
-            GW_D(a1, wa.v[4 * q + 1], x.y); GW_D(b1, wb.v[4 * q + 1], y.y);
-            GW_D(a0, wa.v[4 * q + 2], x.z); GW_D(b0, wb.v[4 * q + 2], y.z);
-            GW_D(a1, wa.v[4 * q + 3], x.w); GW_D(b1, wb.v[4 * q + 3], y.w);
-#undef GW_D
-        }
-    }
-    da = a0 + a1;
-    db = b0 + b1;
-}
-
 template <> __device__ __forceinline__ float block_dot<DT_BF16>(const WBlock<DT_BF16> &w,
                                                                const uint32_t *xb)
 {
