@@ -512,9 +512,9 @@ class ExpertRunner:
         check(lib.gw_moe_block_forward(self.handle, ctypes.byref(b)))
 
     def prefill_view(self) -> dict:
-        """Device addresses of the last grouped batch's routing, activations (two
-        bf16 planes whose sum is the fp16 activation) and per-entry expert outputs
-        in this runner's prefill scratch; valid until its next batch."""
+        """Device addresses of the last grouped batch's routing, fp16 activations
+        ([tokens * top_k, intermediate]; activation_plane 0) and per-entry expert
+        outputs in this runner's prefill scratch; valid until its next batch."""
         v = PrefillViewC()
         check(lib.gw_expert_runner_prefill_view(self.handle, ctypes.byref(v)))
         return {"routing_ids": v.routing_ids, "routing_weights": v.routing_weights,

@@ -8,10 +8,18 @@ script builds, so the script must not depend on the package.
 Compiles every HIP source under godwit_amd/csrc with hipcc for gfx950 only.
 Packed-FP32 instructions are disabled (-packed-fp32-ops): some of their
 forms have returned wrong results on the target pool.
+
+The grouped-GEMM and decode kernels order their loads with counted
+s_waitcnt vmcnt(N) waits that assume every vector-memory operation in
+flight is one the kernel issued itself; a register spill adds scratch
+stores and loads to that count.  The build reads the compiler's per-kernel
+resource report for those sources and fails if any kernel there spills a
+vector register.
 """
 from __future__ import annotations
 
 import os
+import re
 import subprocess
 import sys
 import time
@@ -25,6 +33,38 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 SOURCES = ["gw_kernels.hip", "gw_decode.hip", "gw_prefill.hip", "gw_model.hip", "gw_api.hip"]
 # Host-only C++ (no HIP), compiled by the host compiler.
 HOST_SOURCES = ["gw_host.cpp"]
+# Sources whose kernels must not spill vector registers (counted waits).
+NO_SPILL = {"gw_decode.hip", "gw_prefill.hip"}
+_REMARK = re.compile(r"remark: +(Function Name|VGPRs Spill|AGPRs Spill): (\S+)")
+
+
+def _without_remarks(out: str) -> str:
+    """Compiler output minus the resource-usage remarks and the source excerpt
+    and caret lines printed under each."""
+    keep, skipping = [], False
+    for ln in out.splitlines():
+        if "kernel-resource-usage" in ln:
+            skipping = True
+            continue
+        if skipping and re.match(r"^\s*(\d+\s*)?\|", ln):
+            continue
+        skipping = False
+        keep.append(ln)
+    return "\n".join(keep)
+
+
+def spilled_kernels(report: str) -> list[str]:
+    """Kernels with a vector-register spill in a -Rpass-analysis=
+    kernel-resource-usage report (remarks in order: the kernel name, then its
+    figures)."""
+    bad, name = [], None
+    for m in _REMARK.finditer(report):
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            name = val
+        elif int(val) > 0 and name:
+            bad.append(f"{name} ({key} {val})")
+    return bad
 CXX = os.environ.get("CXX", "g++")
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-fvisibility=hidden"]
 OBJDIR = os.path.join(HERE, "_build")
@@ -54,6 +94,8 @@ def build(verbose: bool = True) -> str:
         if src.endswith(".hip"):
             cmd = [HIPCC, *[f for f in FLAGS if f != "-shared"], *inc, "-c", "-o", obj,
                    os.path.join(CSRC, src)]
+            if src in NO_SPILL:
+                cmd.append("-Rpass-analysis=kernel-resource-usage")
         else:
             cmd = [CXX, *HOST_FLAGS, *inc, "-c", "-o", obj, os.path.join(CSRC, src)]
         procs.append((src, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE,
@@ -61,10 +103,16 @@ def build(verbose: bool = True) -> str:
     objs, failed, noise = [], False, []
     for src, obj, proc in procs:
         out, _ = proc.communicate()
-        noise += [ln for ln in out.splitlines() if ln.strip() and "packed-fp32-ops" not in ln]
+        noise += [ln for ln in _without_remarks(out).splitlines()
+                  if ln.strip() and "packed-fp32-ops" not in ln]
         if proc.returncode != 0:
             failed = True
             sys.stderr.write(f"{src}:\n{out}")
+        elif src in NO_SPILL:
+            spills = spilled_kernels(out)
+            if spills:
+                failed = True
+                sys.stderr.write(f"{src}: vector-register spills:\n  " + "\n  ".join(spills) + "\n")
         objs.append(obj)
     if failed:
         raise RuntimeError("hipcc failed")

@@ -1073,7 +1073,7 @@ struct PrefillScratch {
     int32_t *offsets, *order, *tiles, *ntiles;
     uint16_t *normed;   // [T, hidden] fp16 RMSNorm output (gw_moe_block_forward)
     uint16_t *xsplit;   // [planes][T, hidden] bf16 planes of a fp16 or fp32 x
-    uint16_t *act;      // [2][N, inter] bf16 planes of the fp16 activations
+    uint16_t *act;      // [N, inter] fp16 activations
     float *y;
     uint32_t *arrive;   // [T, ceil(hidden / 256)] combine counters, zero between launches
 };
@@ -1102,7 +1102,7 @@ size_t prefill_layout(const gw_expert_runner *r, int T, int K, int E, char *base
     s.ntiles = reinterpret_cast<int32_t *>(take(sizeof(int32_t)));
     s.normed = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * (size_t)T * r->hidden));
     s.xsplit = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * 3 * (size_t)T * r->hidden));
-    s.act = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * 2 * N * r->inter));
+    s.act = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * N * r->inter));
     s.y = reinterpret_cast<float *>(take(sizeof(float) * N * r->hidden));
     s.arrive = reinterpret_cast<uint32_t *>(
         take(sizeof(uint32_t) * (size_t)T * (size_t)((r->hidden + 255) / 256)));
@@ -1256,7 +1256,6 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
         g.kdim = (int)r->hidden;
         g.fdim = (int)(2 * r->inter);
         g.act_out = ps.act;
-        g.act_plane = (int64_t)T * K * r->inter;
         g.y_out = nullptr;
         ProfScope p(ctx, "prefill_gate_up");
         GW_HIP(gw::launch_prefill_gemm(p.launch(L), true, planes, g, max_tiles, T * K));
@@ -1273,7 +1272,6 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
         g.kdim = (int)r->inter;
         g.fdim = (int)r->hidden;
         g.act_out = nullptr;
-        g.act_plane = 0;
         g.y_out = ps.y;
         g.y_bytes = (int64_t)sizeof(float) * T * K * r->hidden;
         if (fuse_combine) {
@@ -1295,7 +1293,7 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
             g.comb_residual = out_mode == 2 ? 1 : 0;
         }
         ProfScope p(ctx, "prefill_down");
-        GW_HIP(gw::launch_prefill_gemm(p.launch(L), false, 2, g, max_tiles, T * K));
+        GW_HIP(gw::launch_prefill_gemm(p.launch(L), false, 1, g, max_tiles, T * K));
     }
     if (!fuse_combine) {
         ProfScope p(ctx, "prefill_combine");
@@ -1331,7 +1329,7 @@ extern "C" int gw_expert_runner_prefill_view(gw_expert_runner *r, gw_prefill_vie
     v->routing_ids = ps.ids;
     v->routing_weights = ps.weights;
     v->activations = ps.act;
-    v->activation_plane = (int64_t)r->pf_last_tokens * r->pf_last_topk * r->inter;
+    v->activation_plane = 0;
     v->expert_outputs = ps.y;
     v->tokens = r->pf_last_tokens;
     v->top_k = r->pf_last_topk;

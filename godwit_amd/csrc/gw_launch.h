@@ -120,7 +120,7 @@ hipError_t launch_decode_layer(const Launch &L, int grid, size_t lds, int x_dt,
 // One grouped GEMM launch (gate_up or down) over the work items of a grouping.
 struct PrefillGemm {
     const int32_t *tiles, *ntiles, *offsets, *order;
-    const uint16_t *in;           // bf16 planes of [rows, kdim] activations
+    const uint16_t *in;           // bf16 planes of [rows, kdim] (down: one fp16 plane)
     int64_t in_plane;             // elements between planes
     int in_row_div;               // entry -> input row divisor (top_k for x, 1 for act)
     const uint8_t *experts_base;
@@ -128,8 +128,7 @@ struct PrefillGemm {
     int64_t blocks_off, scales_off, bias_off;
     int bias_dt;                  // -1: none
     int kdim, fdim;
-    uint16_t *act_out;            // gate_up: two bf16 planes of [entries, fdim/2]
-    int64_t act_plane;            // elements between those planes
+    uint16_t *act_out;            // gate_up: fp16 activations [entries, fdim/2]
     float *y_out;                 // down: [entries, fdim] fp32
     int act_kind;
     float limit, alpha;

@@ -23,11 +23,15 @@
 // conversion reads a subnormal scale as 2^-127, so in such a row bytes 0 and
 // 1 widen 4x and 2x too large: their products are 2^-250 of a 253/254 block's for activations
 // of like size, and differ from the reference only where every 253/254 block
-// of the row sums to exactly zero.  Activations enter the bf16 matrix cores as
-// exact sums of bf16 planes: bf16 x is one plane, fp16 two (hi = bf16(v), lo =
-// v - hi) and fp32 three.  Every product in the fp32 normal range is then
-// exact and v_mfma_f32_32x32x16_bf16 accumulates in fp32, so the results
-// differ from the reference's scalar loop only in summation order.
+// of the row sums to exactly zero.  The gate_up input enters the bf16 matrix
+// cores as exact sums of bf16 planes: bf16 x is one plane, fp16 two (hi =
+// bf16(v), lo = v - hi) and fp32 three.  The down input is the fp16
+// activation itself (one plane): a wave whose scale bytes all lie in [104,
+// 140] widens its weights to fp16, exactly, and multiplies on
+// v_mfma_f32_32x32x16_f16; any other wave splits each activation into two
+// bf16 values as it reads it.  Every product in the fp32 normal range is then
+// exact and the matrix cores accumulate in fp32, so the results differ from
+// the reference's scalar loop only in summation order.
 #include <hip/hip_runtime.h>
 #include <hip/hip_ext.h>
 
@@ -41,6 +45,7 @@ namespace gw {
 
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
@@ -170,9 +175,9 @@ __global__ __launch_bounds__(kGroupThreads) void prefill_group_kernel(
 // C[256 features x 32 entries] = W_e[f-tile, :] . X[entries, :]^T over K, one
 // 32x32 block per wave, in chunks of kKC 32-element blocks (256 K elements).
 //
-// Operands.  The activations arrive as PL bf16 planes whose sum is exact
-// (bf16 x: the input itself; fp16 or fp32 x: split beforehand; the fp16
-// gate_up activation: written as two planes by the gate_up epilogue).  Per
+// Operands.  The gate_up input arrives as PL bf16 planes whose sum is exact
+// (bf16 x: the input itself; fp16 or fp32 x: split beforehand); the down
+// input is one plane of fp16 activations, written by the gate_up epilogue.  Per
 // chunk a lane (row r = lane & 31, half h = lane >> 5) holds its row's blocks
 // 4h .. 4h+3 (64 contiguous bytes), widened to bf16 with the block scale
 // folded in; MFMA 4i+d takes dword d of block 4h+i, i.e. chunk elements
@@ -195,7 +200,7 @@ struct GemmArgs {
     const int32_t *ntiles;
     const int32_t *offsets;
     const int32_t *order;
-    const uint16_t *in;           // PL bf16 planes of [rows, kdim]
+    const uint16_t *in;           // PL bf16 planes of [rows, kdim] (down: fp16, PL 1)
     int64_t in_plane;             // elements between planes
     uint32_t in_bytes;            // bytes of all planes (below 2^31)
     int in_row_div;               // entry -> input row: entry / in_row_div (K for x, 1 for act)
@@ -204,8 +209,7 @@ struct GemmArgs {
     int64_t blocks_off, scales_off, bias_off;   // section offsets within an expert
     int bias_dt;                  // -1: no bias
     int kdim, fdim;               // K (input width) and weight rows
-    uint16_t *act_out;            // gate_up: two bf16 planes of [N, fdim/2] (fp16 value = hi + lo)
-    int64_t act_plane;            // elements between the two planes
+    uint16_t *act_out;            // gate_up: fp16 activations [N, fdim/2]
     float *y_out;                 // down: [N, fdim] fp32
     int act_kind;
     float limit, alpha;
@@ -318,6 +322,12 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
     static_assert(D >= 2 && D <= 4, "ring depth");
     constexpr int kNW = 4;                    // weight-ring loads per chunk (4 x 16 B)
     constexpr int kNX = 2 * PL;               // LDS-DMA loads per chunk per wave
+    // The down GEMM takes one plane of fp16 activations: a wave whose rows'
+    // scale bytes all lie in [104, 140] widens its weights to fp16, where
+    // e2m1 * 2^(b-127) is exact (the smallest, 2^(b-128), is at least the
+    // fp16 subnormal step 2^-24, and 6 * 2^13 < 65504), and multiplies on the
+    // fp16 MFMA; other waves split each activation into two bf16 values.
+    constexpr bool F16IN = PL == 1 && !GATE_UP;
     // Loads a wave issues after a chunk's DMA until it waits for that DMA.
     constexpr int kYounger = kNW + (D - 2) * (kNX + kNW);
     static_assert(D * PL * kPlaneBytes >= 2048, "the self-grouping lists must fit in the ring");
@@ -552,12 +562,14 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
     // alternate between two accumulators so consecutive MFMAs are independent.
     constexpr int G = PL == 1 ? 4 : PL == 2 ? 2 : 1;
     constexpr int NG = 16 / G;
-    auto multiply = [&](int q, auto s_const) {
+    // FB: the wave's scale bytes leave the fp16 range (F16IN only).  wsrc:
+    // the chunk's weight words.
+    auto multiply = [&](int q, auto s_const, auto fb_const, const u32x4v (&wsrc)[4]) {
         constexpr int s = decltype(s_const)::value;
+        constexpr bool FB = decltype(fb_const)::value;
         // Recomputed per chunk rather than kept in 16 registers per plane.
         uint32_t rbs = rb;
         asm volatile("" : "+v"(rbs));
-        bf16x8 B[2][G][PL];
         auto read_group = [&](int g, bf16x8 (&dst)[G][PL]) {
 #pragma unroll
             for (int j = 0; j < G; ++j) {
@@ -571,49 +583,116 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
         // byte shift, read ahead of the first B group.
         const uint32_t sb0 = sbase + (uint32_t)(srel + 8 * q);
         uint32_t slo = lds_read4(sb0 & ~3u), shi = lds_read4((sb0 & ~3u) + 4);
-        read_group(0, B[0]);
-        lds_wait<G * PL>();
-        asm volatile("" : "+v"(slo), "+v"(shi));
-        const uint32_t sword = __builtin_amdgcn_alignbyte(shi, slo, sb0 & 3u);
         // Bit masks rather than selects, so no branch separates a load from
         // its use.
         uint32_t keep[4];
         float sc[4];
+        auto scales = [&]() {
+            asm volatile("" : "+v"(slo), "+v"(shi));
+            const uint32_t sword = __builtin_amdgcn_alignbyte(shi, slo, sb0 & 3u);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            keep[i] = q * kKC + 4 * h + i < nb ? 0xFFFFFFFFu : 0u;
-            const uint32_t sb = (sword >> (8 * i)) & 0xFFu;
-            sc[i] = decode_scale(sb ^ ((sb ^ 127u) & ~keep[i]));
+            for (int i = 0; i < 4; ++i) {
+                keep[i] = q * kKC + 4 * h + i < nb ? 0xFFFFFFFFu : 0u;
+                const uint32_t sb = (sword >> (8 * i)) & 0xFFu;
+                sc[i] = decode_scale(sb ^ ((sb ^ 127u) & ~keep[i]));
+            }
+        };
+        auto widen_bf16 = [&](int mm) {
+            const int i = mm >> 2, d = mm & 3;
+            const uint32_t w = wsrc[i][d] & keep[i];
+            return __builtin_bit_cast(bf16x8, make_uint4(
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 0)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 1)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 2)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 3))));
+        };
+        if constexpr (FB) {
+            // Weights outside the fp16 range (rare): each fp16 activation v as
+            // the exact sum of two bf16 values, hi = v truncated to bf16 and
+            // lo = v - hi (at most 3 significant bits), into the two
+            // accumulators; one fragment at a time (few registers, no speed).
+            lds_wait<0>();
+            scales();
+#pragma unroll
+            for (int mm = 0; mm < 16; ++mm) {
+                bf16x8 raw = lds_read16(xbase + (uint32_t)(s * kPlaneBytes) + (rbs ^ (uint32_t)(mm << 4)));
+                lds_wait<0>();
+                asm volatile("" : "+v"(raw));
+                const uint4 rw = __builtin_bit_cast(uint4, raw);
+                const uint32_t r4[4] = {rw.x, rw.y, rw.z, rw.w};
+                uint32_t hw[4], lw[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float v0 = f16_bits_to_f32((uint16_t)r4[e]);
+                    const float v1 = f16_bits_to_f32((uint16_t)(r4[e] >> 16));
+                    const uint32_t b0 = __builtin_bit_cast(uint32_t, v0) & 0xFFFF0000u;
+                    const uint32_t b1 = __builtin_bit_cast(uint32_t, v1) & 0xFFFF0000u;
+                    const uint32_t l0 = __builtin_bit_cast(uint32_t, v0 - __builtin_bit_cast(float, b0));
+                    const uint32_t l1 = __builtin_bit_cast(uint32_t, v1 - __builtin_bit_cast(float, b1));
+                    hw[e] = (b0 >> 16) | b1;
+                    lw[e] = (l0 >> 16) | (l1 & 0xFFFF0000u);
+                }
+                const bf16x8 aw = widen_bf16(mm);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    aw, __builtin_bit_cast(bf16x8, make_uint4(hw[0], hw[1], hw[2], hw[3])), acc, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    aw, __builtin_bit_cast(bf16x8, make_uint4(lw[0], lw[1], lw[2], lw[3])), acc1, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            return;
         }
+        bf16x8 B[2][G][PL];
+        read_group(0, B[0]);
+        lds_wait<G * PL>();
+        scales();
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             if (g + 1 < NG) read_group(g + 1, B[(g + 1) & 1]);
-            bf16x8 A[G];
+            if constexpr (F16IN) {
+                // fp16 activations x weights widened to fp16 (exact for this
+                // wave's scale bytes): one MFMA per fragment
+                f16x8 A16[G];
 #pragma unroll
-            for (int j = 0; j < G; ++j) {
-                const int mm = g * G + j, i = mm >> 2, d = mm & 3;
-                const uint32_t w = wq[s][i][d] & keep[i];
-                const uint4 au = make_uint4(
-                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 0)),
-                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 1)),
-                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 2)),
-                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 3)));
-                A[j] = __builtin_bit_cast(bf16x8, au);
-            }
-            if (g + 1 < NG) lds_wait<G * PL>();
-            else lds_wait<0>();
+                for (int j = 0; j < G; ++j) {
+                    const int mm = g * G + j, i = mm >> 2, d = mm & 3;
+                    const uint32_t w = wsrc[i][d] & keep[i];
+                    A16[j] = __builtin_bit_cast(f16x8, make_uint4(
+                        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc[i], 0)),
+                        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc[i], 1)),
+                        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc[i], 2)),
+                        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc[i], 3))));
+                }
+                if (g + 1 < NG) lds_wait<G * PL>();
+                else lds_wait<0>();
 #pragma unroll
-            for (int j = 0; j < G; ++j)
+                for (int j = 0; j < G; ++j) asm volatile("" : "+v"(B[g & 1][j][0]));
 #pragma unroll
-                for (int p = 0; p < PL; ++p) asm volatile("" : "+v"(B[g & 1][j][p]));
-#pragma unroll
-            for (int j = 0; j < G; ++j) {
-#pragma unroll
-                for (int p = 0; p < PL; ++p) {
-                    if ((j * PL + p) & 1)
-                        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[j], B[g & 1][j][p], acc1, 0, 0, 0);
+                for (int j = 0; j < G; ++j) {
+                    const f16x8 b16 = __builtin_bit_cast(f16x8, B[g & 1][j][0]);
+                    if (j & 1)
+                        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A16[j], b16, acc1, 0, 0, 0);
                     else
-                        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[j], B[g & 1][j][p], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(A16[j], b16, acc, 0, 0, 0);
+                }
+            } else {
+                bf16x8 A[G];
+#pragma unroll
+                for (int j = 0; j < G; ++j) A[j] = widen_bf16(g * G + j);
+                if (g + 1 < NG) lds_wait<G * PL>();
+                else lds_wait<0>();
+#pragma unroll
+                for (int j = 0; j < G; ++j)
+#pragma unroll
+                    for (int p = 0; p < PL; ++p) asm volatile("" : "+v"(B[g & 1][j][p]));
+#pragma unroll
+                for (int j = 0; j < G; ++j) {
+#pragma unroll
+                    for (int p = 0; p < PL; ++p) {
+                        if ((j * PL + p) & 1)
+                            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[j], B[g & 1][j][p], acc1, 0, 0, 0);
+                        else
+                            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[j], B[g & 1][j][p], acc, 0, 0, 0);
+                    }
                 }
             }
         }
@@ -624,17 +703,35 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
     // waves (after which every row of chunk q+1 is in LDS and nobody reads
     // chunk q's buffer any more).
     const int nq = (nb + kKC - 1) / kKC;
-    auto step = [&](int q, auto s_const) {
+    auto step = [&](int q, auto s_const, auto fb_const) {
         constexpr int s = decltype(s_const)::value;
         constexpr int sn = (s + D - 1) % D;
         if (q >= nq) return;                          // uniform: past the last chunk
+        if constexpr (decltype(fb_const)::value) {
+            // The split body: the same staging and barrier as the other
+            // waves, but this chunk's weights loaded here and every load
+            // drained before the multiply (no weight ring held in registers).
+            xload(sn, q + D - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            u32x4v w1[4];
+            const int base = q * kKC + 4 * h;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                w1[i] = *(g_u32x4v *)(wrow + (int64_t)min(base + i, nb - 1) * 16);
+            wait_vmcnt<0>();
+            multiply(q, s_const, fb_const, w1);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            return;
+        }
         // The counted wait below relies on a chunk's DMA being issued
         // before its weights: the scheduler may not swap them.
         xload(sn, q + D - 1);
         __builtin_amdgcn_sched_barrier(0);
         wload(sn, q + D - 1);
         __builtin_amdgcn_sched_barrier(0);
-        multiply(q, s_const);
+        multiply(q, s_const, fb_const, wq[s]);
         __builtin_amdgcn_sched_barrier(0);
         wait_vmcnt<kYounger>();
         // A bare barrier: a fenced one would also wait for every LDS-DMA in
@@ -668,11 +765,13 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
     // bytes; bit r of rows_lowered is row r of the wave's 32.  Each wave
     // rewrites only its own rows (unclamped), before its own first read.
     uint32_t rows_lowered;
+    bool f16ok;                                 // wave-uniform
     {
         const int lo = sshift + (wave * 32 + c) * nb;
         const int a0 = lo & ~3;
         const int ndw = (lo + nb - a0 + 3) >> 2;
-        uint32_t big = 0;
+        uint32_t big = 0, bad16 = 0;
+        const bool row_real = f0 + wave * 32 + c < a.fdim;
         for (int j = h; j < ndw; j += 8) {
             uint32_t w4[4];
 #pragma unroll
@@ -680,22 +779,28 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
                 w4[k] = lds_read4(sbase + (uint32_t)(a0 + 4 * min(j + 2 * k, ndw - 1)));
             lds_wait<0>();
 #pragma unroll
+            for (int k = 0; k < 4; ++k) asm volatile("" : "+v"(w4[k]));
+#pragma unroll
             for (int k = 0; k < 4; ++k) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int idx = a0 + 4 * (j + 2 * k) + i;
                     const uint32_t b = (w4[k] >> (8 * i)) & 0xFFu;
-                    big |= (uint32_t)(idx >= lo && idx < lo + nb && b - 253u <= 1u);
+                    const bool mine = idx >= lo && idx < lo + nb;
+                    big |= (uint32_t)(mine && b - 253u <= 1u);
+                    bad16 |= (uint32_t)(mine && row_real && (b < 104u || b > 140u));
                 }
             }
         }
         const uint64_t m = __builtin_amdgcn_ballot_w64(big != 0u);
         rows_lowered = (uint32_t)m | (uint32_t)(m >> 32);
+        f16ok = __builtin_amdgcn_ballot_w64(bad16 != 0u) == 0ull;
         if (rows_lowered != 0u) {                       // wave-uniform, and rare
             if ((rows_lowered >> c) & 1u) {
                 for (int j = h; j < ndw; j += 2) {
-                    const uint32_t w = lds_read4(sbase + (uint32_t)(a0 + 4 * j));
+                    uint32_t w = lds_read4(sbase + (uint32_t)(a0 + 4 * j));
                     lds_wait<0>();
+                    asm volatile("" : "+v"(w));
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int idx = a0 + 4 * j + i;
@@ -708,8 +813,21 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
             lds_wait<0>();
         }
     }
-    for (int q = 0; q < nq_pad; q += D)
-        Unroll<0, D>::run([&](auto s_const) { step(q + decltype(s_const)::value, s_const); });
+    // The K loop, with the fp16 body or, for a wave whose scales leave the
+    // fp16 range, the split one: two copies of the loop rather than a branch
+    // per chunk, so neither body's registers are held across the other.
+    // Barriers match between the copies (one per step).
+    auto kloop = [&](auto fb_const) {
+        for (int q = 0; q < nq_pad; q += D)
+            Unroll<0, D>::run(
+                [&](auto s_const) { step(q + decltype(s_const)::value, s_const, fb_const); });
+    };
+    if constexpr (F16IN) {
+        if (f16ok) kloop(std::false_type{});
+        else kloop(std::true_type{});
+    } else {
+        kloop(std::false_type{});
+    }
     // Every DMA has landed (the padding chunks' too) and, after the barrier,
     // no wave reads the staging ring any more: it holds the output tile next.
     wait_vmcnt<0>();
@@ -734,7 +852,8 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
                     : f16_bits_to_f32(reinterpret_cast<const uint16_t *>(lds8 + lay.bias)[rl]);
     }
     if constexpr (GATE_UP) {
-        // [2 planes][kPT entries][kF/2 activations] bf16
+        // [kPT entries][kF/2 activations] fp16: the reference rounds the
+        // activation to fp16, and the down GEMM reads these bits.
         uint16_t *tile = reinterpret_cast<uint16_t *>(xring);
         constexpr int kCols = kF / 2;
 #pragma unroll
@@ -742,24 +861,18 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
             const int rl = wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3);   // even: gate, +1: up
             const float y = apply_activation(a.act_kind, acc[v] + bv[v], acc[v + 1] + bv[v + 1],
                                              a.limit, a.alpha);
-            // The reference rounds the activation to fp16; it is kept as the
-            // exact sum of two bf16 planes for the down GEMM.
-            const float y16 = f16_bits_to_f32(f32_to_f16_bits(y));
-            const uint16_t hi = f32_to_bf16_bits(y16);
-            tile[c * kCols + (rl >> 1)] = hi;
-            tile[(kPT + c) * kCols + (rl >> 1)] = f32_to_bf16_bits(y16 - bf16_bits_to_f32(hi));
+            tile[c * kCols + (rl >> 1)] = f32_to_f16_bits(y);
         }
         __syncthreads();
         const int half = a.fdim >> 1;
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            // 2 planes x kPT entries x kCols / 8 pieces = 2 kThreads
-            const int idx = (int)threadIdx.x + k * kThreads;
-            const int p = idx / (kPT * 2 * W), t = (idx / (2 * W)) % kPT, piece = idx % (2 * W);
+        // kPT entries x kCols / 8 pieces = kThreads
+        {
+            const int idx = (int)threadIdx.x;
+            const int t = idx / (kCols / 8), piece = idx % (kCols / 8);
             const int col0 = (f0 >> 1) + piece * 8;
             if (t < ntok && col0 + 8 <= half) {
-                const uint4 v = *reinterpret_cast<const uint4 *>(tile + (p * kPT + t) * kCols + piece * 8);
-                *reinterpret_cast<uint4 *>(a.act_out + p * a.act_plane + (int64_t)ent[t] * half + col0) = v;
+                const uint4 v = *reinterpret_cast<const uint4 *>(tile + t * kCols + piece * 8);
+                *reinterpret_cast<uint4 *>(a.act_out + (int64_t)ent[t] * half + col0) = v;
             }
         }
     } else {
@@ -945,7 +1058,8 @@ int prefill_gemm_lds_bytes(int planes, int kdim, int waves, int depth)
 // keep the earlier shape in the list.  `tiles_hint` bounds the work list.
 struct PrefillShape { int waves, depth; };
 
-static PrefillShape prefill_shape(int fdim, int kdim, int planes, int tiles_hint, int cus)
+static PrefillShape prefill_shape(int fdim, int kdim, int planes, int tiles_hint, int cus,
+                                  bool twelve)
 {
     const int c = cus > 0 ? cus : 1;
     const PrefillShape cand[3] = {{8, planes == 3 ? 2 : 4}, {12, planes == 3 ? 2 : 4}, {8, 2}};
@@ -953,6 +1067,7 @@ static PrefillShape prefill_shape(int fdim, int kdim, int planes, int tiles_hint
     int64_t best_cost = -1;
     for (int i = 0; i < (planes == 3 ? 2 : 3); ++i) {
         const PrefillShape sh = cand[i];
+        if (sh.waves == 12 && !twelve) continue;
         const int lds = prefill_gemm_lds_bytes(planes, kdim, sh.waves, sh.depth);
         if (lds > kPrefillLdsMax) continue;
         const int64_t units = (int64_t)tiles_hint * pdiv_up(fdim, 32 * sh.waves);
@@ -988,7 +1103,8 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
     // back from a row's end: K must be a multiple of 32 and at least 128.
     if (g.kdim % 32 != 0 || g.kdim < 128 || g.fdim <= 0 || max_tiles <= 0)
         return hipErrorInvalidValue;
-    if (planes < 1 || planes > 3 || (!gate_up && planes != 2)) return hipErrorInvalidValue;
+    // gate_up: 1-3 bf16 planes of x; down: one plane of fp16 activations
+    if (planes < 1 || planes > 3 || (!gate_up && planes != 1)) return hipErrorInvalidValue;
     // The output tile is stored 8 activations or 4 outputs at a time.
     if ((gate_up && g.fdim % 16 != 0) || (!gate_up && g.fdim % 4 != 0)) return hipErrorInvalidValue;
     GemmArgs a;
@@ -1011,7 +1127,6 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
     a.kdim = g.kdim;
     a.fdim = g.fdim;
     a.act_out = g.act_out;
-    a.act_plane = g.act_plane;
     a.y_out = g.y_out;
     a.act_kind = g.act_kind;
     a.limit = g.limit;
@@ -1048,12 +1163,15 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
             return hipErrorInvalidValue;
         if (max_tiles < std::min(g.sg_experts, g.sg_tokens * g.sg_topk)) return hipErrorInvalidValue;
     }
+    // The down GEMM is built with 8 waves only: its two K-loop bodies (fp16
+    // and split bf16) do not both fit the registers of 12 waves per CU.
+    const bool twelve = gate_up;
     PrefillShape sh = prefill_shape(
         g.fdim, g.kdim, planes, tiles_hint > 0 && tiles_hint < max_tiles ? tiles_hint : max_tiles,
-        L.cus);
-    if (g.force_waves == 8 || g.force_waves == 12) {
-        // Built shapes: 8x4, 12x4 and 8x2 for one or two planes; 8x2 and
-        // 12x2 for three.
+        L.cus, twelve);
+    if (g.force_waves == 8 || (g.force_waves == 12 && twelve)) {
+        // Built shapes: gate_up 8x4, 12x4 and 8x2 for one or two planes, 8x2
+        // and 12x2 for three; down 8x4 and 8x2.
         const int d = planes == 3 ? 2 : g.force_waves == 12 ? 4 : g.force_depth == 2 ? 2 : 4;
         const PrefillShape f = {g.force_waves, d};
         if (prefill_gemm_lds_bytes(planes, g.kdim, f.waves, f.depth) <= kPrefillLdsMax) sh = f;
@@ -1101,8 +1219,13 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
             if (sh.waves == 12) with_shape(I12{}, I2{});
             else with_shape(I8{}, I2{});
         } else {
-            if (sh.waves == 12) with_shape(I12{}, I4{});
-            else if (sh.depth == 2) with_shape(I8{}, I2{});
+            if constexpr (GU) {
+                if (sh.waves == 12) {
+                    with_shape(I12{}, I4{});
+                    return;
+                }
+            }
+            if (sh.depth == 2) with_shape(I8{}, I2{});
             else with_shape(I8{}, I4{});
         }
     };
@@ -1116,7 +1239,7 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
         else if (planes == 2) go(P2{}, Y{});
         else go(P3{}, Y{});
     } else {
-        go(P2{}, N{});
+        go(P1{}, N{});
     }
     if (err != hipSuccess) return err;
     return hipGetLastError();

@@ -308,16 +308,16 @@ int gw_moe_prefill_forward(gw_expert_runner *runner, const gw_moe_layer_args *ar
  * this runner's prefill scratch as the last batch through it left them
  * (gw_moe_prefill_forward, or gw_moe_layer_forward / gw_moe_block_forward on
  * the grouped GEMMs), valid until the next such call.  Entry j = token *
- * top_k + rank.  activations: two bf16 planes [2][tokens * top_k][intermediate]
- * (plane 1 at activations + activation_plane) whose sum is the entry's fp16
- * activation exactly; expert_outputs: [tokens * top_k][hidden] fp32, down
+ * top_k + rank.  activations: fp16 [tokens * top_k][intermediate], each
+ * entry's activation as the reference rounds it (activation_plane is 0: one
+ * plane); expert_outputs: [tokens * top_k][hidden] fp32, down
  * projection plus bias, before the weighted combine.  Returns GW_ERR_ARG
  * before the first batch. */
 typedef struct gw_prefill_view {
     const int32_t *routing_ids;        /* [tokens * top_k] */
     const float *routing_weights;      /* [tokens * top_k] */
     const uint16_t *activations;
-    int64_t activation_plane;          /* elements between the two planes */
+    int64_t activation_plane;          /* 0: the activations are one plane */
     const float *expert_outputs;
     int32_t tokens, top_k;
 } gw_prefill_view;
@@ -326,12 +326,12 @@ int gw_expert_runner_prefill_view(gw_expert_runner *runner, gw_prefill_view *vie
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): gw_moe_prefill_forward with its scratch (routing ids and
- * weights, the tile list, the split x planes, the bf16 activation planes, the
+ * weights, the tile list, the split x planes, the fp16 activations, the
  * expert outputs, the combine counters) carved from a fixed per-device array
  * of GW_STATIC_SCRATCH_BYTES instead of the runner's reserved buffer.  It
  * calls no allocator (with profiling off).  A batch whose scratch exceeds the
- * array returns GW_ERR_SHAPE: about 72 tokens of GPT-OSS-120B (2880 x 2880,
- * top-4) or 78 of Qwen3-30B-A3B fit.  Same arguments and results, byte for
+ * array returns GW_ERR_SHAPE: about 90 tokens of GPT-OSS-120B (2880 x 2880,
+ * top-4) or 88 of Qwen3-30B-A3B fit.  Same arguments and results, byte for
  * byte, as gw_moe_prefill_forward.  Every call on one device shares that
  * device's array and leaves its contents behind: calls that overlap on one GPU
  * (two streams, two runners, two threads) race, and the caller serialises

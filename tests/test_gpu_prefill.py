@@ -15,6 +15,7 @@ import pytest
 
 import godwit_amd as gw
 import oracle
+from godwit_amd._lib import check, lib
 from helpers import ExpertData, expert_metric, layer_check, normal_bf16, rng
 from test_gpu_expert import GPTOSS, QWEN3, SMALL, _make_layer
 
@@ -257,11 +258,12 @@ def test_self_grouped_equals_tile_list(ctx, monkeypatch, shape, E, K, T, x_dtype
     (SMALL, 256, 8, 32, gw.BF16, 4),     # 32 KB of logits: past the 8x2 ring, read in place
 ], ids=["qwen3-t8", "small-f16-t72", "gptoss-f32-t20", "small-e256-t32"])
 def test_gemm_shapes_bit_identical(ctx, monkeypatch, shape, E, K, T, x_dtype, seed):
-    """The grouped GEMMs run 8 waves with a 4-deep ring, 12 waves (4-deep), or 8
-    waves with a 2-deep ring held to 128 VGPRs so that two workgroups share a
-    CU; the launcher picks one per launch and GODWIT_PREFILL_SHAPE forces one at
-    runner creation.  Every shape gives the same bytes (each output keeps its
-    chunk and MFMA order), and the chosen one equals the oracle."""
+    """The grouped GEMMs run 8 waves with a 4-deep ring, 12 waves (4-deep; gate_up
+    only, the down GEMM takes 8x4 instead), or 8 waves with a 2-deep ring held
+    to 128 VGPRs so that two workgroups share a CU; the launcher picks one per
+    launch and GODWIT_PREFILL_SHAPE forces one at runner creation.  Every shape
+    gives the same bytes (each output keeps its chunk and MFMA order), and the
+    chosen one equals the oracle."""
     H, F = shape["hidden"], shape["inter"]
     layout, experts, buf = _make_layer(ctx, shape, E, 2700 + seed)
     r = rng(2800 + seed)
@@ -374,6 +376,102 @@ def _edge_scale_layer(ctx, E, seed):
         experts.append(e)
     buf = ctx.buffer(np.concatenate([e.blob for e in experts]))
     return shape, layout, experts, buf
+
+
+def _download(ctx, addr, dtype, count):
+    out = np.empty(count, dtype)
+    check(lib.gw_memcpy_dtoh(ctx.handle, out.ctypes.data, addr, out.nbytes))
+    return out
+
+
+def _fp16_range_layer(ctx, E, seed):
+    """A 512 x 256 GPT-OSS-activation layer without biases whose down scale
+    bytes sit at the ends of the range where e2m1 * 2^(b-127) is exact in fp16
+    (104: 2^-24, the smallest fp16 subnormal, for code 1; 140: 6 * 2^13 for code
+    7).  Rows come in classes of 32 (one wave of a workgroup): 139/140 only,
+    104/105 only, and two mixed classes in which one row of the 32 holds a 141
+    or a 103 block, which sends that wave to the split bf16 body.  Gate_up
+    scales 2^-22 .. 2^-20 put most activations among the fp16 subnormals."""
+    shape = dict(hidden=512, inter=256, act="gptOssClampedGLU", oact=oracle.ACT_GPTOSS,
+                 bias=False)
+    H, F = shape["hidden"], shape["inter"]
+    layout = gw.ExpertLayout(H, F, E)
+    r = rng(seed)
+    experts = []
+    nbr = F // 32
+    for _ in range(E):
+        e = ExpertData(r, H, F, layout.offsets, layout.stride, with_bias=False)
+        e.gu_scales[:] = r.integers(105, 108, size=e.gu_scales.size, dtype=np.uint8)
+        sc = e.dn_scales.reshape(H, nbr)
+        for row in range(H):
+            cls = (row // 32) % 4
+            if cls == 0:
+                sc[row] = r.choice([139, 140], size=nbr)
+            elif cls == 1:
+                sc[row] = r.choice([104, 105], size=nbr)
+            else:
+                sc[row] = r.choice([104, 105, 120, 139, 140], size=nbr)
+                if row % 32 == (7 if cls == 2 else 19):
+                    sc[row, row % nbr] = 141 if cls == 2 else 103
+        for name, arr in (("gate_up_scales", e.gu_scales), ("down_scales", e.dn_scales)):
+            off = layout.offsets[name]
+            e.blob[off:off + arr.nbytes] = arr.view(np.uint8)
+        experts.append(e)
+    buf = ctx.buffer(np.concatenate([e.blob for e in experts]))
+    return shape, layout, experts, buf
+
+
+@pytest.mark.parametrize("T,forced", [(8, "8x2"), (8, "8x4"), (40, "8x2"), (40, "8x4")],
+                         ids=["self-grouped-t8-8x2", "self-grouped-t8-8x4", "tile-list-t40-8x2",
+                              "tile-list-t40-8x4"])
+def test_prefill_down_fp16_range(ctx, monkeypatch, T, forced):
+    """The down GEMM multiplies fp16 activations by weights widened to fp16 when
+    a wave's scale bytes all lie in [104, 140], and splits each activation into
+    two bf16 values otherwise.  Both are exact products summed in fp32: every
+    expert output row (the runner's prefill scratch) is within the fp32
+    summation bound 2^-16 * sum |terms| of an fp64 evaluation on the GPU's own
+    fp16 activations (expert.metal:101 rounds them to fp16), subnormal
+    activations and 2^-24 weights included, and the layer output matches
+    oracle.moe_layer per feature row (rows span 2^-24 .. 2^13 in scale)."""
+    E, K = 4, 2
+    monkeypatch.setenv("GODWIT_PREFILL_SHAPE", forced)
+    shape, layout, experts, buf = _fp16_range_layer(ctx, E, 3300 + T)
+    H, F = shape["hidden"], shape["inter"]
+    runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+    r = rng(3400 + T)
+    xb, xw = _x(ctx, r, T, H, gw.BF16)
+    logits = r.standard_normal((T, E)).astype(np.float32)
+    lb = ctx.buffer(logits)
+    got, got16, ids, wts = _run(ctx, runner, layout, buf, E, K, xb, gw.BF16, lb, T, H)
+    view = runner.prefill_view()
+    N = T * K
+    assert view["activation_plane"] == 0
+    act = _download(ctx, view["activations"], np.uint16, N * F).reshape(N, F)
+    y = _download(ctx, view["expert_outputs"], np.float32, N * H).reshape(N, H)
+    a32 = act.view(np.float16).astype(np.float32)
+    sub = (a32 != 0) & (np.abs(a32) < 2.0 ** -14)
+    assert sub.mean() > 0.5, sub.mean()             # mostly fp16 subnormals
+    xw = xw.reshape(T, H)
+    for t in range(T):
+        for k in range(K):
+            j = t * K + k
+            o = experts[int(ids[t, k])].oracle_expert().arrays
+            wd = oracle.decode(o[2], o[3], H * F // 32).reshape(H, F).astype(np.float64)
+            y64 = wd @ a32[j].astype(np.float64)
+            bound = (np.abs(wd) @ np.abs(a32[j].astype(np.float64))) * 2.0 ** -16 + 1e-45
+            err = np.abs(y[j] - y64) / bound
+            assert err.max() <= 1.0, (t, k, int(np.argmax(err)), err.max())
+    ref, rids, _ = oracle.moe_layer([e.oracle_expert() for e in experts], K, logits, xw, H, F,
+                                    shape["oact"])
+    assert np.array_equal(ids, rids)
+    for row in range(H):
+        want = ref[:, row].astype(np.float64)
+        d = np.abs(got[:, row].astype(np.float64) - want)
+        assert d.max() <= 1e-3 * np.abs(want).mean(), (row, d.max(), np.abs(want).mean())
+    assert np.array_equal(got16, oracle.f32_to_bf16_bits(got.ravel()))
+    for b in (xb, lb, buf):
+        b.free()
+    runner.close()
 
 
 @pytest.mark.parametrize("T", [8, 40], ids=["self-grouped-t8", "tile-list-t40"])
