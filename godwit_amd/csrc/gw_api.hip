@@ -699,7 +699,8 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     r->fused_combine_max = fc < 0 ? 0 : fc;
     if (const char *shape = getenv("GODWIT_PREFILL_SHAPE")) {
         int w = 0, d = 0;
-        if (sscanf(shape, "%dx%d", &w, &d) == 2 && (w == 8 || w == 12) && (d == 2 || d == 4)) {
+        if (sscanf(shape, "%dx%d", &w, &d) == 2 && (w == 4 || w == 8 || w == 12) &&
+            (d == 2 || d == 4)) {
             r->gemm_waves = w;
             r->gemm_depth = d;
         }

@@ -312,16 +312,20 @@ template <int N> __device__ __forceinline__ void lds_wait()
 }
 
 // W waves, D-deep ring.  The 8-wave, 2-deep form is held to 128 VGPRs (four
-// waves per SIMD), so two of its workgroups share a CU when their LDS fits;
-// the others hold ~165 VGPRs and one workgroup per CU.
+// waves per SIMD), so two of its workgroups share a CU when their LDS fits,
+// and the 4-wave form to 168 (three workgroups per CU); the others hold ~165
+// VGPRs and one workgroup per CU.
 template <int PL, bool GATE_UP, int W, int D, bool COMB>
-__global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm_kernel(GemmArgs a)
+__global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void prefill_gemm_kernel(GemmArgs a)
 {
     // W waves, 32 features each: a workgroup computes kF features x kPT entries.
     constexpr int kF = 32 * W, kThreads = 64 * W;
     static_assert(D >= 2 && D <= 4, "ring depth");
     constexpr int kNW = 4;                    // weight-ring loads per chunk (4 x 16 B)
-    constexpr int kNX = 2 * PL;               // LDS-DMA loads per chunk per wave
+    // Two-row LDS-DMA loads per wave per plane and chunk: 4 waves stage the
+    // 32 rows four loads each, 8 or 12 waves two each.
+    constexpr int kXR = W == 4 ? 4 : 2;
+    constexpr int kNX = kXR * PL;             // LDS-DMA loads per chunk per wave
     // The down GEMM takes one plane of fp16 activations: a wave whose rows'
     // scale bytes all lie in [104, 140] widens its weights to fp16, where
     // e2m1 * 2^(b-127) is exact (the smallest, 2^(b-128), is at least the
@@ -492,16 +496,18 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
     // Staging: wave w copies rows 4w' .. 4w'+3 of each plane (w' = w mod 8;
     // waves past 8 repeat waves 0.. with the same bytes to the same slots, so
     // every wave issues the same loads), two rows per DMA (lanes 0-31 row
-    // 4w'+2n, lanes 32-63 the next); a lane's slot is lane & 31.  The padding
+    // 4w'+2n, lanes 32-63 the next); with 4 waves, wave w copies rows 8w ..
+    // 8w+7 in four DMAs.  A lane's slot is lane & 31.  The padding
     // rows of a partial tile (t >= ntok) are read past the buffer's end: the
     // DMA puts zeros in their slots without a memory access, and their
     // columns of the tile are never stored.
     const int sw = wave & 7;
-    int64_t xrow[2];
-    int xpiece[2];
+    auto xrow0 = [&](int n) { return W == 4 ? 8 * wave + 2 * n : 4 * sw + 2 * n; };
+    int64_t xrow[kXR];
+    int xpiece[kXR];
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-        const int t = 4 * sw + 2 * n + h;
+    for (int n = 0; n < kXR; ++n) {
+        const int t = xrow0(n) + h;
         xpiece[n] = (lane & 31) ^ (t & 15);
         xrow[n] = t < ntok ? (int64_t)(ent[t] / a.in_row_div) * a.kdim : -1;
     }
@@ -516,13 +522,13 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : 1) void prefill_gemm
 #pragma unroll
         for (int p = 0; p < PL; ++p) {
 #pragma unroll
-            for (int n = 0; n < 2; ++n) {
+            for (int n = 0; n < kXR; ++n) {
                 const int k = min(q * (kKC * 32) + xpiece[n] * 8, a.kdim - 8);
                 const uint32_t voff =
                     xrow[n] < 0 ? 0x80000000u   // >= in_bytes (< 2^31): out of range
                                 : (uint32_t)((p * a.in_plane + xrow[n] + k) * 2);
                 uint8_t *dst = xring + (size_t)(buf * PL + p) * kPlaneBytes +
-                               (4 * sw + 2 * n) * kRowBytes;
+                               xrow0(n) * kRowBytes;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (l_void *)dst, 16, voff, 0, 0, 0);
             }
         }
@@ -1054,26 +1060,37 @@ int prefill_gemm_lds_bytes(int planes, int kdim, int waves, int depth)
 // permitting, and more units than CUs): co-resident workgroups overlap each
 // other's latencies (Qwen3 batch-8 down GEMM 25.9 -> 19 us, 512-token gate_up
 // 426 -> 403 us), while one workgroup per CU runs better with a 4-deep ring
-// (a 12-wave gate_up that fits the CUs in one round: 35 against 40 us).  Ties
-// keep the earlier shape in the list.  `tiles_hint` bounds the work list.
+// (a 12-wave gate_up that fits the CUs in one round: 35 against 40 us).  The
+// 4-wave, 2-deep gate_up (one activation plane: 45 KB of LDS at K = 2880,
+// three workgroups per CU) is priced at 6.6 where each CU takes at least six
+// of its units: three independent workgroups overlap one another's weight
+// waits better still (512-token gate_up 382 -> 365 us, Qwen3 batch 32 51.9
+// -> 49.8 us), but with fewer rounds it loses (Qwen3 batch 8: 34.3 against
+// 33.4 us for 12x4).  Ties keep the earlier shape in the list.  `tiles_hint`
+// bounds the work list.
 struct PrefillShape { int waves, depth; };
 
 static PrefillShape prefill_shape(int fdim, int kdim, int planes, int tiles_hint, int cus,
-                                  bool twelve)
+                                  bool twelve, bool four)
 {
     const int c = cus > 0 ? cus : 1;
-    const PrefillShape cand[3] = {{8, planes == 3 ? 2 : 4}, {12, planes == 3 ? 2 : 4}, {8, 2}};
+    const PrefillShape cand[4] = {{8, planes == 3 ? 2 : 4}, {12, planes == 3 ? 2 : 4}, {8, 2},
+                                  {4, 2}};
     PrefillShape best = cand[0];
     int64_t best_cost = -1;
-    for (int i = 0; i < (planes == 3 ? 2 : 3); ++i) {
+    for (int i = 0; i < 4; ++i) {
         const PrefillShape sh = cand[i];
+        if (planes == 3 && i == 2) continue;          // 8x2 is cand[0] for three planes
         if (sh.waves == 12 && !twelve) continue;
+        if (sh.waves == 4 && !four) continue;
         const int lds = prefill_gemm_lds_bytes(planes, kdim, sh.waves, sh.depth);
         if (lds > kPrefillLdsMax) continue;
         const int64_t units = (int64_t)tiles_hint * pdiv_up(fdim, 32 * sh.waves);
         const int64_t per_cu = (units + c - 1) / c;
         const bool shared = sh.waves == 8 && sh.depth == 2 && 2 * lds <= kPrefillLdsMax && per_cu >= 2;
-        const int64_t cost = per_cu * 32 * sh.waves * (shared ? 7 : 8);
+        if (sh.waves == 4 && (3 * lds > kPrefillLdsMax || per_cu < 6)) continue;
+        // In tenths: 8, 7 for the shared 8x2 form, 6.6 for the 4-wave form.
+        const int64_t cost = per_cu * 32 * sh.waves * (sh.waves == 4 ? 66 : shared ? 70 : 80);
         if (best_cost < 0 || cost < best_cost) {
             best = sh;
             best_cost = cost;
@@ -1166,10 +1183,14 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
     // The down GEMM is built with 8 waves only: its two K-loop bodies (fp16
     // and split bf16) do not both fit the registers of 12 waves per CU.
     const bool twelve = gate_up;
+    const bool four = gate_up && planes == 1;       // built for bf16 x only
     PrefillShape sh = prefill_shape(
         g.fdim, g.kdim, planes, tiles_hint > 0 && tiles_hint < max_tiles ? tiles_hint : max_tiles,
-        L.cus, twelve);
-    if (g.force_waves == 8 || (g.force_waves == 12 && twelve)) {
+        L.cus, twelve, four);
+    if (g.force_waves == 4 && four) {
+        const PrefillShape f = {4, 2};
+        if (prefill_gemm_lds_bytes(planes, g.kdim, 4, 2) <= kPrefillLdsMax) sh = f;
+    } else if (g.force_waves == 8 || (g.force_waves == 12 && twelve)) {
         // Built shapes: gate_up 8x4, 12x4 and 8x2 for one or two planes, 8x2
         // and 12x2 for three; down 8x4 and 8x2.
         const int d = planes == 3 ? 2 : g.force_waves == 12 ? 4 : g.force_depth == 2 ? 2 : 4;
@@ -1215,6 +1236,7 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
         using I4 = std::integral_constant<int, 4>;
         using I8 = std::integral_constant<int, 8>;
         using I12 = std::integral_constant<int, 12>;
+        using IW4 = std::integral_constant<int, 4>;
         if constexpr (PL == 3) {
             if (sh.waves == 12) with_shape(I12{}, I2{});
             else with_shape(I8{}, I2{});
@@ -1223,6 +1245,12 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
                 if (sh.waves == 12) {
                     with_shape(I12{}, I4{});
                     return;
+                }
+                if constexpr (PL == 1) {
+                    if (sh.waves == 4) {
+                        with_shape(IW4{}, I2{});
+                        return;
+                    }
                 }
             }
             if (sh.depth == 2) with_shape(I8{}, I2{});

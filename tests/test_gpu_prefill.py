@@ -259,11 +259,12 @@ def test_self_grouped_equals_tile_list(ctx, monkeypatch, shape, E, K, T, x_dtype
 ], ids=["qwen3-t8", "small-f16-t72", "gptoss-f32-t20", "small-e256-t32"])
 def test_gemm_shapes_bit_identical(ctx, monkeypatch, shape, E, K, T, x_dtype, seed):
     """The grouped GEMMs run 8 waves with a 4-deep ring, 12 waves (4-deep; gate_up
-    only, the down GEMM takes 8x4 instead), or 8 waves with a 2-deep ring held
-    to 128 VGPRs so that two workgroups share a CU; the launcher picks one per
-    launch and GODWIT_PREFILL_SHAPE forces one at runner creation.  Every shape
-    gives the same bytes (each output keeps its chunk and MFMA order), and the
-    chosen one equals the oracle."""
+    only, the down GEMM takes 8x4 instead), 8 waves with a 2-deep ring held to
+    128 VGPRs so that two workgroups share a CU, or 4 waves with a 2-deep ring
+    (gate_up with bf16 x only; three workgroups per CU); the launcher picks one
+    per launch and GODWIT_PREFILL_SHAPE forces one at runner creation.  Every
+    shape gives the same bytes (each output keeps its chunk and MFMA order),
+    and the chosen one equals the oracle."""
     H, F = shape["hidden"], shape["inter"]
     layout, experts, buf = _make_layer(ctx, shape, E, 2700 + seed)
     r = rng(2800 + seed)
@@ -271,13 +272,13 @@ def test_gemm_shapes_bit_identical(ctx, monkeypatch, shape, E, K, T, x_dtype, se
     logits = _zipf_logits(r, T, E, K)
     lb = ctx.buffer(logits)
     runs = {}
-    for forced in ("", "8x4", "12x4", "8x2"):
+    for forced in ("", "8x4", "12x4", "8x2", "4x2"):
         monkeypatch.setenv("GODWIT_PREFILL_SHAPE", forced)
         runner = gw.ExpertRunner(ctx, H, F, shape["act"])
         runs[forced] = _run(ctx, runner, layout, buf, E, K, xb, x_dtype, lb, T, H,
                             "prefill_forward")
         runner.close()
-    for forced in ("8x4", "12x4", "8x2"):
+    for forced in ("8x4", "12x4", "8x2", "4x2"):
         for i in range(4):
             assert np.array_equal(runs[forced][i], runs[""][i]), (forced, i)
     got, _, ids, wts = runs[""]
