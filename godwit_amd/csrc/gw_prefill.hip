@@ -1061,13 +1061,15 @@ int prefill_gemm_lds_bytes(int planes, int kdim, int waves, int depth)
 // other's latencies (Qwen3 batch-8 down GEMM 25.9 -> 19 us, 512-token gate_up
 // 426 -> 403 us), while one workgroup per CU runs better with a 4-deep ring
 // (a 12-wave gate_up that fits the CUs in one round: 35 against 40 us).  The
-// 4-wave, 2-deep gate_up (one activation plane: 45 KB of LDS at K = 2880,
-// three workgroups per CU) is priced at 6.6 where each CU takes at least six
-// of its units: three independent workgroups overlap one another's weight
-// waits better still (512-token gate_up 382 -> 365 us, Qwen3 batch 32 51.9
-// -> 49.8 us), but with fewer rounds it loses (Qwen3 batch 8: 34.3 against
-// 33.4 us for 12x4).  Ties keep the earlier shape in the list.  `tiles_hint`
-// bounds the work list.
+// 4-wave, 2-deep form (one plane: 45 KB of LDS at K = 2880, three workgroups
+// per CU) is priced at 6.6 where each CU takes at least six of its units and
+// K spans at least eight chunks: three independent workgroups overlap one
+// another's weight waits better still (512 tokens: gate_up 382 -> 365 us,
+// down 208 -> 192 us; Qwen3 batch 32 gate_up 51.9 -> 49.8 us), but with
+// fewer rounds (Qwen3 batch 8 gate_up: 34.3 against 33.4 us for 12x4) or
+// short rows (Qwen3 down, K = 768: 36.3 against 34.8 us at batch 32) it
+// loses.  Ties keep the earlier shape in the list.  `tiles_hint` bounds the
+// work list.
 struct PrefillShape { int waves, depth; };
 
 static PrefillShape prefill_shape(int fdim, int kdim, int planes, int tiles_hint, int cus,
@@ -1088,7 +1090,7 @@ static PrefillShape prefill_shape(int fdim, int kdim, int planes, int tiles_hint
         const int64_t units = (int64_t)tiles_hint * pdiv_up(fdim, 32 * sh.waves);
         const int64_t per_cu = (units + c - 1) / c;
         const bool shared = sh.waves == 8 && sh.depth == 2 && 2 * lds <= kPrefillLdsMax && per_cu >= 2;
-        if (sh.waves == 4 && (3 * lds > kPrefillLdsMax || per_cu < 6)) continue;
+        if (sh.waves == 4 && (3 * lds > kPrefillLdsMax || per_cu < 6 || kdim < 2048)) continue;
         // In tenths: 8, 7 for the shared 8x2 form, 6.6 for the 4-wave form.
         const int64_t cost = per_cu * 32 * sh.waves * (sh.waves == 4 ? 66 : shared ? 70 : 80);
         if (best_cost < 0 || cost < best_cost) {
@@ -1183,7 +1185,7 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
     // The down GEMM is built with 8 waves only: its two K-loop bodies (fp16
     // and split bf16) do not both fit the registers of 12 waves per CU.
     const bool twelve = gate_up;
-    const bool four = gate_up && planes == 1;       // built for bf16 x only
+    const bool four = planes == 1;                   // bf16 x (gate_up) or down
     PrefillShape sh = prefill_shape(
         g.fdim, g.kdim, planes, tiles_hint > 0 && tiles_hint < max_tiles ? tiles_hint : max_tiles,
         L.cus, twelve, four);
@@ -1251,6 +1253,11 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
                         with_shape(IW4{}, I2{});
                         return;
                     }
+                }
+            } else {
+                if (sh.waves == 4) {
+                    with_shape(IW4{}, I2{});
+                    return;
                 }
             }
             if (sh.depth == 2) with_shape(I8{}, I2{});
