@@ -1076,7 +1076,7 @@ struct PrefillScratch {
     uint16_t *xsplit;   // [planes][T, hidden] bf16 planes of a fp16 or fp32 x
     uint16_t *act;      // [N, inter] fp16 activations
     float *y;
-    uint32_t *arrive;   // [T, ceil(hidden / 256)] combine counters, zero between launches
+    uint32_t *arrive;   // prefill_arrive_count(T, hidden) combine counters, zero between launches
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1106,7 +1106,7 @@ size_t prefill_layout(const gw_expert_runner *r, int T, int K, int E, char *base
     s.act = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * N * r->inter));
     s.y = reinterpret_cast<float *>(take(sizeof(float) * N * r->hidden));
     s.arrive = reinterpret_cast<uint32_t *>(
-        take(sizeof(uint32_t) * (size_t)T * (size_t)((r->hidden + 255) / 256)));
+        take(sizeof(uint32_t) * (size_t)gw::prefill_arrive_count(T, (int)r->hidden)));
     if (ps) *ps = s;
     return o;
 }
@@ -1139,7 +1139,7 @@ extern "C" int gw_expert_runner_reserve_prefill(gw_expert_runner *r, int32_t max
     }
     PrefillScratch ps;
     prefill_layout(r, T, K, E, static_cast<char *>(r->pf_buf), &ps);
-    GW_HIP(hipMemsetAsync(ps.arrive, 0, sizeof(uint32_t) * (size_t)T * ((r->hidden + 255) / 256),
+    GW_HIP(hipMemsetAsync(ps.arrive, 0, sizeof(uint32_t) * (size_t)gw::prefill_arrive_count(T, (int)r->hidden),
                           r->ctx->stream));
     GW_HIP(hipStreamSynchronize(r->ctx->stream));
     r->pf_tokens = T;
@@ -1281,12 +1281,14 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
                 // start from zero by a fill kernel (no memset node in a
                 // captured graph).
                 ProfScope p(ctx, "prefill_clear");
-                GW_HIP(gw::launch_fill_u8(p.launch(L), ps.arrive,
-                                          sizeof(uint32_t) * (size_t)T *
-                                              (size_t)((r->hidden + 255) / 256),
-                                          1, 0, 0, 0, 0));
+                GW_HIP(gw::launch_fill_u8(
+                    p.launch(L), ps.arrive,
+                    sizeof(uint32_t) * (size_t)gw::prefill_arrive_count(T, (int)r->hidden), 1, 0,
+                    0, 0, 0));
             }
             g.arrive = ps.arrive;
+            g.arrive_count = gw::prefill_arrive_count(T, (int)r->hidden);
+            g.comb_tokens = T;
             g.comb_w = ps.weights;
             g.comb_out = a->out;
             g.comb_out_bf16 = a->out_bf16;

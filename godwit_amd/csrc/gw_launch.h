@@ -146,10 +146,14 @@ struct PrefillGemm {
     // results either way.
     int force_waves = 0, force_depth = 0;
     // Down launch with the combine fused in (arrive != null): arrive holds
-    // T x ceil(fdim / 256) zeroed counters (left zeroed), y_bytes the size of
-    // y_out, and the combine writes out [T, fdim] (+ out_bf16) from weights
-    // [T, K], adding to out when residual.
+    // arrive_count zeroed counters (left zeroed), one per token and feature
+    // tile of the chosen shape (prefill_arrive_count covers every shape),
+    // y_bytes the size of y_out, and the combine writes out [comb_tokens,
+    // fdim] (+ out_bf16) from weights [comb_tokens, K], adding to out when
+    // residual.
     uint32_t *arrive = nullptr;
+    int64_t arrive_count = 0;
+    int comb_tokens = 0;
     int64_t y_bytes = 0;
     const float *comb_w = nullptr;
     float *comb_out = nullptr;
@@ -157,6 +161,9 @@ struct PrefillGemm {
     int comb_topk = 0, comb_residual = 0;
 };
 int prefill_max_tiles(int T, int K, int E);
+// Combine counters for T tokens of a down GEMM with fdim output rows: one per
+// token and feature tile of the narrowest built shape.
+int64_t prefill_arrive_count(int T, int fdim);
 // True when a batch is small enough for the self-grouped GEMMs (every expert
 // at most one 32-entry tile); max_tiles is then min(E, T*K).
 bool prefill_self_groups(int T, int K, int E);

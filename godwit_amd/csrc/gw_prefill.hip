@@ -1027,6 +1027,10 @@ hipError_t launch_prefill_route(const Launch &L, const float *logits, int T, int
 
 int prefill_max_tiles(int T, int K, int E) { return pdiv_up((int64_t)T * K, kPT) + E; }
 
+// The narrowest built workgroup: 4 waves of 32 feature rows.
+constexpr int kMinFeatureRows = 128;
+int64_t prefill_arrive_count(int T, int fdim) { return (int64_t)T * pdiv_up(fdim, kMinFeatureRows); }
+
 bool prefill_routes_in_group(int T, int K) { return T <= kRouteGroupTokens && K <= kMaxTopK; }
 
 bool prefill_self_groups(int T, int K, int E)
@@ -1201,6 +1205,12 @@ hipError_t launch_prefill_gemm(const Launch &L, bool gate_up, int planes, const 
     }
     // One workgroup per (feature tile, tile) unit, rounded up to whole XCD
     // rounds; the kernel maps ids to units and retires the spare ones.
+    // The fused combine counts each token's arrivals per feature tile of this
+    // shape: the counters must cover comb_tokens x its tiles.
+    if (!gate_up && g.arrive &&
+        (g.comb_tokens < 1 ||
+         (int64_t)g.comb_tokens * pdiv_up(g.fdim, 32 * sh.waves) > g.arrive_count))
+        return hipErrorInvalidValue;
     const dim3 grid((pdiv_up(g.fdim, 32 * sh.waves) * max_tiles + 7) / 8 * 8);
     const int lds_bytes = prefill_gemm_lds_bytes(planes, g.kdim, sh.waves, sh.depth);
     if (lds_bytes > kPrefillLdsMax) return hipErrorInvalidValue;   // K too wide for the staging

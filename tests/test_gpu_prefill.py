@@ -379,6 +379,41 @@ def _edge_scale_layer(ctx, E, seed):
     return shape, layout, experts, buf
 
 
+@pytest.mark.parametrize("forced", ["4x2", "8x2"])
+@pytest.mark.parametrize("fn", ["prefill_forward", "prefill_forward_static"])
+def test_fused_combine_narrow_feature_tiles(ctx, monkeypatch, forced, fn):
+    """Batches of up to 32 tokens combine inside the down GEMM, which counts
+    each token's arrivals per feature tile; the 4-wave shape cuts 2880 output
+    rows into 23 tiles, the 8-wave ones into 12.  At GPT-OSS width, with a
+    shape forced, the layer equals the oracle and the default shape bit for
+    bit, from the runner's scratch and from the static array (which clears
+    the counters itself)."""
+    shape, E, K, T = GPTOSS, 16, 4, 24
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _make_layer(ctx, shape, E, 3500)
+    r = rng(3600)
+    xb, xw = _x(ctx, r, T, H, gw.BF16)
+    logits = _zipf_logits(r, T, E, K)
+    lb = ctx.buffer(logits)
+    runs = {}
+    for tag in ("", forced):
+        monkeypatch.setenv("GODWIT_PREFILL_SHAPE", tag)
+        runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+        for rep in range(2):     # the second call finds the counters left at zero
+            runs[(tag, rep)] = _run(ctx, runner, layout, buf, E, K, xb, gw.BF16, lb, T, H, fn)
+        runner.close()
+    for key, res in runs.items():
+        for i in range(4):
+            assert np.array_equal(res[i], runs[("", 0)][i]), (key, i)
+    got, _, ids, wts = runs[(forced, 1)]
+    ref, rids, rw = oracle.moe_layer([e.oracle_expert() for e in experts], K, logits, xw, H, F,
+                                     shape["oact"])
+    assert np.array_equal(ids, rids)
+    _close_batch(got, ref)
+    for b in (xb, lb, buf):
+        b.free()
+
+
 def _download(ctx, addr, dtype, count):
     out = np.empty(count, dtype)
     check(lib.gw_memcpy_dtoh(ctx.handle, out.ctypes.data, addr, out.nbytes))
