@@ -1214,11 +1214,16 @@ static int moe_prefill_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int
     const gw::Sections sec = sections_of(r->offsets);
     // Up to fused_combine_max tokens the combine runs inside the down GEMM
     // (the workgroup that completes a token's feature tile sums it), saving a
-    // launch; larger batches keep the combine kernel, since the coherent
-    // write-through of y costs more there than the launch (512 tokens: down
-    // 238 -> 270 us against a 9 us combine).
-    const bool fuse_combine = T <= r->fused_combine_max &&
-                              (int64_t)sizeof(float) * T * K * r->hidden < ((int64_t)1 << 31);
+    // launch.  Larger batches keep the combine kernel where the coherent
+    // write-through of y costs more than the launch (Qwen3 batch 512: down
+    // 49 -> 63 us against an 8.3 us combine), except when the down GEMM runs
+    // the 4-wave shape, where it costs less (GPT-OSS 512 tokens: down 191 ->
+    // 195 us against a 9 us combine and its launch gap).
+    const bool fuse_combine =
+        (T <= r->fused_combine_max ||
+         (r->fused_combine_max > 0 &&
+          gw::prefill_down_four_wave((int)r->hidden, (int)r->inter, T * K, max_tiles, L.cus))) &&
+        (int64_t)sizeof(float) * T * K * r->hidden < ((int64_t)1 << 31);
     gw::PrefillGemm g;
     g.force_waves = r->gemm_waves;
     g.force_depth = r->gemm_depth;

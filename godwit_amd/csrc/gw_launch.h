@@ -164,6 +164,10 @@ int prefill_max_tiles(int T, int K, int E);
 // Combine counters for T tokens of a down GEMM with fdim output rows: one per
 // token and feature tile of the narrowest built shape.
 int64_t prefill_arrive_count(int T, int fdim);
+// True when the down GEMM of a batch (fdim output rows, K = kdim, tiles_hint
+// entries, max_tiles work items) runs the 4-wave shape: the shape that keeps
+// the fused combine cheap.
+bool prefill_down_four_wave(int fdim, int kdim, int tiles_hint, int max_tiles, int cus);
 // True when a batch is small enough for the self-grouped GEMMs (every expert
 // at most one 32-entry tile); max_tiles is then min(E, T*K).
 bool prefill_self_groups(int T, int K, int E);

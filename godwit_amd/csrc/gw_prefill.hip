@@ -1105,6 +1105,12 @@ static PrefillShape prefill_shape(int fdim, int kdim, int planes, int tiles_hint
     return best;
 }
 
+bool prefill_down_four_wave(int fdim, int kdim, int tiles_hint, int max_tiles, int cus)
+{
+    const int hint = tiles_hint > 0 && tiles_hint < max_tiles ? tiles_hint : max_tiles;
+    return prefill_shape(fdim, kdim, 1, hint, cus, false, true).waves == 4;
+}
+
 hipError_t launch_prefill_split(const Launch &L, const void *in, int in_dt, int64_t n,
                                 uint16_t *out)
 {
