@@ -70,7 +70,7 @@ GATE_UP_TRAFFIC_BYTES = 35_944_526
 # The same for the prefill gate_up GEMM launch (512 tokens, seed 1):
 # `bench.py --workload prefill` under rocprofv3 --pmc, the copy scale of the
 # decode run (profiles/prefill_gemm_gptoss_512.md).
-PREFILL_GATE_UP_TRAFFIC_BYTES = 1_238_370_065
+PREFILL_GATE_UP_TRAFFIC_BYTES = 1_238_312_316
 # HBM bytes per decode_layer_kernel launch (the one-kernel layer, GPT-OSS-120B,
 # batch 1), measured as above over the whole 36-layer stack
 # (profiles/decode_layer_traffic.md).
