@@ -74,7 +74,7 @@ PREFILL_GATE_UP_TRAFFIC_BYTES = 1_238_312_316
 # HBM bytes per decode_layer_kernel launch (the one-kernel layer, GPT-OSS-120B,
 # batch 1), measured as above over the whole 36-layer stack
 # (profiles/decode_layer_traffic.md).
-DECODE_LAYER_TRAFFIC_BYTES = 54_357_712
+DECODE_LAYER_TRAFFIC_BYTES = 54_362_786
 
 
 def build_model(ctx, gw, lay, seed: int):
