@@ -526,11 +526,20 @@ class ExpertRunner:
         check(lib.gw_expert_runner_reserve_prefill(self.handle, max_tokens, top_k, expert_count))
 
     def sync_errors(self) -> int:
-        """Failed in-kernel exchanges of the one-token layer kernel since creation
-        (0 when every result is valid).  Waits for the runner's stream."""
+        """Waves of the one-token layer kernel whose exchange wait gave up since
+        creation (0 when every result is valid).  Waits for the runner's stream."""
         n = ctypes.c_uint32(0)
         check(lib.gw_expert_runner_sync_errors(self.handle, ctypes.byref(n)))
         return int(n.value)
+
+    def set_wait_limit(self, polls: int) -> None:
+        """Polls of the one-token layer's exchange before a wait gives up (0: default)."""
+        check(lib.gw_expert_runner_set_wait_limit(self.handle, polls))
+
+    def inject_exchange_fault(self, enable: bool) -> None:
+        """Test hook: one-token layers read an exchange slot nobody writes, so every
+        wait gives up (and every kernel still exits)."""
+        check(lib.gw_expert_runner_inject_exchange_fault(self.handle, 1 if enable else 0))
 
     def close(self) -> None:
         for b in (self._x, self._y):

@@ -10,9 +10,10 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgodwit_hip.so")
 
-GW_OK, GW_ERR_ARG, GW_ERR_SHAPE, GW_ERR_OOM, GW_ERR_HIP, GW_ERR_NO_DEVICE, GW_ERR_UNSUPPORTED = range(7)
+(GW_OK, GW_ERR_ARG, GW_ERR_SHAPE, GW_ERR_OOM, GW_ERR_HIP, GW_ERR_NO_DEVICE, GW_ERR_UNSUPPORTED,
+ GW_ERR_EXCHANGE) = range(8)
 STATUS_NAMES = {0: "GW_OK", 1: "GW_ERR_ARG", 2: "GW_ERR_SHAPE", 3: "GW_ERR_OOM", 4: "GW_ERR_HIP",
-                5: "GW_ERR_NO_DEVICE", 6: "GW_ERR_UNSUPPORTED"}
+                5: "GW_ERR_NO_DEVICE", 6: "GW_ERR_UNSUPPORTED", 7: "GW_ERR_EXCHANGE"}
 F32, F16, BF16 = 0, 1, 2
 ACT_GPTOSS_CLAMPED_GLU, ACT_SILU = 0, 1
 SECTION_COUNT = 6
@@ -106,6 +107,8 @@ SIGNATURES = {
     "gw_expert_runner_set_bias_dtype": (_I, [_P, _I]),
     "gw_expert_runner_section_offsets": (_I, [_P, _I64 * SECTION_COUNT]),
     "gw_expert_runner_sync_errors": (_I, [_P, ctypes.POINTER(ctypes.c_uint32)]),
+    "gw_expert_runner_set_wait_limit": (_I, [_P, ctypes.c_uint32]),
+    "gw_expert_runner_inject_exchange_fault": (_I, [_P, _I]),
     "gw_expert_runner_reserve_prefill": (_I, [_P, _I32, _I32, _I32]),
     "gw_expert_apply": (_I, [_P, _P, _I, ctypes.POINTER(ExpertWeightsC), _P]),
     "gw_expert_apply_batch": (_I, [_P, _P, _I, _P, _P, _I32, _P]),

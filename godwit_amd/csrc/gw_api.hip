@@ -70,6 +70,7 @@ struct gw_context {
     std::vector<ProfEvent> events;       // recorded pairs, in order
     std::vector<hipEvent_t> event_pool;  // reusable events
     std::vector<std::pair<std::string, std::pair<double, int64_t>>> totals;
+    std::vector<gw_expert_runner *> runners;   // checked for failed exchanges at synchronize
 };
 
 // True while the context's stream is being captured, by gw_graph_begin_capture
@@ -213,12 +214,14 @@ extern "C" int gw_context_destroy(gw_context *ctx)
     return GW_OK;
 }
 
+static int check_exchanges(gw_context *ctx);
+
 extern "C" int gw_context_synchronize(gw_context *ctx)
 {
     GW_CHECK(ctx, GW_ERR_ARG, "context is null");
     GW_CHECK(!is_capturing(ctx), GW_ERR_ARG, "synchronize during graph capture");
     GW_HIP(hipStreamSynchronize(ctx->stream));
-    return GW_OK;
+    return check_exchanges(ctx);
 }
 
 extern "C" void *gw_context_stream(gw_context *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
@@ -598,7 +601,10 @@ struct gw_expert_runner {
     float *logits = nullptr;         // [kMaxTokens, kMaxExperts]
     Plan *staging = nullptr;         // pinned host mirror of `plans`
     unsigned *sync_buf = nullptr;    // fused layer exchange: counters | epochs | error word
-    uint64_t *xchg_buf = nullptr;    // one-kernel layer: tagged activation words (zeroed once)
+    uint64_t *xchg_buf = nullptr;    // one-kernel layer: activation words (all ones once)
+    uint32_t spin_limit = gw::kDecodeSpinLimit;   // exchange polls before a wait gives up
+    int poll_fault = 0;              // test hook: read the never-written exchange slot
+    uint32_t xchg_errors_seen = 0;   // failed exchange waits already reported
     // prefill scratch, sized for pf_tokens tokens x pf_topk ranks x pf_experts
     int pf_tokens = 0, pf_topk = 0, pf_experts = 0;
     int pf_last_tokens = 0, pf_last_topk = 0;   // of the last batch in pf_buf
@@ -626,7 +632,11 @@ static gw::SyncArgs sync_of(gw_expert_runner *r)
 extern "C" int gw_expert_runner_destroy(gw_expert_runner *r)
 {
     if (!r) return GW_OK;
-    if (r->ctx) (void)hipStreamSynchronize(r->ctx->stream);
+    if (r->ctx) {
+        (void)hipStreamSynchronize(r->ctx->stream);
+        auto &v = r->ctx->runners;
+        v.erase(std::remove(v.begin(), v.end(), r), v.end());
+    }
     (void)hipFree(r->plans);
     (void)hipFree(r->route_plan);
     (void)hipFree(r->act_buf);
@@ -681,13 +691,14 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     // size measured 1-2% slower per layer on the same box
     const size_t xchg_bytes = std::max<size_t>(gw::kDecodeXchgBytes, 2u << 20);
     if (e == hipSuccess) e = hipMalloc((void **)&r->xchg_buf, xchg_bytes);
-    if (e == hipSuccess) e = hipMemset(r->xchg_buf, 0, xchg_bytes);
+    if (e == hipSuccess) e = hipMemset(r->xchg_buf, 0xFF, xchg_bytes);   // every word empty
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         gw_expert_runner_destroy(r);
         return alloc_failed(e, "runner scratch", 0);
     }
     r->decode_layer = get_env_int("GODWIT_DECODE_LAYER", 1) != 0;
+    ctx->runners.push_back(r);
     const int pa = get_env_int("GODWIT_PREFILL_ABOVE", 1);
     r->prefill_above = pa < 1 ? 1 : pa > gw::kMaxTokens ? gw::kMaxTokens : pa;
     // 16: at 32 tokens the selection in every gate_up workgroup (three rounds
@@ -709,11 +720,48 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     return GW_OK;
 }
 
+// After the stream is idle: a runner whose one-token layers counted a failed
+// exchange since the last check reports it, and runs its later one-token
+// layers with the two-kernel form (no cross-workgroup wait).
+static int check_exchanges(gw_context *ctx)
+{
+    for (gw_expert_runner *r : ctx->runners) {
+        uint32_t n = 0;
+        GW_HIP(hipMemcpy(&n, sync_of(r).err, sizeof(uint32_t), hipMemcpyDeviceToHost));
+        if (n != r->xchg_errors_seen) {
+            const uint32_t fresh = n - r->xchg_errors_seen;
+            r->xchg_errors_seen = n;
+            r->decode_layer = false;
+            return fail(GW_ERR_EXCHANGE,
+                        "%u wave(s) of a one-token layer gave up waiting for the activation "
+                        "exchange (the GPU was shared, or the wait limit is too small): those "
+                        "layers' outputs are invalid; this runner now uses the two-kernel form",
+                        fresh);
+        }
+    }
+    return GW_OK;
+}
+
 extern "C" int gw_expert_runner_sync_errors(gw_expert_runner *r, uint32_t *count)
 {
     GW_CHECK(r && count, GW_ERR_ARG, "null argument");
+    GW_CHECK(!is_capturing(r->ctx), GW_ERR_ARG, "sync_errors during graph capture");
     GW_HIP(hipStreamSynchronize(r->ctx->stream));
     GW_HIP(hipMemcpy(count, sync_of(r).err, sizeof(uint32_t), hipMemcpyDeviceToHost));
+    return GW_OK;
+}
+
+extern "C" int gw_expert_runner_set_wait_limit(gw_expert_runner *r, uint32_t polls)
+{
+    GW_CHECK(r, GW_ERR_ARG, "runner is null");
+    r->spin_limit = polls ? polls : gw::kDecodeSpinLimit;
+    return GW_OK;
+}
+
+extern "C" int gw_expert_runner_inject_exchange_fault(gw_expert_runner *r, int enable)
+{
+    GW_CHECK(r, GW_ERR_ARG, "runner is null");
+    r->poll_fault = enable != 0;
     return GW_OK;
 }
 
@@ -1030,6 +1078,8 @@ static int moe_layer_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int o
             d.out_bf16 = a->out_bf16;
             d.accumulate = out_mode;
             d.sync = sync_of(r);
+            d.spin_limit = r->spin_limit;
+            d.poll_fault = r->poll_fault;
             ProfScope ps(ctx, "moe_layer");
             GW_HIP(gw::launch_decode_layer(ps.launch(L), grid, lds, a->x_dtype, d));
             return GW_OK;

@@ -10,29 +10,41 @@
 // At batch 1 the layer is two dependent streams of weights: k experts' gate_up
 // rows (4 x 8.8 MB for GPT-OSS), then their down rows (4 x 4.4 MB), which
 // need every activation of their expert.  The down rows' addresses are known
-// as soon as the routing is.  Each SIMD runs one gate_up wave and one DMA
-// wave: the gate_up waves stream their rows through a ring of register stages
-// and widen and dot them as they land; the DMA waves, released once the last
-// gate_up stage is queued, copy the workgroup's down rows with their scales
-// and biases straight into LDS by buffer LDS-DMA (no registers held).  A SIMD
-// lets its older wave issue first, so the gate_up rows are queued ahead of
-// the down stream.  The activations are exchanged across the grid while the
-// down rows are still streaming in, and the down products are computed from
-// LDS once both are there.
+// as soon as the routing is.
 //
-// The exchange: a workgroup stores its activations with their launch tag in
-// 8-byte words (device-coherent stores, no wait); the gate_up waves of every
-// workgroup, which hold no down stream of their own, poll all words until
-// each carries the current tag (a bounded spin: a wait that gives
-// up sets an error word, read by gw_expert_runner_sync_errors, so no
-// workgroup ever waits unboundedly) and stages the activations in LDS.  The
-// grid must be co-resident (one workgroup per CU; the host checks occupancy).
+// * gate_up: waves 0-3 (one per SIMD) stream the workgroup's share of gate_up
+//   rows through a ring of register stages and widen and dot each stage as it
+//   lands; the share is a whole number of 4-feature quads, so the workgroup's
+//   fp16 activations fill whole 8-byte exchange words.
+// * down: every wave owns a fixed set of units (16 down rows x 4 MXFP4 blocks)
+//   and copies exactly those rows' bytes into LDS by buffer LDS-DMA, in a
+//   layout where the matrix-core operand reads are bank-conflict free.  Waves
+//   4-7 issue theirs once the gate_up waves have queued their last stage (a
+//   SIMD issues its older wave first, so the gate_up rows stay ahead); waves
+//   0-3 once their activations are out.
+// * exchange: a workgroup publishes its activations as 8-byte words of four
+//   fp16 values (device-coherent stores) into the launch's slot; every word of
+//   the slot was reset to an all-ones sentinel by the previous launch, so a
+//   word differing from it is this launch's, whole (an aligned 8-byte store is
+//   seen whole or not at all).  Each wave reads the activation blocks its own
+//   units need straight into matrix-core operand registers, rereading words
+//   still holding the sentinel past the L2 (a bounded spin: a wait that gives
+//   up counts an error, read by gw_expert_runner_sync_errors, so no workgroup
+//   ever waits unboundedly).  The grid must be co-resident (one workgroup per
+//   CU; the host checks occupancy).
+// * down products: v_mfma_f32_16x16x32_f16, weights widened to fp16 with the
+//   block scale folded in (exact for scale bytes 104..140), the activation
+//   columns one per selected expert; blocks with other scale bytes are dotted
+//   on the VALU with the fp32 scale product instead.  Per-wave partial sums
+//   meet in LDS and are summed in a fixed order, then biased and combined in
+//   router order (expert_accumulate).
 //
 // The gate_up rows are computed exactly as in the two-kernel form
 // (gate_up_kernel): the same widening, block dots, scale products, lane order
-// and reductions, so the activations are the same bytes.  The down rows are
-// split over the lanes differently (see step 6), so their fp32 sums may round
-// differently; both forms hold the reference's tolerance.
+// and reductions, so the activations are the same bytes.  The down sums are
+// accumulated in another order than the reference's sequential loop (products
+// are exact, only the fp32 rounding of the sums differs); both hold the
+// reference's tolerance.
 #include <hip/hip_ext.h>
 
 #include <type_traits>
@@ -47,20 +59,23 @@ namespace {
 
 constexpr int kDT = 512;          // threads per workgroup
 constexpr int kDW = kDT / 64;     // waves per workgroup
-// Waves 0..kGuWaves-1 (one per SIMD) stream and compute the gate_up rows and
-// then poll the exchange; the others issue the down stream's LDS-DMA.
+// Waves 0..kGuWaves-1 (one per SIMD) stream and compute the gate_up rows.
 constexpr int kGuWaves = 4;
-constexpr int kDmaWaves = kDW - kGuWaves;
+constexpr int kDmaWaves = kDW - kGuWaves;   // the others copy the down rows into LDS
 constexpr int kChunk = 1024;      // bytes one wave-wide 16-byte LDS-DMA moves
 constexpr int kRsrcWord3 = 0x00020000;   // raw (untyped) buffer access
 constexpr int kNt = 2;                   // buffer cache policy: non-temporal (streamed once)
+constexpr int kSc1 = 16;                 // buffer cache policy: device-coherent (past the L2)
 constexpr uint32_t kOutOfRange = 0x80000000u;   // buffer offset past any layer (reads zero)
-constexpr int kXWords = 16;              // exchange words per workgroup at most (3 activations each)
-constexpr int kXSlotWords = kDecodeMaxGrid * kXWords;   // one launch's words
-static_assert(kXSlotWords * 8 * kDecodeXchgSlots <= kDecodeXchgBytes, "exchange buffer");
-constexpr unsigned kSpinLimit = 1u << 18;
+constexpr uint64_t kEmpty = ~0ull;       // an exchange word not written this launch
+// Exchange slots: launches alternate between slots 0 and 1; slot 2 is never
+// written (a host flag points the readers at it to exercise the give-up path).
+constexpr int kXSlotWords = kDecodeXchgSlotBytes / 8;
+static_assert(3 * kDecodeXchgSlotBytes <= kDecodeXchgBytes, "exchange buffer");
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void l_void;
 
 template <int TPR_, int M_> struct DShape {
@@ -71,39 +86,29 @@ template <int TPR_, int M_> struct DShape {
 }  // namespace
 
 // Byte layout of the kernel's LDS (host and device compute the same).
-__host__ __device__ inline DecodeLds decode_lds(int hidden, int inter, int top_k, int nrmax,
-                                               int sw_total, int rows_per_wg)
+// pieces / scale_pieces: 1 KiB pieces of the down rows and of their scale
+// bytes; parts: fp32 partial sums of the down rows (step groups x rows);
+// rows_per_wg: gate_up rows a workgroup can hold (its fp16 activations take
+// that many bytes at most).
+__host__ __device__ inline DecodeLds decode_lds(int hidden, int pieces, int scale_pieces, int parts,
+                                               int rows_per_wg)
 {
     DecodeLds l;
-    const int hb = hidden / 32, fb = inter / 32;
-    l.route = 0;                                   // int32 ids[8], float w[8], done count, rank counts
+    const int hb = hidden / 32;
+    l.route = 0;                                   // int32 ids[8], float w[8], counters
     l.xs = 128;                                    // x, 20 dwords per block
     l.actl = l.xs + hb * 80;                       // this workgroup's fp16 activations
-    l.dma = (l.actl + rows_per_wg + 255) & ~255;   // the down stream (+ one spare chunk)
-    const int dma_bytes = (top_k * sw_total + kChunk - 1) / kChunk * kChunk + kChunk;
-    l.as = l.dma + dma_bytes;                      // all activations, fp16 [top_k][inter]
-    // (the routing keys and logits, 1 KiB, use the same area before the exchange)
-    l.vals = l.as + max(top_k * fb * 64, 1024);    // down outputs [top_k][nrmax]
-    l.total = l.vals + top_k * nrmax * 4;
+    l.dma = (l.actl + rows_per_wg + 255) & ~255;   // down pieces (routing keys before them)
+    l.scl = l.dma + (pieces > 1 ? pieces : 1) * kChunk;
+    l.part = l.scl + scale_pieces * kChunk;
+    l.total = l.part + parts * 4;
     return l;
-}
-
-// Per-expert windows of the down stream in LDS: the workgroup's down rows,
-// their scale bytes and their biases, each from a 16-byte aligned start.
-__host__ __device__ inline void decode_windows(int hidden, int inter, int nrmax, int bias_bytes,
-                                               int &sww, int &sws, int &swb)
-{
-    (void)hidden;
-    const int fb = inter / 32;
-    sww = nrmax * fb * 16;
-    sws = (nrmax * fb + 15 + 15) & ~15;
-    swb = bias_bytes > 0 ? (nrmax * bias_bytes + 15 + 15) & ~15 : 0;
 }
 
 namespace {
 
-// The bias element of a gate_up row is read with the stage as the aligned
-// dword containing it (one load whatever the dtype).
+// The bias element of a row is read as the aligned dword containing it (one
+// load whatever the dtype).
 __device__ __forceinline__ float bias_of(uint32_t bw, int bshift, int bias_dt)
 {
     if (bias_dt < 0) return 0.0f;
@@ -133,20 +138,51 @@ template <int TPR> __device__ __forceinline__ float next_segment(float v)
     }
 }
 
+// An LDS word read the compiler cannot see: after a wave has issued an
+// LDS-DMA, the compiler makes every LDS access it can see wait for all of
+// the wave's loads in flight.
+__device__ __forceinline__ uint32_t lds_peek(const void *p)
+{
+    uint32_t v;
+    const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+    return v;
+}
+
+// Four fp16 weights of a block (one packed dword) widened with the block's
+// scale folded in: exact when the e8m0 byte lies in [104, 140].
+__device__ __forceinline__ f16x8 widen_scaled(uint32_t w, float sc)
+{
+    return __builtin_bit_cast(
+        f16x8, make_uint4(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 0)),
+                          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 1)),
+                          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 2)),
+                          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 3))));
+}
+
+// 1 when either 8-byte word of a 16-byte read still holds the sentinel.
+__device__ __forceinline__ uint32_t pair_empty(const u32x4 &v)
+{
+    return (uint32_t)((v.x & v.y) == ~0u) | (uint32_t)((v.z & v.w) == ~0u);
+}
+
 }  // namespace
 
-// XK: x dtype (bf16 or fp16).  GS / DS: row shapes of gate_up (hidden wide)
-// and down (intermediate wide) rows.  NSG: gate_up stages (of kGuWaves * 64 /
-// TPR rows) a workgroup's share fills.  NDMA: 1 KiB LDS-DMA pieces each DMA
-// wave issues for the down stream.  PD: ticks of the 100 MHz real-time
-// counter between publishing and the first poll of the exchange.  XW: words
-// of a workgroup's exchange slot (a power of two, at most kXWords).
-template <int XK, class GS, int NSG, class DS, int NDMA, int PD, int XW>
+// XK: x dtype (bf16 or fp16).  GS: gate_up row shape (hidden wide).  NSG:
+// gate_up stages (of kGuWaves * 64 / TPR rows) a workgroup's share fills.
+// TD: 16-row tiles of down rows (the workgroup's rows of every selected
+// expert, expert-major); CH: 8-block chunks of a down row; NSP: 1 KiB pieces
+// of scale bytes each DMA wave copies.  WT: tile groups the waves are split
+// into (each wave takes TD / WT tiles); the kDW / WT step groups take SPW
+// steps of four blocks each.  PD: ticks of the 100 MHz real-time counter
+// between the activations being out and the first read of the exchange.
+template <int XK, class GS, int NSG, int TD, int CH, int NSP, int WT, int SPW, int PD>
 __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
 {
     constexpr int TPG = GS::TPR, MG = GS::M, SEGG = 64 / TPG, RGW = kGuWaves * SEGG;
-    constexpr int TPD = DS::TPR, MD = DS::M, SEGD = 64 / TPD;
     constexpr int BD = XL<XK>::kBlockDw;
+    constexpr int TPW = TD / WT, WS = kDW / WT, UPW = TPW * SPW;
+    static_assert(TD % WT == 0 && kDW % WT == 0, "wave split");
     extern __shared__ __align__(16) uint32_t lds[];
     uint8_t *lds8 = reinterpret_cast<uint8_t *>(lds);
 
@@ -155,22 +191,21 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int b = blockIdx.x;
     const int bsz = a.bias_dt == DT_F32 ? 4 : 2;
-    int sww, sws, swb;
-    decode_windows(H, F, a.nrmax, a.bias_dt >= 0 ? bsz : 0, sww, sws, swb);
-    const int swt = sww + sws + swb;
-    int p0, p1;                          // gate_up: (expert, feature) pairs [p0, p1)
-    slice_of(K * F, p0, p1);
+    int q0, q1;                          // gate_up: (expert, feature) quads [q0, q1)
+    slice_of((K * F) >> 2, q0, q1);
+    const int p0 = 4 * q0, p1 = 4 * q1;  // ... pairs [p0, p1)
     int r0, r1;                          // down: output rows [r0, r1) of every expert
     slice_of(H, r0, r1);
     const int nr = r1 - r0;
-    const DecodeLds L = decode_lds(H, F, K, a.nrmax, swt, RGW * NSG);
+    const int nrows_dn = K * nr;         // down rows, expert-major: row k * nr + q
+    const DecodeLds L = decode_lds(H, TD * CH * 2, (kDW - kGuWaves) * NSP, WS * 16 * TD, RGW * NSG);
     int32_t *eid = reinterpret_cast<int32_t *>(lds8 + L.route);
     float *ew = reinterpret_cast<float *>(lds8 + L.route + 32);
     unsigned *gu_done = reinterpret_cast<unsigned *>(lds8 + L.route + 64);   // gate_up waves done
+    unsigned *landed = reinterpret_cast<unsigned *>(lds8 + L.route + 108);   // DMA waves landed
     uint32_t *xs = reinterpret_cast<uint32_t *>(lds8 + L.xs);
     uint16_t *actl = reinterpret_cast<uint16_t *>(lds8 + L.actl);
-    uint32_t *as = reinterpret_cast<uint32_t *>(lds8 + L.as);
-    float *vals = reinterpret_cast<float *>(lds8 + L.vals);
+    float *part = reinterpret_cast<float *>(lds8 + L.part);
     // Launches this workgroup has completed (written back at the end).
     const unsigned epoch1 = a.sync.epochs[b] + 1;
 
@@ -182,11 +217,11 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     // is its position in Router.select's result (the selection sort picks
     // the K largest in descending order whatever its permutation holds);
     // otherwise wave 0 runs the exact selection.  The softmax over the
-    // selected logits is computed by a DMA wave, off the gate_up path.  More
-    // experts: wave 0 routes alone (select_one).
+    // selected logits is computed by a down-stream wave, off the gate_up
+    // path.  More experts: wave 0 routes alone (select_one).
     const bool by_rank = a.experts <= 128;
-    uint32_t *rkey = reinterpret_cast<uint32_t *>(lds8 + L.as);   // keys [128]; the
-    float *rlogit = reinterpret_cast<float *>(lds8 + L.as + 512);  // exchange area is free
+    uint32_t *rkey = reinterpret_cast<uint32_t *>(lds8 + L.dma);   // keys [128]; the down
+    float *rlogit = reinterpret_cast<float *>(lds8 + L.dma + 512);  // pieces come later
     unsigned *rcount = reinterpret_cast<unsigned *>(lds8 + L.route + 68);   // [kMaxTopK + 1]
     if (wave == 0) {
         if (by_rank) {
@@ -204,9 +239,9 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             // flags a NaN
             const bool any_nan = __ballot(nan) != 0ull;
             if (lane <= K) rcount[lane] = lane == K && any_nan ? 1u : 0u;
-            if (lane == 0) *gu_done = 0u;
+            if (lane == 0) *gu_done = 0u, *landed = 0u;
         } else {
-            if (lane == 0) *gu_done = 0u;
+            if (lane == 0) *gu_done = 0u, *landed = 0u;
             int sid;
             float w;
             select_one<4>(a.logits, a.experts, K, sid, w);
@@ -276,53 +311,118 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     const __amdgpu_buffer_rsrc_t lr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(a.base), (short)0, (int)a.base_bytes, kRsrcWord3);
 
+    // ---- the down stream --------------------------------------------------------
+    // The workgroup's down rows of every selected expert, expert-major (row
+    // rho = k * nr + q is output row r0 + q of expert rank k), in tiles of 16
+    // rows.  Piece (t, c, h) (1 KiB) holds rows 16t + 8h .. +7 and blocks
+    // 8c .. 8c+7: row r8 at r8 * 128, block b in slot b ^ r8, so a DMA lane
+    // group copies one whole 128-byte line of a row, and an operand read of
+    // eight lanes (eight rows, one block each) touches every LDS bank once.
+    // The scale bytes follow as one window per expert (nr * fb bytes from a
+    // 16-byte aligned start).  The DMA waves copy it all and count themselves
+    // in LDS once their copies have landed.
+    constexpr int NPIECE = TD * CH * 2;
+    static_assert(NPIECE % kDmaWaves == 0, "pieces per DMA wave");
+    constexpr int NPD = NPIECE / kDmaWaves;
+    const int s0 = r0 * fb, shs = s0 & 15;
+    const int sws = (nr * fb + shs + 15) & ~15;   // scale window per expert
+    const float inv_nr = 1.0f / (float)nr, inv_sws = 1.0f / (float)sws;
+    const int rbd = fb * 16;
+    // Units: (t, s) = 16 rows x blocks 4s..4s+3.  Wave w takes tiles tg*TPW..
+    // and steps sg*SPW.. (tg = w % WT, sg = w / WT); operand lane l' reads row
+    // l' & 15, block 4s + (l' >> 4).
+    const int tg = wave % WT, sg = wave / WT;
+    const int rr = lane & 15, gr = lane >> 4;
+    // The finishing lanes (wave kGuWaves, lane q < nr) read row q's bias of
+    // every selected expert early, all loads in flight together (the dword
+    // holding the element; decoded at the combine).
+    uint32_t BW[kMaxTopK];
+    int BSHF[kMaxTopK];
+    auto read_bias = [&]() {
+        uint32_t ba[kMaxTopK];
+#pragma unroll
+        for (int k = 0; k < kMaxTopK; ++k) {
+            const bool use = k < K && lane < nr && a.bias_dt >= 0;
+            ba[k] = use ? (uint32_t)eid[min(k, K - 1)] * (uint32_t)a.stride + (uint32_t)a.sec.dn_bias +
+                              (uint32_t)((r0 + lane) * bsz)
+                        : kOutOfRange;
+            BSHF[k] = (int)(ba[k] & 2u) * 8;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < kMaxTopK; ++k) BW[k] = __builtin_amdgcn_raw_buffer_load_b32(lr, ba[k] & ~3u, 0, 0);
+    };
+
     if (wave >= kGuWaves) {
-        // ---- 3a. the down stream (waves kGuWaves..): the workgroup's down
-        // rows, their scale bytes and biases straight into LDS by LDS-DMA.
-        // Piece c of DMA wave d is packed position (d + kDmaWaves*c) KiB of
-        // the per-expert windows [rows | scale bytes | biases] x top_k; pieces
-        // past the end read zeros into the spare chunk without a memory
-        // access.  These waves share each SIMD with a gate_up wave, which
-        // takes precedence in issuing, so the gate_up rows are queued first.
+        // ---- 2a. waves kGuWaves..: clear this workgroup's share of the next
+        // launch's exchange slot (its last readers finished with the previous
+        // launch), then wait until the gate_up waves have queued their last
+        // stage and queue this wave's down units behind them.
+        if (wave == kGuWaves + 1) {
+            uint64_t *nx = a.xchg + (size_t)((epoch1 + 1) & 1u) * kXSlotWords;
+            const int words = (kMaxTopK * F) >> 2, per = (words + (int)gridDim.x - 1) / (int)gridDim.x;
+            for (int i = lane; i < per; i += 64) {
+                const int w = b * per + i;
+                if (w < words) __hip_atomic_store(nx + w, kEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        if (wave == kGuWaves) read_bias();
         const int d = wave - kGuWaves;
-        const int total = K * swt;
-        const int nchunks = (total + kChunk - 1) / kChunk;
-        const int rbd = fb * 16;
-        const int s0 = r0 * fb, b0 = r0 * bsz;
-        const int s0a = s0 & ~15, b0a = b0 & ~15;
-        const int lim_w = nr * rbd, lim_s = (s0 - s0a) + nr * fb;
-        const int lim_b = a.bias_dt >= 0 ? (b0 - b0a) + nr * bsz : 0;
-        const uint32_t rel_w = (uint32_t)(a.sec.dn_blocks + (int64_t)r0 * rbd);
-        const uint32_t rel_s = (uint32_t)(a.sec.dn_scales + s0a) - (uint32_t)sww;
-        const uint32_t rel_b = (uint32_t)(a.sec.dn_bias + b0a) - (uint32_t)(sww + sws);
-        const float inv_swt = 1.0f / (float)swt;
-        // Wait until the gate_up waves have queued their last stage.
+        uint32_t va[NPD], vs[NSP];
+        {
+            const int r8 = lane >> 3, sl = lane & 7;
+#pragma unroll
+            for (int pp = 0; pp < NPD; ++pp) {
+                const int P = d + kDmaWaves * pp;
+                const int t = P / (2 * CH), c = (P >> 1) % CH, h = P & 1;
+                const int rho = 16 * t + 8 * h + r8, blk = 8 * c + (sl ^ r8);
+                const bool ok = rho < nrows_dn && blk < fb;
+                int k, q;
+                divmod_small(ok ? rho : 0, nr, inv_nr, k, q);
+                va[pp] = ok ? (uint32_t)eid[k] * (uint32_t)a.stride + (uint32_t)a.sec.dn_blocks +
+                                  (uint32_t)((r0 + q) * rbd + blk * 16)
+                            : kOutOfRange;
+            }
+#pragma unroll
+            for (int pp = 0; pp < NSP; ++pp) {
+                const int pos = (d + kDmaWaves * pp) * kChunk + lane * 16;
+                int k, o;
+                divmod_small(pos, sws, inv_sws, k, o);
+                const bool ok = k < K && o < shs + nr * fb;
+                vs[pp] = ok ? (uint32_t)eid[min(k, K - 1)] * (uint32_t)a.stride + (uint32_t)a.sec.dn_scales +
+                                  (uint32_t)(s0 - shs + o)
+                            : kOutOfRange;
+            }
+#pragma unroll
+            for (int pp = 0; pp < NPD; ++pp) asm volatile("" : "+v"(va[pp]));
+#pragma unroll
+            for (int pp = 0; pp < NSP; ++pp) asm volatile("" : "+v"(vs[pp]));
+        }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
+        // (the builtin's operands as plain locals: with an array element among
+        // them the host pass emitted no launch stub for the kernel)
 #pragma unroll
-        for (int c = 0; c < NDMA; ++c) {
-            const int chunk = d + kDmaWaves * c;
-            const int pos = chunk * kChunk + lane * 16;
-            int k, o;
-            divmod_small(pos, swt, inv_swt, k, o);
-            const uint32_t eo = (uint32_t)eid[min(k, K - 1)] * (uint32_t)a.stride;
-            const bool is_w = o < sww, is_s = !is_w && o < sww + sws;
-            const int lim = is_w ? lim_w : is_s ? lim_s + sww : lim_b + sww + sws;
-            const uint32_t rel = is_w ? rel_w : is_s ? rel_s : rel_b;
-            const bool ok = pos < total && o < lim;
-            const uint32_t voff = ok ? eo + rel + (uint32_t)o : kOutOfRange;
-            uint8_t *dst = lds8 + L.dma + (chunk < nchunks ? chunk : nchunks) * kChunk;
+        for (int pp = 0; pp < NPD; ++pp) {
+            const uint32_t voff = va[pp];
+            uint8_t *dst = lds8 + L.dma + (d + kDmaWaves * pp) * kChunk;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(lr, (l_void *)dst, 16, voff, 0, 0, 0);
+        }
+#pragma unroll
+        for (int pp = 0; pp < NSP; ++pp) {
+            const uint32_t voff = vs[pp];
+            uint8_t *dst = lds8 + L.scl + (d + kDmaWaves * pp) * kChunk;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(lr, (l_void *)dst, 16, voff, 0, 0, 0);
         }
     } else {
-        // ---- 3b. gate_up (waves 0..kGuWaves-1, one per SIMD): RGW rows a
+        // ---- 2b. gate_up (waves 0..kGuWaves-1, one per SIMD): RGW rows a
         // stage, a ring of D stages in flight (stage s + D issued once stage s
         // is consumed), widened and dotted as they land.  Rows past the share
         // read zeros without a memory access (buffer loads over the layer).
         constexpr int D = NSG < 2 ? NSG : 2;
         u32x4 W[D][MG];
-        uint32_t SC[D][MG];
+        uint32_t SCG[D][MG];
         uint32_t BW[D];
         int BSH[D];
 #define GW_ISSUE_STAGE(S)                                                                       \
@@ -340,7 +440,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             W[q_][m_] = __builtin_bit_cast(                                                     \
                 u32x4, __builtin_amdgcn_raw_buffer_load_b128(                                   \
                            lr, live_ ? row_ + (uint32_t)cb_ * 16 : kOutOfRange, 0, kNt));       \
-            SC[q_][m_] = __builtin_amdgcn_raw_buffer_load_b8(                                   \
+            SCG[q_][m_] = __builtin_amdgcn_raw_buffer_load_b8(                                  \
                 lr, live_ ? srow_ + (uint32_t)cb_ : kOutOfRange, 0, 0);                         \
         }                                                                                       \
         const uint32_t ba_ = a.bias_dt >= 0                                                     \
@@ -352,8 +452,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     } while (0)
         Unroll<0, D>::run([&](auto sc) { GW_ISSUE_STAGE(decltype(sc)::value); });
         // This lane's activation blocks into registers, read with ds_read_b128
-        // written out: the compiler would make an LDS read after an LDS-DMA
-        // wait for every load in flight; x was stored before the barrier above.
+        // written out (the x stores happened before the barrier above).
         uint4 X[MG][4];
         {
             const uint32_t xa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)xs;
@@ -388,7 +487,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
                 WBlock<XK> wb;
                 widen_v(W[q][m], wb);
                 float dd = block_dot_r<XK>(wb, X[m]);
-                dd *= decode_scale(SC[q][m]);
+                dd *= decode_scale(SCG[q][m]);
                 acc += use ? dd : 0.0f;
             }
             acc = seg_sum<TPG>(acc);
@@ -406,206 +505,227 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
                 __builtin_amdgcn_sched_barrier(0);
             }
             if constexpr (s == (NSG > D ? NSG - 1 - D : 0)) {
-                // the last stage is queued (or all were up front): the DMA
-                // waves may queue the down stream behind it
+                // the last stage is queued (or all were up front): the other
+                // waves may queue their down units behind it
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
             }
         });
 #undef GW_ISSUE_STAGE
-    }
-    // The gate_up waves count themselves done in LDS (their activations are
-    // written first); the publishing wave waits for the count instead of a
-    // barrier, which would also wait for the DMA waves still queuing the
-    // down stream.
-    if (wave < kGuWaves) {
+        // ---- 3. the activations out: the gate_up waves count themselves done
+        // in LDS (their activations are written first); wave 0 waits for the
+        // count and publishes the workgroup's words.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (lane == 0) __hip_atomic_fetch_add(gu_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         if (wave == 0) {
             while (__hip_atomic_load(gu_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
                    (unsigned)kGuWaves)
                 __builtin_amdgcn_s_sleep(1);
+            uint64_t *xw = a.xchg + (size_t)(epoch1 & 1u) * kXSlotWords;
+            if (lane < q1 - q0) {
+                uint64_t v = *reinterpret_cast<const uint64_t *>(actl + 4 * lane);
+                v = v == kEmpty ? v ^ 1ull : v;   // all-ones (four NaNs): another NaN
+                __hip_atomic_store(xw + q0 + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
 
-    // ---- 5. exchange ---------------------------------------------------------
-    // Workgroup b publishes its activations as XW 8-byte words, three
-    // fp16 values and the 16-bit launch tag each, with device-coherent stores;
-    // an aligned 8-byte store is seen whole or not at all, so the tag marks
-    // the word valid and no separate flag, wait or counter is needed.  The
-    // gate_up waves (no down stream of their own, so their loads are not
-    // queued behind it) then read all words, keeping those carrying this
-    // launch's tag and polling the rest (a bounded spin), and place the
-    // activations in LDS while the down stream still lands; the DMA waves
-    // wait for their part of it.  Every workgroup completes every launch, so
-    // all agree on the tag.
-    const int G = gridDim.x;
-    const int npair = K * F;
-    const unsigned pq = (unsigned)npair / (unsigned)G, pr = (unsigned)npair - pq * (unsigned)G;
-    const uint64_t tag = (uint64_t)(epoch1 & 0xFFFFu);
-    uint64_t *xw = a.xchg + (epoch1 % kDecodeXchgSlots) * kXSlotWords;
-    if (wave == 0 && 3 * lane < p1 - p0) {
-        uint64_t v = tag << 48;
-#pragma unroll
-        for (int e = 0; e < 3; ++e) {
-            const int j = 3 * lane + e;
-            v |= (uint64_t)(j < p1 - p0 ? actl[j] : 0) << (16 * e);
+    // ---- 4. the exchange: this wave's activation blocks into operand registers
+    // Lane (c, g) = lane c + 16 g holds, for each of the wave's steps s, the
+    // block 4s + g of expert rank c (c < K; other lanes hold zeros): the B
+    // operand of the unit's four MFMAs, one fp16 octet each.
+    {
+        unsigned spins = 0;
+        while (lds_peek(gu_done) < (unsigned)kGuWaves) {
+            if (++spins > a.spin_limit) break;    // cannot happen: the gate_up waves finish
+            __builtin_amdgcn_s_sleep(1);
         }
-        __hip_atomic_store(xw + b * XW + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t t_pub = wall_clock64();
+        while (wall_clock64() - t_pub < (uint64_t)PD) __builtin_amdgcn_s_sleep(2);
+    }
+    const int slot = a.poll_fault ? 2 : (int)(epoch1 & 1u);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        a.xchg + (size_t)slot * kXSlotWords, (short)0, kDecodeXchgSlotBytes, kRsrcWord3);
+    uint32_t boff[SPW];
+    u32x4 Bv[SPW][4];
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+        const int blk = 4 * (sg * SPW + j) + gr;
+        boff[j] = rr < K && blk < fb ? (uint32_t)((rr * F + 32 * blk) * 2) : kOutOfRange;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            Bv[j][m] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, boff[j] + 16u * m, 0, 0));
     }
     if (wave >= kGuWaves) {
-        __builtin_amdgcn_s_waitcnt(0);            // this wave's part of the down stream is in LDS
-    } else {
-        // Thread t reads word j = t % XW of workgroups t / XW +
-        // u * kPbStep.  The first round's loads are all issued before any
-        // LDS address is formed, so that work overlaps their latency.
-        constexpr int kPollT = kGuWaves * 64;
-        static_assert(XW <= kXWords && (XW & (XW - 1)) == 0, "slot words");
-        constexpr int WPT = kDecodeMaxGrid * XW / kPollT;        // words per thread
-        constexpr int kPbStep = kPollT / XW;
-        static_assert(WPT <= 32, "pending mask");
-        const int t = (int)threadIdx.x;
-        const int j = t % XW, pb0 = t / XW;
-        uint32_t pending = 0;
+        // the pieces were issued before the reads above, which complete in order
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * SPW) : "memory");
+        if (lane == 0) asm volatile("ds_add_u32 %0, %1" ::"v"((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)landed), "v"(1u) : "memory");
+    }
+    {
+        // Words still empty are read again past this chip's L2 (the first
+        // read may be served by an L2 line fetched before they were written).
+        uint32_t pend = 0;
 #pragma unroll
-        for (int u = 0; u < WPT; ++u) {
-            const int pb = pb0 + u * kPbStep;
-            const int np = (int)pq + (pb < (int)pr ? 1 : 0);
-            pending |= (uint32_t)((pb < G) & (3 * j < np)) << u;
-        }
-        {
-            const uint64_t t_pub = wall_clock64();
-            while (wall_clock64() - t_pub < (uint64_t)PD) __builtin_amdgcn_s_sleep(2);
-        }
-        // The first round may be served by this chip's L2 (the first of its
-        // compute units to read a line fetches it once for all); a word
-        // found stale there is read again past the L2.
-        uint64_t v[WPT];
+        for (int j = 0; j < SPW; ++j)
 #pragma unroll
-        for (int u = 0; u < WPT; ++u)
-            v[u] = (pending >> u) & 1u
-                       ? __hip_atomic_load(xw + t + u * kPollT, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_WAVEFRONT)
-                       : 0ull;
-        __builtin_amdgcn_sched_barrier(0);
-        // Word (pb, j) holds pairs pb * pq + min(pb, pr) + 3j .. +2 of the
-        // linear fp16 [top_k][inter] layout; they are written with ds_write
-        // written out, which waits only for this word's load.
-        const uint32_t as_addr = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)(lds8 + L.as);
+            for (int m = 0; m < 4; ++m)
+                pend |= pair_empty(Bv[j][m]) << (4 * j + m);
         unsigned spins = 0;
-        for (;;) {
-#pragma unroll
-            for (int u = 0; u < WPT; ++u) {
-                if (((pending >> u) & 1u) && (v[u] >> 48) == tag) {
-                    pending &= ~(1u << u);
-                    const int pb = pb0 + u * kPbStep;
-                    const int nv = (int)pq + (pb < (int)pr ? 1 : 0) - 3 * j;   // >= 1
-                    const uint32_t pair = __umul24((uint32_t)pb, pq) + (uint32_t)min(pb, (int)pr) +
-                                          (uint32_t)(3 * j);
-                    const uint32_t addr = as_addr + 2 * pair;
-                    const uint32_t lo = (uint32_t)v[u], hi = (uint32_t)(v[u] >> 32);
-                    asm volatile("ds_write_b16 %0, %1" ::"v"(addr), "v"(lo) : "memory");
-                    if (nv > 1) asm volatile("ds_write_b16_d16_hi %0, %1 offset:2" ::"v"(addr), "v"(lo) : "memory");
-                    if (nv > 2) asm volatile("ds_write_b16 %0, %1 offset:4" ::"v"(addr), "v"(hi) : "memory");
-                }
-            }
-            if (!pending) break;
-            if (++spins > kSpinLimit) {
-                atomicOr(a.sync.err, 1u);
+        bool gave_up = false;
+        while (pend) {
+            if (++spins > a.spin_limit) {
+                gave_up = true;
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-            for (int u = 0; u < WPT; ++u)
-                v[u] = (pending >> u) & 1u
-                           ? __hip_atomic_load(xw + t + u * kPollT, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT)
-                           : 0ull;
+            for (int j = 0; j < SPW; ++j)
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    if ((pend >> (4 * j + m)) & 1u)
+                        Bv[j][m] = __builtin_bit_cast(
+                            u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, boff[j] + 16u * m, 0, kSc1));
+#pragma unroll
+            for (int j = 0; j < SPW; ++j)
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    if (!pair_empty(Bv[j][m])) pend &= ~(1u << (4 * j + m));
         }
+        if (__ballot(gave_up) != 0ull && lane == 0) atomicAdd(a.sync.err, 1u);
     }
-    __syncthreads();
-
-    // ---- 6. down from LDS -------------------------------------------------------
-    // Groups of RPW rows (one per TPD-lane segment of a wave) of one expert;
-    // each wave takes a contiguous run of groups, so the blocks of its
-    // expert's activations that its lanes need are read from LDS into
-    // registers once per expert, not once per block.
     {
-        constexpr int RPW = SEGD;
-        const int segd = lane / TPD, tld = lane % TPD;
-        const int rbd = fb * 16;
-        const int shs = (r0 * fb) & 15, shb = (r0 * bsz) & 15;
-        const int gpk = (nr + RPW - 1) / RPW;            // groups per expert
-        const int ngroups = K * gpk;
-        const int gpw = (ngroups + kDW - 1) / kDW;       // groups per wave
-        const int g0 = wave * gpw, g1 = min(g0 + gpw, ngroups);
-        int kx = -1;
-        uint4 A[MD][4];
-        // (k, group within expert) advanced per group: no division in the loop
-        int k = g0 / gpk, qg = g0 - k * gpk;
-        for (int g = g0; g < g1; ++g) {
-            const int q = qg * RPW + segd;
-            const bool valid = q < nr;
-            const int qc = valid ? q : 0;
-            const uint8_t *wrow = lds8 + L.dma + k * swt + qc * rbd;
-            const uint8_t *srow = lds8 + L.dma + k * swt + sww + shs + qc * fb;
-            // this group's weight blocks and scale bytes, all read before use
-            u32x4 wv[MD];
-            uint32_t sv[MD];
+        unsigned spins = 0;
+        while (lds_peek(landed) < (unsigned)kDmaWaves) {
+            if (++spins > a.spin_limit) break;    // cannot happen: every DMA wave counts itself
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+
+    // ---- 5. down products of the wave's units on the matrix cores -------------
+    f32x4 acc[TPW][2];
+    float vf[TPW];
 #pragma unroll
-            for (int m = 0; m < MD; ++m) {
-                const int cb = tld + m * TPD;
-                const int cbc = valid && cb < fb ? cb : 0;
-                wv[m] = *reinterpret_cast<const u32x4 *>(wrow + cbc * 16);
-                sv[m] = srow[cbc];
+    for (int tt = 0; tt < TPW; ++tt) {
+        acc[tt][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        acc[tt][1] = acc[tt][0];
+        vf[tt] = 0.0f;
+    }
+    u32x4 RAW[UPW];
+    uint32_t SC[UPW];
+    bool sok[TPW];
+    {
+        const int r8 = rr & 7;
+#pragma unroll
+        for (int tt = 0; tt < TPW; ++tt) {
+            const int t = tg * TPW + tt, rho = 16 * t + rr;
+            sok[tt] = rho < nrows_dn;
+            int k, q;
+            divmod_small(sok[tt] ? rho : 0, nr, inv_nr, k, q);
+            const uint8_t *srow = lds8 + L.scl + k * sws + shs + q * fb;
+#pragma unroll
+            for (int j = 0; j < SPW; ++j) {
+                const int st = sg * SPW + j, i = j * TPW + tt;
+                const int blk = 4 * st + gr;
+                const int piece = (t * CH + (st >> 1)) * 2 + (rr >> 3);
+                const int slot = (4 * (st & 1) + gr) ^ r8;
+                RAW[i] = *reinterpret_cast<const u32x4 *>(lds8 + L.dma + piece * kChunk + r8 * 128 + slot * 16);
+                SC[i] = srow[blk < fb ? blk : 0];
             }
-            if (k != kx) {                                // wave-uniform
-                const uint32_t *xk = as + k * fb * 16;
+        }
+    }
+    uint32_t oor = 0;                    // units whose block this lane dots on the VALU
 #pragma unroll
-                for (int m = 0; m < MD; ++m) {
-                    const int cb = tld + m * TPD;
-                    const uint4 *xv = reinterpret_cast<const uint4 *>(xk + (cb < fb ? cb : 0) * 16);
+    for (int j = 0; j < SPW; ++j) {
+        const bool blk_ok = 4 * (sg * SPW + j) + gr < fb;
 #pragma unroll
-                    for (int qq = 0; qq < 4; ++qq) A[m][qq] = xv[qq];
+        for (int tt = 0; tt < TPW; ++tt) {
+            const int i = j * TPW + tt;
+            const uint32_t sb = SC[i] & 0xFFu;
+            const bool live = sok[tt] && blk_ok;
+            const bool inr = live && sb - 104u <= 36u;
+            oor |= (uint32_t)(live && !inr) << i;
+            const float scl = __uint_as_float((inr ? sb : 127u) << 23);
+            const uint32_t msk = inr ? ~0u : 0u;
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                acc[tt][m & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    widen_scaled(RAW[i][m] & msk, scl), __builtin_bit_cast(f16x8, Bv[j][m]),
+                    acc[tt][m & 1], 0, 0, 0);
+        }
+    }
+    const bool any_fb = __ballot(oor != 0u) != 0ull;
+    if (any_fb) {
+        // Scale bytes outside the fp16-exact range (rare): the block dotted on
+        // the VALU with its activations fetched from the lane of this row's
+        // expert, times the fp32 scale (referenceMXFP4's arithmetic).
+#pragma unroll
+        for (int j = 0; j < SPW; ++j)
+#pragma unroll
+            for (int tt = 0; tt < TPW; ++tt) {
+                const int i = j * TPW + tt;
+                if (__ballot((oor >> i) & 1u) == 0ull) continue;
+                int k, q;
+                divmod_small(16 * (tg * TPW + tt) + rr, nr, inv_nr, k, q);
+                const int src = (min(k, 15) + 16 * gr) * 4;
+                uint4 xa[4];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    xa[m].x = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)Bv[j][m].x);
+                    xa[m].y = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)Bv[j][m].y);
+                    xa[m].z = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)Bv[j][m].z);
+                    xa[m].w = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)Bv[j][m].w);
                 }
-                kx = k;
-            }
-            float acc = 0.0f;
-#pragma unroll
-            for (int m = 0; m < MD; ++m) {
-                const int cb = tld + m * TPD;
-                const bool use = valid && cb < fb;
                 WBlock<DT_F16> wb;
-                widen_v(wv[m], wb);
-                const float d = block_dot_r<DT_F16>(wb, A[m]) * decode_scale(sv[m]);
-                acc += use ? d : 0.0f;
+                widen_v(RAW[i], wb);
+                const float d = block_dot_r<DT_F16>(wb, xa) * decode_scale(SC[i] & 0xFFu);
+                vf[tt] += (oor >> i) & 1u ? d : 0.0f;
             }
-            acc = seg_sum<TPD>(acc);
-            if (valid && tld == 0) {
-                float bias = 0.0f;
-                if (a.bias_dt >= 0) {
-                    const uint8_t *bp = lds8 + L.dma + k * swt + sww + sws + shb + q * bsz;
-                    bias = a.bias_dt == DT_F32 ? *reinterpret_cast<const float *>(bp)
-                                               : load_as_f32(bp, a.bias_dt, 0);
-                }
-                vals[k * a.nrmax + q] = acc + bias;
-            }
-            if (++qg == gpk) {
-                qg = 0;
-                ++k;
-            }
+    }
+    // Partial sum of row rho = 16 t + r from its expert's column: lane l holds
+    // D[4 (l >> 4) + v][l & 15].
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+        const int t = tg * TPW + tt;
+        const f32x4 dsum = acc[tt][0] + acc[tt][1];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int rho = 16 * t + 4 * gr + v;
+            int k, q;
+            divmod_small(rho < nrows_dn ? rho : 0, nr, inv_nr, k, q);
+            if (rho < nrows_dn && k == rr) part[sg * 16 * TD + rho] = dsum[v];
+        }
+    }
+    if (any_fb) {
+        // the VALU blocks' sums of each row (its four lanes), added in a fixed order
+#pragma unroll
+        for (int tt = 0; tt < TPW; ++tt) {
+            float v = vf[tt];
+            v += __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ 16) * 4, __float_as_int(v)));
+            v += __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ 32) * 4, __float_as_int(v)));
+            const int rho = 16 * (tg * TPW + tt) + rr;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (gr == 0 && rho < nrows_dn) part[sg * 16 * TD + rho] += v;
         }
     }
     __syncthreads();
 
-    // Combine in router order: dst += out_k * w_k, the product and the sum
-    // rounded separately (expert_accumulate).  accumulate: 0 overwrite; 1 add
-    // to out (applyAssignments); 2 out += the finished sum (the residual add
-    // after the block, TransformerLayer.swift:232-238).
-    for (int q = threadIdx.x; q < nr; q += kDT) {
-        const int64_t o = r0 + q;
+    // ---- 6. bias and combine in router order: dst += out_k * w_k, the product
+    // and the sum rounded separately (expert_accumulate).  accumulate: 0
+    // overwrite; 1 add to out (applyAssignments); 2 out += the finished sum
+    // (the residual add after the block, TransformerLayer.swift:232-238).
+    if (wave == kGuWaves && lane < nr) {
+        const int64_t o = r0 + lane;
         float dst = a.accumulate == 1 ? a.out[o] : 0.0f;
-        for (int k = 0; k < K; ++k) dst = add_scaled_rn(dst, vals[k * a.nrmax + q], ew[k]);
+#pragma unroll
+        for (int k = 0; k < kMaxTopK; ++k) {
+            if (k < K) {
+                const int rho = k * nr + lane;
+                float v = part[rho];
+#pragma unroll
+                for (int g = 1; g < WS; ++g) v += part[g * 16 * TD + rho];
+                dst = add_scaled_rn(dst, v + bias_of(BW[k], BSHF[k], a.bias_dt), ew[k]);
+            }
+        }
         if (a.accumulate == 2) dst = a.out[o] + dst;
         a.out[o] = dst;
         if (a.out_bf16) a.out_bf16[o] = f32_to_bf16_bits(dst);
@@ -620,23 +740,24 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
 namespace {
 
 // Instantiations: GPT-OSS (hidden = intermediate = 2880: 90-block rows, up to
-// top-4: 90 gate_up rows a workgroup on 256 CUs, three 32-row stages) and
-// Qwen3-30B-A3B (2048 / 768: 64- and 24-block rows, up to top-8).
+// top-4: 88 or 96 gate_up rows a workgroup on 256 CUs in six 16-row stages;
+// 44 or 48 down rows in three tiles, 23 steps over eight step groups) and
+// Qwen3-30B-A3B (2048 / 768: 64- and 24-block rows, up to top-8: 48 gate_up
+// rows in three stages; 64 down rows in four tiles, each wave one tile and
+// three of the six steps).
 enum { kShapeGptOss = 0, kShapeQwen3 = 1 };
-constexpr int kNdma[2] = {20, 10};   // 1 KiB pieces per DMA wave
-// The first poll of the exchange waits this many ticks (10 ns) after the
-// workgroup published, measured best on MI355X: about the spread of the
-// grid's publish times (a round that comes too early costs a second memory
-// round trip), and for GPT-OSS also the time its own down stream, queued
-// ahead of the poll's loads, still takes to land.
-constexpr int kPollDelay[2] = {140, 40};
-// Words of a workgroup's exchange slot: GPT-OSS publishes up to 15 (45
-// activations at top-4 on 256 CUs), Qwen3 8 (24 at top-8), so two Qwen3
-// slots share a 128-byte line.  A poll's time follows the lines each compute
-// unit reads, so the slots are packed to the power of two that holds them.
-constexpr int kSlotWords[2] = {16, 8};
 constexpr int kStagesG[2] = {6, 3};
 constexpr int kRowsPerStage[2] = {kGuWaves * 64 / 16, kGuWaves * 64 / 16};
+constexpr int kTiles[2] = {3, 4};
+constexpr int kChunks[2] = {12, 3};
+constexpr int kScalePieces[2] = {2, 1};
+constexpr int kTileGroups[2] = {1, 4};
+constexpr int kStepsPerWave[2] = {3, 3};
+// The first read of the exchange waits this many ticks (10 ns) after the
+// workgroup's activations are out, measured best on MI355X: about the spread
+// of the grid's publish times (a read that comes too early costs a second
+// memory round trip).
+constexpr int kPollDelay[2] = {140, 40};
 
 int shape_of(int hidden, int inter)
 {
@@ -647,47 +768,56 @@ int shape_of(int hidden, int inter)
     return -1;
 }
 
-// Calls f(kernel) with the instantiation for (shape, x dtype).
-template <class F> void with_kernel(int shape, int x_dt, F &&f)
+#define GW_DECODE_KERNEL(S, XD)                                                                 \
+    decode_layer_kernel<XD, DShape<16, (S) == kShapeGptOss ? 6 : 4>, kStagesG[S], kTiles[S],   \
+                        kChunks[S], kScalePieces[S], kTileGroups[S], kStepsPerWave[S],         \
+                        kPollDelay[S]>
+
+typedef void (*DecodeKernel)(DecodeArgs);
+
+// The instantiation for (shape, x dtype).
+DecodeKernel kernel_for(int shape, int x_dt)
 {
-    if (shape == kShapeGptOss) {
-        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 6>, kStagesG[kShapeGptOss], DShape<32, 3>, kNdma[kShapeGptOss], kPollDelay[kShapeGptOss], kSlotWords[kShapeGptOss]>);
-        else f(decode_layer_kernel<DT_F16, DShape<16, 6>, kStagesG[kShapeGptOss], DShape<32, 3>, kNdma[kShapeGptOss], kPollDelay[kShapeGptOss], kSlotWords[kShapeGptOss]>);
-    } else {
-        if (x_dt == DT_BF16) f(decode_layer_kernel<DT_BF16, DShape<16, 4>, kStagesG[kShapeQwen3], DShape<8, 3>, kNdma[kShapeQwen3], kPollDelay[kShapeQwen3], kSlotWords[kShapeQwen3]>);
-        else f(decode_layer_kernel<DT_F16, DShape<16, 4>, kStagesG[kShapeQwen3], DShape<8, 3>, kNdma[kShapeQwen3], kPollDelay[kShapeQwen3], kSlotWords[kShapeQwen3]>);
-    }
+    if (shape == kShapeGptOss)
+        return x_dt == DT_BF16 ? &GW_DECODE_KERNEL(kShapeGptOss, DT_BF16)
+                               : &GW_DECODE_KERNEL(kShapeGptOss, DT_F16);
+    return x_dt == DT_BF16 ? &GW_DECODE_KERNEL(kShapeQwen3, DT_BF16)
+                           : &GW_DECODE_KERNEL(kShapeQwen3, DT_F16);
 }
 
 }  // namespace
+#undef GW_DECODE_KERNEL
 
 int decode_layer_plan(const Launch &L, int hidden, int inter, int x_dt, int top_k, int experts,
                       int64_t stride, int bias_dt, DecodeArgs *args, size_t *lds_bytes)
 {
+    (void)bias_dt;
     const int shape = shape_of(hidden, inter);
     if (shape < 0 || (x_dt != DT_BF16 && x_dt != DT_F16)) return 0;
     if (top_k < 1 || top_k > kMaxTopK || experts > 256 || experts < top_k) return 0;
     if ((int64_t)experts * stride >= (int64_t)kOutOfRange) return 0;   // 32-bit buffer offsets
     const int G = L.cus;
     if (G <= 0 || G > kDecodeMaxGrid) return 0;
-    // Each workgroup publishes at most 3 * XW activations.
-    if (((int64_t)top_k * inter + G - 1) / G > 3 * kSlotWords[shape]) return 0;
-    // Every workgroup's gate_up share must fit the register stages.
-    const int rows_g = 2 * (int)(((int64_t)top_k * inter + G - 1) / G);
-    if (rows_g > kStagesG[shape] * kRowsPerStage[shape]) return 0;
+    // A slot holds every word a launch of this width can publish.
+    if ((int64_t)kMaxTopK * inter * 2 > kDecodeXchgSlotBytes) return 0;
+    // Every workgroup's gate_up share (whole quads) must fit the register stages.
+    const int quads = (int)(((int64_t)top_k * inter / 4 + G - 1) / G);
+    if (8 * quads > kStagesG[shape] * kRowsPerStage[shape]) return 0;
+    // The down rows of every selected expert fit the tiles, the blocks the steps.
     const int nrmax = (hidden + G - 1) / G;
-    const int bsz = bias_dt == DT_F32 ? 4 : bias_dt >= 0 ? 2 : 0;
-    int sww, sws, swb;
-    decode_windows(hidden, inter, nrmax, bsz, sww, sws, swb);
-    const int swt = sww + sws + swb;
-    const int chunks = (top_k * swt + kChunk - 1) / kChunk;
-    if (chunks > kDmaWaves * kNdma[shape]) return 0;
-    const DecodeLds l = decode_lds(hidden, inter, top_k, nrmax, swt,
+    if (top_k * nrmax > 16 * kTiles[shape]) return 0;
+    const int wt = kTileGroups[shape], spw = kStepsPerWave[shape];
+    const int fb = inter / 32;
+    if ((fb + 3) / 4 > (8 / wt) * spw || (fb + 7) / 8 > kChunks[shape]) return 0;
+    // every expert's scale window (from a 16-byte aligned start) fits the pieces
+    const int sws_max = (nrmax * fb + 15 + 15) & ~15;
+    if (top_k * sws_max > (8 - kGuWaves) * kScalePieces[shape] * kChunk) return 0;
+    const DecodeLds l = decode_lds(hidden, kTiles[shape] * kChunks[shape] * 2,
+                                   (8 - kGuWaves) * kScalePieces[shape], (8 / wt) * 16 * kTiles[shape],
                                    kStagesG[shape] * kRowsPerStage[shape]);
     if (l.total > kDecodeLdsMax) return 0;
     // The exchange needs the whole grid resident: one workgroup per CU.
-    const void *fn = nullptr;
-    with_kernel(shape, x_dt, [&](auto k) { fn = reinterpret_cast<const void *>(k); });
+    const void *fn = reinterpret_cast<const void *>(kernel_for(shape, x_dt));
     static const void *attr_done[4] = {};
     int slot = -1;
     for (int i = 0; i < 4; ++i)
@@ -715,7 +845,8 @@ hipError_t launch_decode_layer(const Launch &L, int grid, size_t lds, int x_dt, 
 {
     const int shape = shape_of(a.hidden, a.inter);
     if (shape < 0 || grid <= 0) return hipErrorInvalidValue;
-    with_kernel(shape, x_dt, [&](auto kernel) { GW_LAUNCH(kernel, dim3(grid), dim3(kDT), lds, L, a); });
+    const DecodeKernel kernel = kernel_for(shape, x_dt);
+    GW_LAUNCH(kernel, dim3(grid), dim3(kDT), lds, L, a);
     return hipGetLastError();
 }
 

@@ -82,8 +82,11 @@ hipError_t launch_down(const Launch &L, const Plan *plan, int max_tokens, int ma
 constexpr int kSyncEpochCapacity = 8192;      // per-workgroup epochs a runner keeps
 constexpr int kDecodeLdsMax = 160 * 1024;     // LDS of one gfx950 compute unit
 constexpr int kDecodeMaxGrid = 256;           // workgroups of the one-kernel layer at most
-constexpr int kDecodeXchgSlots = 4;           // one-kernel layer's exchange: launches rotate
-constexpr int kDecodeXchgBytes = 32768 * kDecodeXchgSlots;   // over this many slots
+// The one-kernel layer's exchange: launches alternate between two slots of
+// 8-byte activation words (four fp16 each); a third slot is never written.
+constexpr int kDecodeXchgSlotBytes = 256 * 1024;
+constexpr int kDecodeXchgBytes = 3 * kDecodeXchgSlotBytes;
+constexpr uint32_t kDecodeSpinLimit = 1u << 18;   // polls before a wait gives up
 
 struct DecodeArgs {
     const float *logits;          // [experts] router logits of the token
@@ -97,7 +100,7 @@ struct DecodeArgs {
     int hidden, inter;
     Sections sec;
     int bias_dt;                  // -1: none
-    uint64_t *xchg;               // kDecodeXchgBytes of tagged activation words; zeroed once
+    uint64_t *xchg;               // kDecodeXchgBytes of activation words; all ones initially
     int act_kind;
     float limit, alpha;
     float *out;                   // [hidden]
@@ -105,8 +108,10 @@ struct DecodeArgs {
     int accumulate;               // 0 overwrite, 1 add to out, 2 residual: out += sum
     SyncArgs sync;
     int nrmax;                    // most down rows a workgroup owns (ceil(hidden / grid))
+    uint32_t spin_limit;          // polls of the exchange before a wait gives up
+    int poll_fault;               // 1: read the never-written slot (tests the give-up path)
 };
-struct DecodeLds { int route, xs, actl, dma, as, vals, total; };
+struct DecodeLds { int route, xs, actl, dma, scl, part, total; };
 
 // Grid (one workgroup per CU) of the one-kernel layer for this shape, or 0
 // when it is not available (shape, dtype or top-k not built, LDS, or the grid

@@ -50,7 +50,9 @@ typedef enum gw_status {
     GW_ERR_OOM = 3,         /* device allocation failed */
     GW_ERR_HIP = 4,         /* HIP runtime error (message has hipGetErrorString) */
     GW_ERR_NO_DEVICE = 5,   /* no HIP device / device index out of range */
-    GW_ERR_UNSUPPORTED = 6  /* valid request this build does not implement */
+    GW_ERR_UNSUPPORTED = 6, /* valid request this build does not implement */
+    GW_ERR_EXCHANGE = 7     /* a one-token layer's bounded wait gave up: see
+                               gw_expert_runner_sync_errors */
 } gw_status;
 
 typedef enum gw_dtype { GW_F32 = 0, GW_F16 = 1, GW_BF16 = 2 } gw_dtype;
@@ -406,16 +408,38 @@ int gw_moe_block_forward(gw_expert_runner *runner, const gw_moe_block_args *args
 
 /* For one token (the decode step of a single sequence) with 16-bit x the
  * layer above runs as ONE kernel, one workgroup per compute unit, whose
- * workgroups exchange the activations through device memory (shapes with
- * 65..96- or 25..64-block rows, top-k <= 8, up to 256 experts; other cases,
- * and GODWIT_DECODE_LAYER=0 in the environment when the runner is created,
- * use a gate_up and a down kernel).  The exchange's waits are bounded, and a
- * wait that gives up is counted here instead of hanging the device.  No
- * counterpart in the reference (there the command buffer's encoder
- * boundaries order the stages).  Blocks until the runner's stream is idle;
- * *count is the number of failed exchanges since the runner was created (0
- * when every result is valid). */
+ * workgroups exchange the activations through device memory.  Eligible:
+ * 16-bit x, top-k <= 8, up to 256 experts, and either GPT-OSS-class rows
+ * (hidden and intermediate both 65..96 blocks of 32) with top-k <= 4, or
+ * Qwen3-class rows (hidden 25..64 blocks, intermediate 9..24 blocks); other
+ * cases, and GODWIT_DECODE_LAYER=0 in the environment when the runner is
+ * created, use a gate_up and a down kernel.
+ *
+ * Co-residency contract: the kernel's workgroups wait for each other, so all
+ * of them must run at once.  The host checks that one workgroup fits each
+ * compute unit of an idle device; nothing else may run on the GPU during a
+ * one-token layer (no other stream, runner or process).  The waits are
+ * bounded: a wait that gives up is counted instead of hanging the device,
+ * and that launch's outputs are invalid.  gw_context_synchronize then
+ * returns GW_ERR_EXCHANGE, and the runner runs later one-token layers with
+ * the two-kernel form, which has no such wait.
+ *
+ * No counterpart in the reference (there the command buffer's encoder
+ * boundaries order the stages).  Blocks until the runner's stream is idle
+ * (GW_ERR_ARG during graph capture); *count is the number of waves whose
+ * wait gave up since the runner was created (0 when every result is valid). */
 int gw_expert_runner_sync_errors(gw_expert_runner *runner, uint32_t *count);
+
+/* The bounded wait of the one-token layer: polls of the exchange before a
+ * wait gives up (0 restores the default, 2^18, some milliseconds).  No
+ * counterpart in the reference. */
+int gw_expert_runner_set_wait_limit(gw_expert_runner *runner, uint32_t polls);
+
+/* Test hook for the failure path above: with enable != 0 the one-token
+ * layer's workgroups read an exchange slot that no launch writes, so every
+ * wait runs to its limit and gives up while every kernel still exits
+ * normally.  Never set in normal use.  No counterpart in the reference. */
+int gw_expert_runner_inject_exchange_fault(gw_expert_runner *runner, int enable);
 
 /* ---- graphs (replace per-call command buffers with one replayable graph) */
 

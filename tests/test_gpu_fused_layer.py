@@ -84,9 +84,11 @@ def test_fused_layer_equals_two_kernel_form(ctx, monkeypatch, shape, n_experts, 
     f_out, f16, f_ids, f_w = got["fused"]
     s_out, s16, s_ids, s_w = got["split"]
     assert np.array_equal(f_ids, s_ids) and np.array_equal(f_w, s_w)
-    if shape is QWEN3 or x_dtype == gw.F32:
+    if x_dtype == gw.F32:   # both runners use the two kernels
         assert np.array_equal(f_out, s_out) and np.array_equal(f16, s16)
     else:
+        # the one-kernel layer sums the down rows on the matrix cores, in
+        # another order than the two-kernel form's lanes: fp32 rounding only
         assert np.max(np.abs(f_out - s_out)) <= 1e-5 * np.max(np.abs(s_out))
     assert np.array_equal(f16, oracle.f32_to_bf16_bits(f_out))
     assert fused.sync_errors() == 0
