@@ -61,7 +61,6 @@ constexpr int kDT = 512;          // threads per workgroup
 constexpr int kDW = kDT / 64;     // waves per workgroup
 // Waves 0..kGuWaves-1 (one per SIMD) stream and compute the gate_up rows.
 constexpr int kGuWaves = 4;
-constexpr int kDmaWaves = kDW - kGuWaves;   // the others copy the down rows into LDS
 constexpr int kChunk = 1024;      // bytes one wave-wide 16-byte LDS-DMA moves
 constexpr int kRsrcWord3 = 0x00020000;   // raw (untyped) buffer access
 constexpr int kNt = 2;                   // buffer cache policy: non-temporal (streamed once)
@@ -86,17 +85,17 @@ template <int TPR_, int M_> struct DShape {
 }  // namespace
 
 // Byte layout of the kernel's LDS (host and device compute the same).
-// pieces / scale_pieces: 1 KiB pieces of the down rows and of their scale
-// bytes; parts: fp32 partial sums of the down rows (step groups x rows);
-// rows_per_wg: gate_up rows a workgroup can hold (its fp16 activations take
-// that many bytes at most).
+// pieces: 1 KiB pieces of the down rows (one per unit); scale_pieces: 1 KiB
+// pieces of their scale bytes; parts: fp32 partial sums of the down rows
+// (step groups x rows); rows_per_wg: gate_up rows a workgroup can hold (its
+// fp16 activations take that many bytes at most).
 __host__ __device__ inline DecodeLds decode_lds(int hidden, int pieces, int scale_pieces, int parts,
                                                int rows_per_wg)
 {
     DecodeLds l;
     const int hb = hidden / 32;
     l.route = 0;                                   // int32 ids[8], float w[8], counters
-    l.xs = 128;                                    // x, 20 dwords per block
+    l.xs = 256;                                    // x, 20 dwords per block
     l.actl = l.xs + hb * 80;                       // this workgroup's fp16 activations
     l.dma = (l.actl + rows_per_wg + 255) & ~255;   // down pieces (routing keys before them)
     l.scl = l.dma + (pieces > 1 ? pieces : 1) * kChunk;
@@ -169,14 +168,14 @@ __device__ __forceinline__ uint32_t pair_empty(const u32x4 &v)
 }  // namespace
 
 // XK: x dtype (bf16 or fp16).  GS: gate_up row shape (hidden wide).  NSG:
-// gate_up stages (of kGuWaves * 64 / TPR rows) a workgroup's share fills.
+// gate_up stages (of kGuWaves * 64 / TPR rows) a workgroup's share fills, GD
+// of them in flight per wave.
 // TD: 16-row tiles of down rows (the workgroup's rows of every selected
-// expert, expert-major); CH: 8-block chunks of a down row; NSP: 1 KiB pieces
-// of scale bytes each DMA wave copies.  WT: tile groups the waves are split
-// into (each wave takes TD / WT tiles); the kDW / WT step groups take SPW
-// steps of four blocks each.  PD: ticks of the 100 MHz real-time counter
-// between the activations being out and the first read of the exchange.
-template <int XK, class GS, int NSG, int TD, int CH, int NSP, int WT, int SPW, int PD>
+// expert, expert-major).  WT: tile groups the waves are split into (each
+// wave takes TD / WT tiles); the kDW / WT step groups take SPW steps of four
+// blocks each.  NSP: 1 KiB pieces of down scale bytes each DMA wave copies.  PD: ticks of the 100 MHz real-time counter between the
+// workgroup publishing its activations and its first read of the exchange.
+template <int XK, class GS, int NSG, int GD, int TD, int WT, int SPW, int NSP, int PD>
 __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
 {
     constexpr int TPG = GS::TPR, MG = GS::M, SEGG = 64 / TPG, RGW = kGuWaves * SEGG;
@@ -198,11 +197,13 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     slice_of(H, r0, r1);
     const int nr = r1 - r0;
     const int nrows_dn = K * nr;         // down rows, expert-major: row k * nr + q
-    const DecodeLds L = decode_lds(H, TD * CH * 2, (kDW - kGuWaves) * NSP, WS * 16 * TD, RGW * NSG);
+    const DecodeLds L = decode_lds(H, kDW * UPW, (kDW - kGuWaves) * NSP, WS * 16 * TD, RGW * NSG);
     int32_t *eid = reinterpret_cast<int32_t *>(lds8 + L.route);
     float *ew = reinterpret_cast<float *>(lds8 + L.route + 32);
     unsigned *gu_done = reinterpret_cast<unsigned *>(lds8 + L.route + 64);   // gate_up waves done
-    unsigned *landed = reinterpret_cast<unsigned *>(lds8 + L.route + 108);   // DMA waves landed
+    unsigned *ready = reinterpret_cast<unsigned *>(lds8 + L.route + 112);    // [4] gate_up waves' units landed
+    unsigned *t_pub = reinterpret_cast<unsigned *>(lds8 + L.route + 128);    // publish time (0: not yet)
+    unsigned *scl_in = reinterpret_cast<unsigned *>(lds8 + L.route + 132);   // DMA waves' scale pieces landed
     uint32_t *xs = reinterpret_cast<uint32_t *>(lds8 + L.xs);
     uint16_t *actl = reinterpret_cast<uint16_t *>(lds8 + L.actl);
     float *part = reinterpret_cast<float *>(lds8 + L.part);
@@ -239,9 +240,11 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             // flags a NaN
             const bool any_nan = __ballot(nan) != 0ull;
             if (lane <= K) rcount[lane] = lane == K && any_nan ? 1u : 0u;
-            if (lane == 0) *gu_done = 0u, *landed = 0u;
+            if (lane == 0) *gu_done = 0u, *t_pub = 0u, *scl_in = 0u;
+            if (lane < 4) ready[lane] = 0u;
         } else {
-            if (lane == 0) *gu_done = 0u, *landed = 0u;
+            if (lane == 0) *gu_done = 0u, *t_pub = 0u, *scl_in = 0u;
+            if (lane < 4) ready[lane] = 0u;
             int sid;
             float w;
             select_one<4>(a.logits, a.experts, K, sid, w);
@@ -314,25 +317,57 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     // ---- the down stream --------------------------------------------------------
     // The workgroup's down rows of every selected expert, expert-major (row
     // rho = k * nr + q is output row r0 + q of expert rank k), in tiles of 16
-    // rows.  Piece (t, c, h) (1 KiB) holds rows 16t + 8h .. +7 and blocks
-    // 8c .. 8c+7: row r8 at r8 * 128, block b in slot b ^ r8, so a DMA lane
-    // group copies one whole 128-byte line of a row, and an operand read of
-    // eight lanes (eight rows, one block each) touches every LDS bank once.
-    // The scale bytes follow as one window per expert (nr * fb bytes from a
-    // 16-byte aligned start).  The DMA waves copy it all and count themselves
-    // in LDS once their copies have landed.
-    constexpr int NPIECE = TD * CH * 2;
-    static_assert(NPIECE % kDmaWaves == 0, "pieces per DMA wave");
-    constexpr int NPD = NPIECE / kDmaWaves;
-    const int s0 = r0 * fb, shs = s0 & 15;
-    const int sws = (nr * fb + shs + 15) & ~15;   // scale window per expert
-    const float inv_nr = 1.0f / (float)nr, inv_sws = 1.0f / (float)sws;
+    // rows; a unit (t, s) is rows 16t..16t+15 x blocks 4s..4s+3.  The two
+    // waves of SIMD d (gate_up wave d, DMA wave kGuWaves + d) share tiles
+    // tg*TPW.. (tg = d % WT) and 2 * SPW steps from (d / WT) * 2 * SPW: the
+    // gate_up wave takes the first SPW, the DMA wave the rest; a wave's unit
+    // i = j * TPW + tt is tile tg*TPW + tt, the wave's j-th step.  The rows
+    // come in 1 KiB pieces of 8 rows x 8 blocks (a chunk): row r8 at r8 * 128,
+    // block b in slot b ^ r8, so a DMA lane group copies one whole 128-byte
+    // line of a row and an operand read of eight lanes (rows 0..7 or 8..15 of
+    // a tile, one block each) touches every LDS bank once.  DMA wave
+    // kGuWaves + d copies its SIMD's pieces chunk by chunk, flags its gate_up
+    // wave once that wave's chunks have landed, and widens its own units as
+    // theirs land; every wave widens its units' weights to fp16 in registers
+    // while the exchange is still in flight.
+    constexpr int PPS = TPW * SPW * 2;   // pieces per SIMD: SPW chunks x TPW tiles x 2 row halves
+    constexpr int CG = (SPW + 1) / 2;    // chunks holding the gate_up wave's steps
     const int rbd = fb * 16;
-    // Units: (t, s) = 16 rows x blocks 4s..4s+3.  Wave w takes tiles tg*TPW..
-    // and steps sg*SPW.. (tg = w % WT, sg = w / WT); operand lane l' reads row
-    // l' & 15, block 4s + (l' >> 4).
-    const int tg = wave % WT, sg = wave / WT;
+    const float inv_nr = 1.0f / (float)nr;
+    const int simd = wave & 3, kind = wave >> 2;
+    const int tg = simd % WT, sg = (simd / WT) * 2 + kind;   // tile group, step group
+    const int sbase = (simd / WT) * 2 * SPW;                  // the SIMD's first step
     const int rr = lane & 15, gr = lane >> 4;
+    // The scale bytes follow as one window per expert in LDS: nr * fb bytes
+    // from a 16-byte aligned start, expert k's at k * sws.  This lane's
+    // operand rows (one per tile): whether they exist and where their scale
+    // bytes sit in the window.
+    const int s0 = r0 * fb, shs = s0 & 15;
+    const int sws = (nr * fb + shs + 15) & ~15;
+    const float inv_sws = 1.0f / (float)sws;
+    uint32_t srow[TPW];
+    bool sok[TPW];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+        const int rho = 16 * (tg * TPW + tt) + rr;
+        sok[tt] = rho < nrows_dn;
+        int k, q;
+        divmod_small(sok[tt] ? rho : 0, nr, inv_nr, k, q);
+        srow[tt] = (uint32_t)(L.scl + k * sws + shs + q * fb);
+    }
+    // Layer offset of DMA lane `lane`'s 16 bytes of this SIMD's piece
+    // (chunk cl, tile tt, row half h).
+    auto piece_off = [&](int cl, int tt, int h) -> uint32_t {
+        const int t = tg * TPW + tt, c = sbase / 2 + cl;
+        const int r8 = lane >> 3, blk = 8 * c + ((lane & 7) ^ r8);
+        const int rho = 16 * t + 8 * h + r8;
+        const bool ok = rho < nrows_dn && blk < fb;
+        int k, q;
+        divmod_small(ok ? rho : 0, nr, inv_nr, k, q);
+        return ok ? (uint32_t)eid[k] * (uint32_t)a.stride + (uint32_t)a.sec.dn_blocks +
+                        (uint32_t)((r0 + q) * rbd + blk * 16)
+                  : kOutOfRange;
+    };
     // The finishing lanes (wave kGuWaves, lane q < nr) read row q's bias of
     // every selected expert early, all loads in flight together (the dword
     // holding the element; decoded at the combine).
@@ -368,59 +403,58 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         }
         if (wave == kGuWaves) read_bias();
         const int d = wave - kGuWaves;
-        uint32_t va[NPD], vs[NSP];
-        {
-            const int r8 = lane >> 3, sl = lane & 7;
+        uint32_t va[PPS], vs[NSP];
 #pragma unroll
-            for (int pp = 0; pp < NPD; ++pp) {
-                const int P = d + kDmaWaves * pp;
-                const int t = P / (2 * CH), c = (P >> 1) % CH, h = P & 1;
-                const int rho = 16 * t + 8 * h + r8, blk = 8 * c + (sl ^ r8);
-                const bool ok = rho < nrows_dn && blk < fb;
-                int k, q;
-                divmod_small(ok ? rho : 0, nr, inv_nr, k, q);
-                va[pp] = ok ? (uint32_t)eid[k] * (uint32_t)a.stride + (uint32_t)a.sec.dn_blocks +
-                                  (uint32_t)((r0 + q) * rbd + blk * 16)
-                            : kOutOfRange;
-            }
+        for (int cl = 0; cl < SPW; ++cl)
 #pragma unroll
-            for (int pp = 0; pp < NSP; ++pp) {
-                const int pos = (d + kDmaWaves * pp) * kChunk + lane * 16;
-                int k, o;
-                divmod_small(pos, sws, inv_sws, k, o);
-                const bool ok = k < K && o < shs + nr * fb;
-                vs[pp] = ok ? (uint32_t)eid[min(k, K - 1)] * (uint32_t)a.stride + (uint32_t)a.sec.dn_scales +
-                                  (uint32_t)(s0 - shs + o)
-                            : kOutOfRange;
-            }
+            for (int tt = 0; tt < TPW; ++tt)
 #pragma unroll
-            for (int pp = 0; pp < NPD; ++pp) asm volatile("" : "+v"(va[pp]));
+                for (int h = 0; h < 2; ++h) va[(cl * TPW + tt) * 2 + h] = piece_off(cl, tt, h);
 #pragma unroll
-            for (int pp = 0; pp < NSP; ++pp) asm volatile("" : "+v"(vs[pp]));
+        for (int pp = 0; pp < NSP; ++pp) {
+            const int pos = (d + (kDW - kGuWaves) * pp) * kChunk + lane * 16;
+            int k, o;
+            divmod_small(pos, sws, inv_sws, k, o);
+            const bool ok = k < K && o < shs + nr * fb;
+            vs[pp] = ok ? (uint32_t)eid[min(k, K - 1)] * (uint32_t)a.stride + (uint32_t)a.sec.dn_scales +
+                              (uint32_t)(s0 - shs + o)
+                        : kOutOfRange;
         }
+#pragma unroll
+        for (int i = 0; i < PPS; ++i) asm volatile("" : "+v"(va[i]));
+#pragma unroll
+        for (int pp = 0; pp < NSP; ++pp) asm volatile("" : "+v"(vs[pp]));
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         // (the builtin's operands as plain locals: with an array element among
         // them the host pass emitted no launch stub for the kernel)
 #pragma unroll
-        for (int pp = 0; pp < NPD; ++pp) {
-            const uint32_t voff = va[pp];
-            uint8_t *dst = lds8 + L.dma + (d + kDmaWaves * pp) * kChunk;
+        for (int pp = 0; pp < NSP; ++pp) {
+            const uint32_t voff = vs[pp];
+            uint8_t *dst = lds8 + L.scl + (d + (kDW - kGuWaves) * pp) * kChunk;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(lr, (l_void *)dst, 16, voff, 0, 0, 0);
         }
 #pragma unroll
-        for (int pp = 0; pp < NSP; ++pp) {
-            const uint32_t voff = vs[pp];
-            uint8_t *dst = lds8 + L.scl + (d + kDmaWaves * pp) * kChunk;
+        for (int i = 0; i < PPS; ++i) {
+            const uint32_t voff = va[i];
+            uint8_t *dst = lds8 + L.dma + (simd * PPS + i) * kChunk;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(lr, (l_void *)dst, 16, voff, 0, 0, 0);
         }
+        // the scale pieces have landed once only weight pieces are in flight,
+        // the gate_up wave's chunks once only the later chunks are
+        const uint32_t cnt_addr = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)scl_in;
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PPS) : "memory");
+        if (lane == 0) asm volatile("ds_add_u32 %0, %1" ::"v"(cnt_addr), "v"(1u) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((SPW - CG) * TPW * 2) : "memory");
+        if (lane == 0)
+            asm volatile("ds_write_b32 %0, %1" ::"v"((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)(ready + d)), "v"(1u) : "memory");
     } else {
         // ---- 2b. gate_up (waves 0..kGuWaves-1, one per SIMD): RGW rows a
         // stage, a ring of D stages in flight (stage s + D issued once stage s
         // is consumed), widened and dotted as they land.  Rows past the share
         // read zeros without a memory access (buffer loads over the layer).
-        constexpr int D = NSG < 2 ? NSG : 2;
+        constexpr int D = NSG < GD ? NSG : GD;
         u32x4 W[D][MG];
         uint32_t SCG[D][MG];
         uint32_t BW[D];
@@ -506,7 +540,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             }
             if constexpr (s == (NSG > D ? NSG - 1 - D : 0)) {
                 // the last stage is queued (or all were up front): the other
-                // waves may queue their down units behind it
+                // waves may queue the down units behind it
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -527,21 +561,32 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
                 v = v == kEmpty ? v ^ 1ull : v;   // all-ones (four NaNs): another NaN
                 __hip_atomic_store(xw + q0 + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
+            if (lane == 0) *t_pub = (uint32_t)wall_clock64() | 1u;
         }
     }
 
     // ---- 4. the exchange: this wave's activation blocks into operand registers
     // Lane (c, g) = lane c + 16 g holds, for each of the wave's steps s, the
     // block 4s + g of expert rank c (c < K; other lanes hold zeros): the B
-    // operand of the unit's four MFMAs, one fp16 octet each.
-    {
+    // operand of the unit's four MFMAs, one fp16 octet each.  A gate_up wave
+    // reads once its units' pieces are flagged, a DMA wave once it has flagged
+    // its gate_up wave's, both at least PD ticks after this workgroup
+    // published; the reads queue behind the down pieces still in flight.
+    if (wave < kGuWaves) {
         unsigned spins = 0;
-        while (lds_peek(gu_done) < (unsigned)kGuWaves) {
-            if (++spins > a.spin_limit) break;    // cannot happen: the gate_up waves finish
+        while (lds_peek(ready + wave) == 0u) {
+            if (++spins > a.spin_limit) break;    // cannot happen: the DMA wave flags them
             __builtin_amdgcn_s_sleep(1);
         }
-        const uint64_t t_pub = wall_clock64();
-        while (wall_clock64() - t_pub < (uint64_t)PD) __builtin_amdgcn_s_sleep(2);
+    }
+    {
+        unsigned spins = 0, tp;
+        while ((tp = lds_peek(t_pub)) == 0u) {
+            if (++spins > a.spin_limit) break;    // cannot happen: wave 0 publishes
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if constexpr (PD > 0)
+            while ((uint32_t)wall_clock64() - tp < (uint32_t)PD) __builtin_amdgcn_s_sleep(2);
     }
     const int slot = a.poll_fault ? 2 : (int)(epoch1 & 1u);
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
@@ -550,17 +595,103 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     u32x4 Bv[SPW][4];
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
-        const int blk = 4 * (sg * SPW + j) + gr;
+        const int blk = 4 * (sbase + kind * SPW + j) + gr;
         boff[j] = rr < K && blk < fb ? (uint32_t)((rr * F + 32 * blk) * 2) : kOutOfRange;
 #pragma unroll
         for (int m = 0; m < 4; ++m)
             Bv[j][m] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, boff[j] + 16u * m, 0, 0));
     }
-    if (wave >= kGuWaves) {
-        // the pieces were issued before the reads above, which complete in order
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * SPW) : "memory");
-        if (lane == 0) asm volatile("ds_add_u32 %0, %1" ::"v"((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)landed), "v"(1u) : "memory");
+    // ---- 5. this wave's units widened to fp16 while the exchange is in flight
+    // A DMA wave takes each of its own pieces as it lands (the vector-memory
+    // counter completes in order: piece i is in once only the later pieces
+    // and the exchange reads are outstanding); a gate_up wave's are all in.
+    // ds_read_b128 written out: the compiler would make each read wait for
+    // every load in flight.
+    f16x8 AH[UPW][4];
+    uint32_t SC[UPW];                    // the units' scale bytes
+    uint32_t oor = 0;                    // units whose block this lane dots on the VALU
+    {
+        // operand lane: row rr of the tile (piece half rr >> 3, row rr & 7),
+        // block gr of the step's four (slot (4 (step & 1) + gr) ^ (rr & 7))
+        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)(lds8 + L.dma) +
+                              (uint32_t)(simd * PPS * kChunk + (rr >> 3) * kChunk + (rr & 7) * 128);
+        const bool dma_wave = wave >= kGuWaves;
+        {
+            unsigned spins = 0;
+            while (lds_peek(scl_in) < (unsigned)(kDW - kGuWaves)) {
+                if (++spins > a.spin_limit) break;    // cannot happen: every DMA wave counts itself
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        // the unit's weights and scale byte: an address per lane, then the
+        // widening (a gate_up wave reads all its units first, with one wait)
+        auto unit_addr = [&](int j, int tt, uint32_t &wa, uint32_t &sa, bool &live) {
+            const int sl = kind * SPW + j, blk = 4 * (sbase + sl) + gr;
+            live = sok[tt] && blk < fb;
+            wa = base + (uint32_t)(((sl >> 1) * TPW + tt) * 2 * kChunk + 16 * ((4 * (sl & 1) + gr) ^ (rr & 7)));
+            sa = srow[tt] + (uint32_t)(live ? blk : 0);
+        };
+        auto widen_unit = [&](int i, int tt, u32x4 w, uint32_t sb, bool live) {
+            SC[i] = sb;
+            const bool inr = live && sb - 104u <= 36u;
+            oor |= (uint32_t)(live && !inr) << i;
+            const float scl = __uint_as_float((inr ? sb : 127u) << 23);
+            const uint32_t msk = inr ? ~0u : 0u;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                AH[i][m] = widen_scaled(w[m] & msk, scl);
+                asm volatile("" : "+v"(AH[i][m]));   // widened now, not after the later waits
+            }
+        };
+        if (dma_wave) {
+            Unroll<0, UPW>::run([&](auto ic) {
+                constexpr int i = decltype(ic)::value, j = i / TPW, tt = i % TPW;
+                // a DMA wave's unit has landed once only later chunks' pieces
+                // and the exchange reads are in flight
+                if constexpr (j == 0 || ((SPW + j) >> 1) != ((SPW + j - 1) >> 1)) {
+                    constexpr int later = SPW - 1 - ((SPW + j) >> 1);
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(later * TPW * 2 + 4 * SPW) : "memory");
+                }
+                uint32_t wa, sa;
+                bool live;
+                unit_addr(j, tt, wa, sa, live);
+                u32x4 w;
+                uint32_t sb;
+                asm volatile("ds_read_b128 %0, %2\n\tds_read_u8 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                             : "=v"(w), "=v"(sb) : "v"(wa), "v"(sa) : "memory");
+                widen_unit(i, tt, w, sb, live);
+            });
+        } else {
+            u32x4 w[UPW];
+            uint32_t sb[UPW];
+            bool live[UPW];
+#pragma unroll
+            for (int i = 0; i < UPW; ++i) {
+                uint32_t wa, sa;
+                unit_addr(i / TPW, i % TPW, wa, sa, live[i]);
+                u32x4 wv;
+                uint32_t sv;
+                asm volatile("ds_read_b128 %0, %2\n\tds_read_u8 %1, %3"
+                             : "=v"(wv), "=v"(sv) : "v"(wa), "v"(sa) : "memory");
+                w[i] = wv;
+                sb[i] = sv;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int i = 0; i < UPW; ++i) {
+                u32x4 wv = w[i];
+                uint32_t sv = sb[i];
+                asm volatile("" : "+v"(wv), "+v"(sv));   // loaded by the wait above
+                widen_unit(i, i % TPW, wv, sv, live[i]);
+            }
+        }
     }
+    // the exchange reads are looked at only now, after the widening (the
+    // compiler would hoist the check, and its wait for them, above it)
+#pragma unroll
+    for (int j = 0; j < SPW; ++j)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) asm volatile("" : "+v"(Bv[j][m]));
     {
         // Words still empty are read again past this chip's L2 (the first
         // read may be served by an L2 line fetched before they were written).
@@ -593,15 +724,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         }
         if (__ballot(gave_up) != 0ull && lane == 0) atomicAdd(a.sync.err, 1u);
     }
-    {
-        unsigned spins = 0;
-        while (lds_peek(landed) < (unsigned)kDmaWaves) {
-            if (++spins > a.spin_limit) break;    // cannot happen: every DMA wave counts itself
-            __builtin_amdgcn_s_sleep(1);
-        }
-    }
-
-    // ---- 5. down products of the wave's units on the matrix cores -------------
+    // ---- 6. down products on the matrix cores -------------------------------
     f32x4 acc[TPW][2];
     float vf[TPW];
 #pragma unroll
@@ -610,54 +733,20 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         acc[tt][1] = acc[tt][0];
         vf[tt] = 0.0f;
     }
-    u32x4 RAW[UPW];
-    uint32_t SC[UPW];
-    bool sok[TPW];
-    {
-        const int r8 = rr & 7;
 #pragma unroll
-        for (int tt = 0; tt < TPW; ++tt) {
-            const int t = tg * TPW + tt, rho = 16 * t + rr;
-            sok[tt] = rho < nrows_dn;
-            int k, q;
-            divmod_small(sok[tt] ? rho : 0, nr, inv_nr, k, q);
-            const uint8_t *srow = lds8 + L.scl + k * sws + shs + q * fb;
+    for (int j = 0; j < SPW; ++j)
 #pragma unroll
-            for (int j = 0; j < SPW; ++j) {
-                const int st = sg * SPW + j, i = j * TPW + tt;
-                const int blk = 4 * st + gr;
-                const int piece = (t * CH + (st >> 1)) * 2 + (rr >> 3);
-                const int slot = (4 * (st & 1) + gr) ^ r8;
-                RAW[i] = *reinterpret_cast<const u32x4 *>(lds8 + L.dma + piece * kChunk + r8 * 128 + slot * 16);
-                SC[i] = srow[blk < fb ? blk : 0];
-            }
-        }
-    }
-    uint32_t oor = 0;                    // units whose block this lane dots on the VALU
-#pragma unroll
-    for (int j = 0; j < SPW; ++j) {
-        const bool blk_ok = 4 * (sg * SPW + j) + gr < fb;
-#pragma unroll
-        for (int tt = 0; tt < TPW; ++tt) {
-            const int i = j * TPW + tt;
-            const uint32_t sb = SC[i] & 0xFFu;
-            const bool live = sok[tt] && blk_ok;
-            const bool inr = live && sb - 104u <= 36u;
-            oor |= (uint32_t)(live && !inr) << i;
-            const float scl = __uint_as_float((inr ? sb : 127u) << 23);
-            const uint32_t msk = inr ? ~0u : 0u;
+        for (int tt = 0; tt < TPW; ++tt)
 #pragma unroll
             for (int m = 0; m < 4; ++m)
                 acc[tt][m & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    widen_scaled(RAW[i][m] & msk, scl), __builtin_bit_cast(f16x8, Bv[j][m]),
-                    acc[tt][m & 1], 0, 0, 0);
-        }
-    }
+                    AH[j * TPW + tt][m], __builtin_bit_cast(f16x8, Bv[j][m]), acc[tt][m & 1], 0, 0, 0);
     const bool any_fb = __ballot(oor != 0u) != 0ull;
     if (any_fb) {
         // Scale bytes outside the fp16-exact range (rare): the block dotted on
         // the VALU with its activations fetched from the lane of this row's
         // expert, times the fp32 scale (referenceMXFP4's arithmetic).
+        const uint8_t *pbase = lds8 + L.dma + simd * PPS * kChunk + (rr >> 3) * kChunk + (rr & 7) * 128;
 #pragma unroll
         for (int j = 0; j < SPW; ++j)
 #pragma unroll
@@ -675,8 +764,11 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
                     xa[m].z = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)Bv[j][m].z);
                     xa[m].w = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)Bv[j][m].w);
                 }
+                const int sl = kind * SPW + j;
                 WBlock<DT_F16> wb;
-                widen_v(RAW[i], wb);
+                widen_v(*reinterpret_cast<const u32x4 *>(pbase + ((sl >> 1) * TPW + tt) * 2 * kChunk +
+                                                          16 * ((4 * (sl & 1) + gr) ^ (rr & 7))),
+                        wb);
                 const float d = block_dot_r<DT_F16>(wb, xa) * decode_scale(SC[i] & 0xFFu);
                 vf[tt] += (oor >> i) & 1u ? d : 0.0f;
             }
@@ -709,7 +801,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     }
     __syncthreads();
 
-    // ---- 6. bias and combine in router order: dst += out_k * w_k, the product
+    // ---- 7. bias and combine in router order: dst += out_k * w_k, the product
     // and the sum rounded separately (expert_accumulate).  accumulate: 0
     // overwrite; 1 add to out (applyAssignments); 2 out += the finished sum
     // (the residual add after the block, TransformerLayer.swift:232-238).
@@ -747,17 +839,18 @@ namespace {
 // three of the six steps).
 enum { kShapeGptOss = 0, kShapeQwen3 = 1 };
 constexpr int kStagesG[2] = {6, 3};
+constexpr int kRingG[2] = {2, 2};         // gate_up stages in flight per wave
 constexpr int kRowsPerStage[2] = {kGuWaves * 64 / 16, kGuWaves * 64 / 16};
 constexpr int kTiles[2] = {3, 4};
-constexpr int kChunks[2] = {12, 3};
-constexpr int kScalePieces[2] = {2, 1};
 constexpr int kTileGroups[2] = {1, 4};
 constexpr int kStepsPerWave[2] = {3, 3};
-// The first read of the exchange waits this many ticks (10 ns) after the
-// workgroup's activations are out, measured best on MI355X: about the spread
-// of the grid's publish times (a read that comes too early costs a second
-// memory round trip).
-constexpr int kPollDelay[2] = {140, 40};
+constexpr int kScalePieces[2] = {2, 1};   // per DMA wave
+// The first read of the exchange waits at least this many ticks (10 ns)
+// after the workgroup published (a read that comes before the slowest
+// publisher costs a second round trip).  Measured on MI355X: GPT-OSS spans
+// the same from 0 to 1 us (the reads queue behind the down pieces anyway);
+// Qwen3 0.3 us is best.
+constexpr int kPollDelay[2] = {60, 30};
 
 int shape_of(int hidden, int inter)
 {
@@ -769,9 +862,8 @@ int shape_of(int hidden, int inter)
 }
 
 #define GW_DECODE_KERNEL(S, XD)                                                                 \
-    decode_layer_kernel<XD, DShape<16, (S) == kShapeGptOss ? 6 : 4>, kStagesG[S], kTiles[S],   \
-                        kChunks[S], kScalePieces[S], kTileGroups[S], kStepsPerWave[S],         \
-                        kPollDelay[S]>
+    decode_layer_kernel<XD, DShape<16, (S) == kShapeGptOss ? 6 : 4>, kStagesG[S], kRingG[S], kTiles[S], \
+                        kTileGroups[S], kStepsPerWave[S], kScalePieces[S], kPollDelay[S]>
 
 typedef void (*DecodeKernel)(DecodeArgs);
 
@@ -808,13 +900,11 @@ int decode_layer_plan(const Launch &L, int hidden, int inter, int x_dt, int top_
     if (top_k * nrmax > 16 * kTiles[shape]) return 0;
     const int wt = kTileGroups[shape], spw = kStepsPerWave[shape];
     const int fb = inter / 32;
-    if ((fb + 3) / 4 > (8 / wt) * spw || (fb + 7) / 8 > kChunks[shape]) return 0;
+    if ((fb + 3) / 4 > (8 / wt) * spw) return 0;
     // every expert's scale window (from a 16-byte aligned start) fits the pieces
-    const int sws_max = (nrmax * fb + 15 + 15) & ~15;
-    if (top_k * sws_max > (8 - kGuWaves) * kScalePieces[shape] * kChunk) return 0;
-    const DecodeLds l = decode_lds(hidden, kTiles[shape] * kChunks[shape] * 2,
-                                   (8 - kGuWaves) * kScalePieces[shape], (8 / wt) * 16 * kTiles[shape],
-                                   kStagesG[shape] * kRowsPerStage[shape]);
+    if (top_k * ((nrmax * fb + 15 + 15) & ~15) > (8 - kGuWaves) * kScalePieces[shape] * kChunk) return 0;
+    const DecodeLds l = decode_lds(hidden, 8 * (kTiles[shape] / wt) * spw, (8 - kGuWaves) * kScalePieces[shape],
+                                   (8 / wt) * 16 * kTiles[shape], kStagesG[shape] * kRowsPerStage[shape]);
     if (l.total > kDecodeLdsMax) return 0;
     // The exchange needs the whole grid resident: one workgroup per CU.
     const void *fn = reinterpret_cast<const void *>(kernel_for(shape, x_dt));
