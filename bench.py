@@ -14,12 +14,16 @@ blocks is outside the timed path).  Weights are seeded synthetic MXFP4
 Prints ONE JSON line (the driver's contract).  `value` is whole-job algorithmic
 HBM throughput in GB/s: every selected expert's packed nibbles, scales and bf16
 biases, plus the logits, activations and outputs, per token, divided by the
-wall time per token measured around the timed steps.  The `roofline` object
-covers the dominant kernel (fused gate_up) timed with hipEvents on the
-library's stream; `cpu_baseline` is the CPU oracle (a scalar port of the
-reference's CPU path) on a bounded sample of the same workload, one thread,
-with the same port's GEMV rows split over the host's cores beside it
-(`all_cores`).
+wall time per token of the median timing round.  The timed steps run as the
+reference's protocol does (DequantGEMVBenchmark.swift:290-322): 7 rounds of
+--steps tokens each, every round bracketed by a device synchronisation, the
+median round reported beside the min and max.  The `roofline` object covers
+the dominant kernel (decode_layer_kernel, the one-kernel MoE layer) timed
+with hipEvents on the library's stream; `sync_errors` counts the layer
+kernel's failed exchange waits (the run fails if there is any);
+`cpu_baseline` is the CPU oracle (a scalar port of the reference's CPU path)
+on a bounded sample of the same workload, one thread, with the same port's
+GEMV rows split over the host's cores beside it (`all_cores`).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -62,19 +66,36 @@ def gate_up_bytes(lay) -> int:
 
 
 COUNTER_LAYERS = L
-# HBM bytes per gate_up_kernel launch (GPT-OSS-120B layer, batch 1): rocprofv3
-# FETCH_SIZE + WRITE_SIZE per dispatch from `bench.py --counter-pass 256`, each
-# scaled by what the counter reads for a 256 MiB device-to-device copy
-# (profiles/decode_gate_up_down_traffic.md).
-GATE_UP_TRAFFIC_BYTES = 35_944_526
-# The same for the prefill gate_up GEMM launch (512 tokens, seed 1):
-# `bench.py --workload prefill` under rocprofv3 --pmc, the copy scale of the
-# decode run (profiles/prefill_gemm_gptoss_512.md).
-PREFILL_GATE_UP_TRAFFIC_BYTES = 1_238_312_316
-# HBM bytes per decode_layer_kernel launch (the one-kernel layer, GPT-OSS-120B,
-# batch 1), measured as above over the whole 36-layer stack
-# (profiles/decode_layer_traffic.md).
-DECODE_LAYER_TRAFFIC_BYTES = 54_362_786
+# Measured HBM bytes per launch of a roofline kernel: rocprofv3 FETCH_SIZE and
+# WRITE_SIZE per dispatch (separate --pmc runs), each scaled by what the
+# counter reads for a 256 MiB device-to-device copy.  Each figure is tied to
+# the SHA-256 (first 16 hex digits) of the kernel source it was measured on:
+# a run whose source differs reports `traffic: null` rather than a stale
+# number.
+#   gate_up_kernel, GPT-OSS-120B layer, batch 1 (profiles/decode_gate_up_down_traffic.md)
+GATE_UP_TRAFFIC = (35_944_526, "gw_kernels.hip", None)
+#   prefill gate_up GEMM, 512 tokens, seed 1 (profiles/prefill_gemm_gptoss_512.md)
+PREFILL_GATE_UP_TRAFFIC = (1_238_312_316, "gw_prefill.hip", "76b214d588f4f005")
+#   decode_layer_kernel (the one-kernel layer), GPT-OSS-120B, batch 1, over the
+#   whole 36-layer stack (profiles/decode_layer_traffic.md)
+DECODE_LAYER_TRAFFIC = (54_362_786, "gw_decode.hip", "64716d5f32a86341")
+
+
+def source_sha16(name: str) -> str:
+    import hashlib
+    with open(os.path.join(ROOT, "godwit_amd", "csrc", name), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def measured_traffic(entry) -> dict:
+    """The `traffic` figure for the roofline object and where it came from:
+    the bytes when the kernel source is the one they were measured on."""
+    nbytes, src, sha = entry
+    cur = source_sha16(src)
+    if sha is not None and cur == sha:
+        return {"traffic": nbytes, "traffic_source": f"{src} {sha}"}
+    return {"traffic": None,
+            "traffic_source": f"not measured on this {src} ({cur}); see profiles/"}
 
 
 def build_model(ctx, gw, lay, seed: int):
@@ -287,6 +308,7 @@ def gptoss20b_bench(gw, args) -> int:
                 kernels[name] = {"launches": n, "avg_us": ms / n * 1e3}
         ctx.set_profiling(False)
         log("kernels: " + ", ".join(f"{k} {v['avg_us']:.2f} us" for k, v in kernels.items()))
+    sync_err = runner.sync_errors()
     nbytes = K * expert_bytes(lay) + E20 * H * 4 + H * 2 + H * 4 + H * 2
     value = nbytes / dt / 1e9
     log(f"gpt-oss-20b layer: {dt * 1e6:.2f} us per layer, {value:.0f} GB/s "
@@ -311,8 +333,8 @@ def gptoss20b_bench(gw, args) -> int:
                   "router, batch 1",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(dt * ncopy * 1e3, 4),
-        "us_per_layer": round(dt * 1e6, 2), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32",
+        "us_per_layer": round(dt * 1e6, 2), "sync_errors": sync_err, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "compute": "e2m1 weights (MXFP4, exact) x bf16 activations, fp32 products and sums; "
                    "fp32 router",
         "data": "synthetic (seeded MXFP4, biases N(0,0.02) bf16, router fp32 N(0,0.02), "
@@ -327,11 +349,18 @@ def gptoss20b_bench(gw, args) -> int:
     return 0
 
 
+def host_cpus() -> dict:
+    """The host's CPU counts: all logical CPUs, the ones this process may run
+    on (affinity), and OMP_NUM_THREADS when set."""
+    omp = os.environ.get("OMP_NUM_THREADS")
+    return {"os_cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "omp_num_threads": int(omp) if omp and omp.isdigit() else None}
+
+
 def host_threads() -> int:
-    """Host threads for the all-core CPU baseline: the process's CPU share
-    (OMP_NUM_THREADS when set, else the affinity mask), at most 16."""
-    n = int(os.environ.get("OMP_NUM_THREADS") or 0) or len(os.sched_getaffinity(0))
-    return max(1, min(16, n))
+    """Host threads for the all-core CPU baseline: every CPU this process may
+    run on (its affinity mask)."""
+    return max(1, len(os.sched_getaffinity(0)))
 
 
 def cpu_baseline(seconds: float, threads: int = 1) -> dict:
@@ -373,22 +402,23 @@ def cpu_baseline(seconds: float, threads: int = 1) -> dict:
             "threads": threads}
 
 
-def timed_rounds(steps: int, run_step, sync, window: int = 20):
-    """The reference's timing protocol (DequantGEMVBenchmark.swift:290-322: 7 rounds,
-    median reported): the `steps` timed steps run as max(1, steps // window)
-    consecutive rounds of about `window` steps, each bracketed by a device
-    synchronisation.  Returns (per-step seconds of each round, total seconds)."""
-    n_rounds = max(1, steps // window)
-    bounds = [steps * i // n_rounds for i in range(n_rounds + 1)]
+TIMING_ROUNDS = 7   # DequantGEMVBenchmark.timingRounds
+
+
+def timed_rounds(steps: int, run_step, sync, rounds: int = TIMING_ROUNDS):
+    """The reference's timing protocol (DequantGEMVBenchmark.swift:290-322):
+    `rounds` consecutive rounds of `steps` steps each (step indices run on
+    across rounds), each bracketed by a device synchronisation.  Returns
+    (per-step seconds of each round, total seconds)."""
     per_step = []
     sync()
     t0 = time.perf_counter()
-    for i in range(n_rounds):
+    for i in range(rounds):
         tr = time.perf_counter()
-        for j in range(bounds[i], bounds[i + 1]):
+        for j in range(i * steps, (i + 1) * steps):
             run_step(j)
         sync()
-        per_step.append((time.perf_counter() - tr) / (bounds[i + 1] - bounds[i]))
+        per_step.append((time.perf_counter() - tr) / steps)
     return per_step, time.perf_counter() - t0
 
 
@@ -397,6 +427,34 @@ def round_stats(per_step, scale: float) -> dict:
     v = sorted(x * scale for x in per_step)
     return {"rounds": len(v), "median": round(v[len(v) // 2], 3), "min": round(v[0], 3),
             "max": round(v[-1], 3)}
+
+
+def prefill_cpu_baseline(seconds: float, logits: np.ndarray) -> dict:
+    """The oracle's MoE layer (as in cpu_baseline) on the first tokens of the
+    prefill workload, one at a time, until `seconds` have elapsed: the tokens'
+    own Zipf-routed top-4 of 128 experts, whose slots point into a pool of 32
+    distinct synthetic experts (slot e is pool entry e mod 32)."""
+    import oracle
+    r = np.random.default_rng(78)
+    pool = []
+    for _ in range(32):
+        pool.append(oracle.Expert(
+            r.integers(0, 256, 2 * F * H // 2, dtype=np.uint8),
+            r.integers(119, 128, 2 * F * H // 32, dtype=np.uint8),
+            r.integers(0, 256, H * F // 2, dtype=np.uint8),
+            r.integers(119, 128, H * F // 32, dtype=np.uint8),
+            oracle.round_to_bf16((r.standard_normal(2 * F) * 0.02).astype(np.float32)),
+            oracle.round_to_bf16((r.standard_normal(H) * 0.02).astype(np.float32))))
+    slots = [pool[e % 32] for e in range(E)]
+    tokens, t0 = 0, time.perf_counter()
+    while True:
+        x = oracle.round_to_bf16(r.standard_normal((1, H)).astype(np.float32))
+        oracle.moe_layer(slots, K, logits[tokens % len(logits)][None, :], x, H, F)
+        tokens += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            break
+    return {"tokens": tokens, "seconds": dt, "tokens_per_s": tokens / dt}
 
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 matrix peak
@@ -478,6 +536,14 @@ def prefill_bench(gw, args) -> int:
         f"{flops / dt / 1e12:.1f} TFLOP/s algorithmic")
     if kernels:
         log("kernels: " + ", ".join(f"{k} {v['avg_us']:.2f} us" for k, v in kernels.items()))
+    cpu = None
+    if args.cpu_seconds > 0:
+        c = prefill_cpu_baseline(args.cpu_seconds, logits)
+        cpu = {"value": round(c["tokens_per_s"], 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"the first {c['tokens']} of the {T} tokens, one at a time through the "
+                         f"scalar C oracle's MoE layer (their own top-4 of 128, experts drawn "
+                         f"from a pool of 32 synthetic ones), 1 thread, {c['seconds']:.1f} s"}
+        log(f"cpu baseline: {c['tokens_per_s']:.2f} tokens/s")
     # The grouped GEMMs sit below the bf16 ridge (about 60 flop per weight byte
     # against 2500 TFLOP/s / 8 TB/s = 312), so the roofline is HBM: the gate_up
     # launch moves the gate_up sections of every touched expert once.
@@ -489,7 +555,7 @@ def prefill_bench(gw, args) -> int:
         ach = gu_bytes / (gu * 1e-6) / 1e9
         gu_tflops = 2.0 * T * K * 2 * F * H / (gu * 1e-6) / 1e12
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": PREFILL_GATE_UP_TRAFFIC_BYTES,
+                "frac": round(ach / PEAK_HBM_GBS, 4), **measured_traffic(PREFILL_GATE_UP_TRAFFIC),
                 "kernel": "prefill_gemm_kernel (gate_up grouped GEMM)",
                 "avg_launch_us": round(gu, 3), "algorithmic_bytes": gu_bytes,
                 "mfma_tflops": round(gu_tflops, 1),
@@ -512,7 +578,7 @@ def prefill_bench(gw, args) -> int:
         "config": {"workload": "gptoss120b-moe-layer-prefill-512", "tokens": T, "experts": E,
                    "experts_touched": touched, "top_k": K, "hidden": H, "intermediate": F,
                    "parallelism": "single-gpu"},
-        "kernels": kernels, "roofline": roof, "cpu_baseline": None}), flush=True)
+        "kernels": kernels, "roofline": roof, "cpu_baseline": cpu}), flush=True)
     runner.close()
     ctx.close()
     return 0
@@ -543,7 +609,8 @@ def qwen3_bench(gw, args, batch: int) -> int:
         layers.append(buf)
     ctx.synchronize()
     log(f"resident experts: {Lq} x {Eq} x {lay.stride} B = {Lq * lay.layer_file_size / 1e9:.2f} GB")
-    total = args.warmup + args.steps
+    timed = TIMING_ROUNDS * args.steps
+    total = args.warmup + timed
     step_logits = Lq * batch * Eq * 4
     logits_all = ctx.empty(total * step_logits)
     ctx.fill_normal(logits_all, gw.F32, total * Lq * batch * Eq, 0.0, 1.0, args.seed * 31 + 7)
@@ -602,6 +669,7 @@ def qwen3_bench(gw, args, batch: int) -> int:
         ctx.set_profiling(False)
         log("kernels: " + ", ".join(f"{k} {v['avg_us']:.2f} us x{v['launches']}"
                                     for k, v in kernels.items()))
+    sync_err = runner.sync_errors()
     roof = None
     gu = "gate_up" if "gate_up" in kernels else "prefill_gate_up"
     if "moe_layer" in kernels:
@@ -625,10 +693,11 @@ def qwen3_bench(gw, args, batch: int) -> int:
                 "avg_launch_us": round(kernels[gu]["avg_us"], 3)}
     print(json.dumps({
         "metric": f"HBM GB/s (% of peak) + µs/token, Qwen3 MXFP4 MoE stack, batch {batch}",
-        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": timed,
+        "steps_per_round": args.steps,
         "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
         "us_per_token": round(dt * 1e6 / batch, 2), "hbm_frac_of_peak": round(value / PEAK_HBM_GBS, 4),
-        "us_per_token_mean": round(elapsed / args.steps * 1e6 / batch, 2),
+        "us_per_token_mean": round(elapsed / timed * 1e6 / batch, 2), "sync_errors": sync_err,
         **stats, "rounds_unit": "us/token",
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "compute": "e2m1 weights (MXFP4, exact) x bf16 activations, fp32 products and sums",
@@ -639,14 +708,17 @@ def qwen3_bench(gw, args, batch: int) -> int:
         "kernels": kernels, "roofline": roof, "cpu_baseline": None}), flush=True)
     runner.close()
     ctx.close()
+    if sync_err:
+        log(f"FAILED: {sync_err} exchange wait(s) gave up; the timed outputs are invalid")
+        return 1
     return 0
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=140,
-                    help="timed steps, run as rounds of 20 (the median round is reported)")
+    ap.add_argument("--steps", type=int, default=20,
+                    help="timed steps per round; 7 rounds run (the median round is reported)")
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -697,7 +769,8 @@ def main() -> int:
     log(f"resident experts: {L} x {E} x {lay.stride} B = {L * lay.layer_file_size / 1e9:.2f} GB "
         f"(filled in {time.perf_counter() - t0:.1f}s); {ctx.cu_count} CUs")
 
-    total_steps = args.warmup + args.steps
+    timed = TIMING_ROUNDS * args.steps
+    total_steps = args.warmup + timed
     logits_all = ctx.empty(total_steps * L * E * 4)
     ctx.fill_normal(logits_all, gw.F32, total_steps * L * E, 0.0, 1.0, args.seed * 31 + 7)
     cur_logits = ctx.empty(L * E * 4)
@@ -733,7 +806,7 @@ def main() -> int:
 
     bytes_token = L * (K * expert_bytes(lay) + E * 4 + H * 2 + H * 4 + H * 2)
     value = bytes_token / s_per_token / 1e9
-    log(f"{args.steps} tokens in {elapsed * 1e3:.2f} ms ({stats['rounds']} rounds): median "
+    log(f"{timed} tokens in {elapsed * 1e3:.2f} ms ({stats['rounds']} rounds): median "
         f"{stats['median']:.1f} us/token (min {stats['min']:.1f}, max {stats['max']:.1f}), "
         f"{value:.0f} GB/s ({value / PEAK_HBM_GBS * 100:.1f}% of {PEAK_HBM_GBS:.0f})")
 
@@ -764,11 +837,13 @@ def main() -> int:
         achieved = nbytes / (k_us * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                    "traffic": (GATE_UP_TRAFFIC_BYTES if dom == "gate_up"
-                                else DECODE_LAYER_TRAFFIC_BYTES),
+                    **measured_traffic(GATE_UP_TRAFFIC if dom == "gate_up" else DECODE_LAYER_TRAFFIC),
                     "kernel": desc, "bytes_per_launch": nbytes, "avg_launch_us": round(k_us, 3)}
         log("kernels: " + ", ".join(f"{k} {v['avg_us']:.2f} us x{v['launches']}"
                                     for k, v in kernels.items()))
+    # every wave of every one-kernel layer found its exchange words (a wait
+    # that gave up would have left wrong outputs in the timed steps)
+    sync_err = runner.sync_errors()
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -793,8 +868,10 @@ def main() -> int:
         cpu["all_cores"] = {
             "value": round(bytes_token / (ca["us_per_token"] * 1e-6) / 1e9, 4), "unit": "GB/s",
             "us_per_token": round(ca["us_per_token"], 1), "cores": ca["threads"],
+            "host_cpus": host_cpus(),
             "sample": f"{ca['tokens']} token(s), same workload, GEMV rows over "
-                      f"{ca['threads']} OpenMP threads, {ca['seconds']:.1f} s"}
+                      f"{ca['threads']} OpenMP threads (every CPU of the process's affinity "
+                      f"mask), {ca['seconds']:.1f} s"}
         log(f"cpu baseline, {ca['threads']} threads: {ca['us_per_token']:.0f} us/token "
             f"({cpu['all_cores']['value']:.3f} GB/s)")
 
@@ -803,11 +880,13 @@ def main() -> int:
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": timed,
+        "steps_per_round": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(s_per_token * 1e3, 4),
         "us_per_token": round(s_per_token * 1e6, 2),
-        "us_per_token_mean": round(elapsed / args.steps * 1e6, 2),
+        "us_per_token_mean": round(elapsed / timed * 1e6, 2),
+        "sync_errors": sync_err,
         **stats, "rounds_unit": "us/token",
         "hbm_frac_of_peak": round(value / PEAK_HBM_GBS, 4),
         "higher_is_better": True,
@@ -829,6 +908,9 @@ def main() -> int:
     graph.destroy()
     runner.close()
     ctx.close()
+    if sync_err:
+        log(f"FAILED: {sync_err} exchange wait(s) gave up; the timed outputs are invalid")
+        return 1
     return 0
 
 

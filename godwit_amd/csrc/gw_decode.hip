@@ -572,17 +572,21 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     // reads once its units' pieces are flagged, a DMA wave once it has flagged
     // its gate_up wave's, both at least PD ticks after this workgroup
     // published; the reads queue behind the down pieces still in flight.
+    // Waits on this workgroup's own waves (all resident with it) are bounded by
+    // the fixed kDecodeSpinLimit, not the caller's exchange limit, and a wait
+    // that ran out is counted like a failed exchange wait.
+    bool local_fail = false;
     if (wave < kGuWaves) {
         unsigned spins = 0;
         while (lds_peek(ready + wave) == 0u) {
-            if (++spins > a.spin_limit) break;    // cannot happen: the DMA wave flags them
+            if (++spins > kDecodeSpinLimit) { local_fail = true; break; }   // the DMA wave flags them
             __builtin_amdgcn_s_sleep(1);
         }
     }
     {
         unsigned spins = 0, tp;
         while ((tp = lds_peek(t_pub)) == 0u) {
-            if (++spins > a.spin_limit) break;    // cannot happen: wave 0 publishes
+            if (++spins > kDecodeSpinLimit) { local_fail = true; break; }   // wave 0 publishes
             __builtin_amdgcn_s_sleep(1);
         }
         if constexpr (PD > 0)
@@ -619,7 +623,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         {
             unsigned spins = 0;
             while (lds_peek(scl_in) < (unsigned)(kDW - kGuWaves)) {
-                if (++spins > a.spin_limit) break;    // cannot happen: every DMA wave counts itself
+                if (++spins > kDecodeSpinLimit) { local_fail = true; break; }   // every DMA wave counts itself
                 __builtin_amdgcn_s_sleep(1);
             }
         }
@@ -702,7 +706,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             for (int m = 0; m < 4; ++m)
                 pend |= pair_empty(Bv[j][m]) << (4 * j + m);
         unsigned spins = 0;
-        bool gave_up = false;
+        bool gave_up = local_fail;
         while (pend) {
             if (++spins > a.spin_limit) {
                 gave_up = true;

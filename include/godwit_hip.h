@@ -431,7 +431,8 @@ int gw_moe_block_forward(gw_expert_runner *runner, const gw_moe_block_args *args
 int gw_expert_runner_sync_errors(gw_expert_runner *runner, uint32_t *count);
 
 /* The bounded wait of the one-token layer: polls of the exchange before a
- * wait gives up (0 restores the default, 2^18, some milliseconds).  No
+ * wait gives up (0 restores the default, 2^18, some milliseconds).  Waits on
+ * a workgroup's own waves keep the fixed 2^18 bound whatever is set here.  No
  * counterpart in the reference. */
 int gw_expert_runner_set_wait_limit(gw_expert_runner *runner, uint32_t polls);
 

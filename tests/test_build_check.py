@@ -52,3 +52,16 @@ def test_without_remarks_keeps_other_diagnostics():
 def test_no_spill_sources_are_the_counted_wait_kernels():
     assert gwbuild.NO_SPILL == {"gw_decode.hip", "gw_prefill.hip"}
     assert gwbuild.NO_SPILL <= set(gwbuild.SOURCES)
+
+
+def test_spill_check_fails_without_kernel_records():
+    """A NO_SPILL source whose compiler output holds no kernel record (the
+    report flag dropped, or every kernel compiled away) fails the build: an
+    empty report must not pass as "no spills"."""
+    clean = REPORT.replace("VGPRs Spill: 56", "VGPRs Spill: 0").replace("AGPRs Spill: 3",
+                                                                      "AGPRs Spill: 0")
+    assert gwbuild.spill_check(clean) == []
+    assert len(gwbuild.spill_check(REPORT)) == 2
+    for text in ("", "gw_prefill.hip:40:9: warning: unused variable 'x' [-Wunused-variable]\n"):
+        problems = gwbuild.spill_check(text)
+        assert len(problems) == 1 and "no kernel-resource-usage records" in problems[0]

@@ -4,14 +4,16 @@ two-kernel form of the same layer (GODWIT_DECODE_LAYER=0) and against the CPU
 oracle.
 
 Both forms compute the gate_up rows with the same lane mapping and order, so
-their activations are the same bytes.  The one-kernel form splits a GPT-OSS
-down row over 32 lanes (3 blocks each) where the two-kernel form uses 16 (6
-each), so the fp32 row sums may round differently: the forms are required to
-agree to 1e-5 of the output's peak there, and bit for bit for Qwen3 (same down
-lane mapping in both).  Routing is exact in both.  The oracle check uses the
-reference's expert metric, max|d|/mean|ref| < 1e-3 (GodwitCLI/main.swift:518-532).
-Every test also requires the kernel's bounded waits to have all succeeded.  The
-one-kernel form takes 16-bit x; fp32 x stays on the two kernels.
+their activations are the same bytes.  The one-kernel form sums the down rows
+on the matrix cores (16x16x32 fp16 products accumulated in fp32) where the
+two-kernel form sums them lane by lane on the VALU, so the fp32 row sums may
+round differently: the forms are required to agree to 1e-5 of the output's
+peak.  Routing is exact in both.  The oracle check uses the reference's
+expert metric, max|d|/mean|ref| < 1e-3 (GodwitCLI/main.swift:518-532).  Every
+test also requires the kernel's bounded waits to have all succeeded, except
+the one that makes them give up on purpose (from the host: every kernel
+still exits normally).  The one-kernel form takes 16-bit x; fp32 x stays on
+the two kernels.
 """
 import numpy as np
 import pytest
@@ -106,18 +108,60 @@ def test_fused_layer_equals_two_kernel_form(ctx, monkeypatch, shape, n_experts, 
     split.close()
 
 
-def test_fused_layer_graph_chain_replays(ctx, monkeypatch):
-    """A captured chain of 12 one-token layers (each layer's bf16 output is the next
-    one's input), replayed 6 times: every replay equals the eager chain, the first
-    layer matches the oracle, and no exchange ever gave up.  The replays advance the
-    kernel's launch epochs well past their first values."""
-    shape = GPTOSS
-    H, F, n_experts, layers = shape["hidden"], shape["inter"], 16, 12
-    layout, experts, buf = _make_layer(ctx, shape, n_experts, 1400)
+def _oracle_token(buf, layout, n_experts, top_k, logits, xw, shape):
+    """oracle.moe_layer for one token, downloading only the experts the router
+    selects (the other entries of the list repeat one of them; the oracle's
+    own routing never reads them)."""
+    from helpers import expert_from_blob
+    ids, _ = oracle.router_select(logits, top_k)
+    sel = {int(e): expert_from_blob(buf.download(np.uint8, layout.stride, offset=int(e) * layout.stride),
+                                    layout) for e in ids}
+    first = sel[int(ids[0])]
+    experts = [sel.get(i, first) for i in range(n_experts)]
+    out, oids, _ = oracle.moe_layer(experts, top_k, logits[None, :], xw, shape["hidden"],
+                                    shape["inter"], shape["oact"])
+    assert list(oids[0]) == list(ids)
+    return out[0]
+
+
+def _chain_weights(ctx, shape, n_experts, layers, seed):
+    from helpers import fill_layer_device
+    layout = gw.ExpertLayout(shape["hidden"], shape["inter"], n_experts)
+    bufs = []
+    for l in range(layers):
+        bufs.append(ctx.empty(layout.stride * n_experts))
+        fill_layer_device(ctx, bufs[-1], layout, n_experts, seed + 7 * l, biases=shape["bias"])
+    return layout, bufs
+
+
+def _replay_equals_eager(ctx, chain, reset, outputs, eager, replays=4):
+    graph = gw.Graph.capture(ctx, chain)
+    for _ in range(replays):
+        reset()
+        graph.launch()
+        ctx.synchronize()
+        for l, (o, want) in enumerate(zip(outputs, eager)):
+            assert np.array_equal(o.download(want.dtype, want.size), want), l
+    graph.destroy()
+
+
+@pytest.mark.parametrize("shape,n_experts,top_k,layers",
+                         [(GPTOSS, 128, 4, 8), (GPTOSS, 16, 4, 12)], ids=["gptoss120b-8", "gptoss-16x12"])
+def test_fused_layer_chain_per_layer(ctx, monkeypatch, shape, n_experts, top_k, layers):
+    """A chain of one-token layers with their own weights, each layer's bf16
+    output the next one's input (GPT-OSS's clamped activation keeps the values
+    bounded without the norm between layers): every layer's output matches
+    the oracle run on that layer's own GPU bf16 input, and its bf16 copy is
+    the next input.  The chain is then captured and replayed 4 times: every
+    replay equals the eager chain at every layer, and no exchange ever gave
+    up.  The replays advance the kernel's launch epochs well past their first
+    values."""
+    H, F = shape["hidden"], shape["inter"]
+    layout, bufs = _chain_weights(ctx, shape, n_experts, layers, 1400)
     monkeypatch.setenv("GODWIT_DECODE_LAYER", "1")
     runner = gw.ExpertRunner(ctx, H, F, shape["act"])
-    r = rng(1401)
-    xbits, xw = normal_bf16(r, H)
+    r = rng(1401 + n_experts)
+    xbits, _ = normal_bf16(r, H)
     logits = r.standard_normal((layers, n_experts)).astype(np.float32)
     lb = ctx.buffer(logits)
     xs = [ctx.buffer(xbits)] + [ctx.empty(H * 2) for _ in range(layers)]
@@ -125,28 +169,167 @@ def test_fused_layer_graph_chain_replays(ctx, monkeypatch):
 
     def chain():
         for l in range(layers):
-            runner.layer_forward(buf.ptr, layout.stride, n_experts, 4, xs[l].ptr, gw.BF16, 1,
-                                 outs[l].ptr, logits=lb.address(l * n_experts * 4),
+            runner.layer_forward(bufs[l].ptr, layout.stride, n_experts, top_k, xs[l].ptr, gw.BF16,
+                                 1, outs[l].ptr, logits=lb.address(l * n_experts * 4),
                                  out_bf16=xs[l + 1].ptr)
 
     counts = _kernel_counts(ctx, chain)
-    assert counts["moe_layer"] == layers, counts
-    first = outs[0].download(np.float32, H)
-    eager = outs[-1].download(np.float32, H)
-    ref, _, _ = oracle.moe_layer([e.oracle_expert() for e in experts], 4, logits[:1], xw, H, F,
-                                 shape["oact"])
-    _close(first, ref[0])
-    graph = gw.Graph.capture(ctx, chain)
-    for _ in range(6):
-        outs[-1].zero()
-        graph.launch()
-        ctx.synchronize()
-        assert np.array_equal(outs[-1].download(np.float32, H), eager)
+    assert counts == {"moe_layer": layers, "gate_up": 0, "down": 0}, counts
+    eager = [o.download(np.float32, H) for o in outs]
+    inputs = [x.download(np.uint16, H) for x in xs]
+    for l in range(layers):
+        assert np.all(np.isfinite(eager[l])), l
+        assert np.array_equal(inputs[l + 1], oracle.f32_to_bf16_bits(eager[l])), l
+        ref = _oracle_token(bufs[l], layout, n_experts, top_k, logits[l],
+                            oracle.bf16_bits_to_f32(inputs[l]), shape)
+        _close(eager[l], ref)
+
+    def reset():
+        for o in outs:
+            o.zero()
+
+    _replay_equals_eager(ctx, chain, reset, outs, eager)
     assert runner.sync_errors() == 0
-    graph.destroy()
-    for b in xs + outs + [lb, buf]:
+    for b in xs + outs + bufs + [lb]:
         b.free()
     runner.close()
+
+
+@pytest.mark.parametrize("shape,n_experts,top_k,layers,eps",
+                         [(QWEN3, 128, 8, 8, 1e-6), (GPTOSS, 128, 4, 8, 1e-5)],
+                         ids=["qwen3-8", "gptoss120b-8"])
+def test_fused_block_chain_per_layer(ctx, monkeypatch, shape, n_experts, top_k, layers, eps):
+    """The decode step's MoE half over a stack of layers with their own weights
+    and norm weights (TransformerLayer.swift:140-143, 232-238): stream +=
+    MoE(RMSNorm(stream)), each layer's MoE one launch.  Every layer is run
+    eagerly and checked against the oracle composition on that layer's own GPU
+    input stream (oracle.rmsnorm_f16, the oracle layer, the fp32 residual add):
+    the change the layer made to the stream to the expert metric, the routing
+    exact.  The stack is then captured and replayed 4 times from the same
+    starting stream: every layer's bf16 copy of the stream equals the eager
+    one.  (Qwen3's SwiGLU has no clamp: bare layers chained without the norm
+    overflow fp16 within a few layers, so this is the form its chain takes.)"""
+    H, F = shape["hidden"], shape["inter"]
+    layout, bufs = _chain_weights(ctx, shape, n_experts, layers, 1700)
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "1")
+    runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+    r = rng(1701 + n_experts)
+    stream0 = r.standard_normal(H).astype(np.float32)
+    wbits = [oracle.f32_to_bf16_bits((1.0 + 0.1 * r.standard_normal(H)).astype(np.float32))
+             for _ in range(layers)]
+    logits = r.standard_normal((layers, n_experts)).astype(np.float32)
+    lb = ctx.buffer(logits)
+    wb = [ctx.buffer(w) for w in wbits]
+    sb = ctx.buffer(stream0)
+    copies = [ctx.empty(H * 2) for _ in range(layers)]
+    ids = [ctx.empty(top_k * 4) for _ in range(layers)]
+
+    def layer(l):
+        runner.block_forward(bufs[l].ptr, layout.stride, n_experts, top_k, 1, sb.ptr, wb[l].ptr,
+                             eps, logits=lb.address(l * n_experts * 4), out_bf16=copies[l].ptr,
+                             routing_ids=ids[l].ptr)
+
+    ctx.set_profiling(True)
+    ctx.profile_reset()
+    stream = stream0
+    for l in range(layers):
+        layer(l)
+        ctx.synchronize()
+        after = sb.download(np.float32, H)
+        normed = oracle.rmsnorm_f16(stream, wbits[l], eps).view(np.float16).astype(np.float32)
+        ref = _oracle_token(bufs[l], layout, n_experts, top_k, logits[l], normed[0], shape)
+        rid, _ = oracle.router_select(logits[l], top_k)
+        assert list(ids[l].download(np.int32, top_k)) == list(rid), l
+        assert np.all(np.isfinite(after)), l
+        _close(after - stream, ref)
+        assert np.array_equal(copies[l].download(np.uint16, H), oracle.f32_to_bf16_bits(after)), l
+        stream = after
+    assert ctx.profile("moe_layer")[1] == layers
+    assert ctx.profile("gate_up")[1] == 0
+    ctx.set_profiling(False)
+    eager = [c.download(np.uint16, H) for c in copies]
+    _replay_equals_eager(ctx, lambda: [layer(l) for l in range(layers)],
+                         lambda: sb.upload(stream0), copies, eager)
+    assert runner.sync_errors() == 0
+    for b in copies + ids + wb + bufs + [sb, lb]:
+        b.free()
+    runner.close()
+
+
+def test_exchange_give_up_is_reported_and_falls_back(ctx, monkeypatch):
+    """The bounded exchange wait made to give up from the host: the one-token
+    layer reads a slot no launch writes, with a 64-poll limit.  Every kernel
+    exits, the runner counts the waves that gave up, the next synchronize
+    reports GW_ERR_EXCHANGE once, and the runner's later one-token layers run
+    as two kernels and match the oracle."""
+    from godwit_amd._lib import GW_ERR_EXCHANGE
+    shape, n_experts, top_k = QWEN3, 32, 8
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _make_layer(ctx, shape, n_experts, 1500)
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "1")
+    runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+    r = rng(1501)
+    xb, xw = _inputs(ctx, r, H, gw.BF16)
+    logits = r.standard_normal(n_experts).astype(np.float32)
+    lb = ctx.buffer(logits)
+    out = ctx.empty(H * 4)
+    runner.set_wait_limit(64)
+    runner.inject_exchange_fault(True)
+    counts = _kernel_counts(ctx, lambda: runner.layer_forward(
+        buf.ptr, layout.stride, n_experts, top_k, xb.ptr, gw.BF16, 1, out.ptr, logits=lb.ptr))
+    assert counts == {"moe_layer": 1, "gate_up": 0, "down": 0}, counts
+    with pytest.raises(gw.GodwitError) as err:
+        ctx.synchronize()
+    assert err.value.status == GW_ERR_EXCHANGE, err.value
+    gave_up = runner.sync_errors()
+    assert gave_up > 0
+    ctx.synchronize()   # reported once
+    runner.inject_exchange_fault(False)
+    runner.set_wait_limit(0)
+    got = {}
+    counts = _kernel_counts(ctx, lambda: got.__setitem__(
+        "x", _forward(ctx, runner, layout, buf, n_experts, top_k, xb, gw.BF16, lb, H)))
+    assert counts == {"moe_layer": 0, "gate_up": 1, "down": 1}, counts
+    ref, _, _ = oracle.moe_layer([e.oracle_expert() for e in experts], top_k, logits[None, :], xw,
+                                 H, F, shape["oact"])
+    _close(got["x"][0], ref[0])
+    assert runner.sync_errors() == gave_up
+    for b in (xb, lb, out, buf):
+        b.free()
+    runner.close()
+
+
+def test_fused_layer_f32_bias_qwen3(ctx, monkeypatch):
+    """fp32 bias sections (set_bias_dtype(GW_F32)) on the one-token layer at
+    Qwen3's shape: one launch, the oracle fed the same fp32 biases, the
+    two-kernel form to 1e-5 of the peak, and no exchange gave up."""
+    from test_gpu_boundary import _f32_bias_layer
+    shape, n_experts, top_k = QWEN3, 32, 8
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _f32_bias_layer(ctx, shape, n_experts, 1600)
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "1")
+    fused = gw.ExpertRunner(ctx, H, F, shape["act"], bias_dtype=gw.F32)
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "0")
+    split = gw.ExpertRunner(ctx, H, F, shape["act"], bias_dtype=gw.F32)
+    r = rng(1601)
+    xb, xw = _inputs(ctx, r, H, gw.BF16)
+    logits = r.standard_normal(n_experts).astype(np.float32)
+    lb = ctx.buffer(logits)
+    got = {}
+    counts = _kernel_counts(ctx, lambda: got.__setitem__(
+        "fused", _forward(ctx, fused, layout, buf, n_experts, top_k, xb, gw.BF16, lb, H)))
+    assert counts == {"moe_layer": 1, "gate_up": 0, "down": 0}, counts
+    got["split"] = _forward(ctx, split, layout, buf, n_experts, top_k, xb, gw.BF16, lb, H)
+    f_out, s_out = got["fused"][0], got["split"][0]
+    assert np.max(np.abs(f_out - s_out)) <= 1e-5 * np.max(np.abs(s_out))
+    ref, _, _ = oracle.moe_layer([e.oracle_expert() for e in experts], top_k, logits[None, :], xw,
+                                 H, F, shape["oact"])
+    _close(f_out, ref[0])
+    assert fused.sync_errors() == 0
+    for b in (xb, lb, buf):
+        b.free()
+    fused.close()
+    split.close()
 
 
 @pytest.mark.parametrize("shape,n_experts,top_k", [(GPTOSS, 32, 4), (GPTOSS, 128, 4),
