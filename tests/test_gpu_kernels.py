@@ -112,18 +112,28 @@ def test_gemv_config0_shape(ctx, x_dtype):
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 32), (3, 64), (17, 768), (5, 4096), (33, 2048),
-                                       (7, 32 * 600)])
-def test_gemv_ragged_shapes(ctx, rows, cols):
+                                       (7, 32 * 600), (8196, 2880), (5000, 32 * 100)])
+@pytest.mark.parametrize("x_dtype", [gw.BF16, gw.F32], ids=["bf16", "f32"])
+def test_gemv_ragged_shapes(ctx, rows, cols, x_dtype):
+    """Ragged row counts and widths, bf16 and fp32 x, against the oracle and
+    the float64 sum (rows past 512 workgroups' worth, rows wider than the
+    register stages)."""
     r = rng(rows * 1000 + cols)
     packed, scales = mxfp4_matrix(r, rows, cols)
     bits, bias = bias_bf16(r, rows)
     xb16, xw = normal_bf16(r, cols)
+    if x_dtype == gw.F32:
+        xw = r.standard_normal(cols).astype(np.float32)
     ref = oracle.gemv_bias(packed, scales, bias, xw, rows, cols)
-    got = _run_gemv(ctx, packed, scales, xb16, gw.BF16, rows, cols, bias=bits, bias_dtype=gw.BF16)
+    x = xb16 if x_dtype == gw.BF16 else xw
+    got = _run_gemv(ctx, packed, scales, x, x_dtype, rows, cols, bias=bits, bias_dtype=gw.BF16)
     assert gemv_metric(got, ref) < 1e-3
+    w = oracle.decode(packed, scales, rows * cols // 32).astype(np.float64).reshape(rows, cols)
+    assert gemv_metric(got, w @ xw.astype(np.float64) + bias) < 1e-4
 
 
-def test_gemv_edge_scales(ctx):
+@pytest.mark.parametrize("x_dtype", [gw.F16, gw.F32], ids=["f16", "f32"])
+def test_gemv_edge_scales(ctx, x_dtype):
     """Subnormal scale bytes 0/1, the largest scale 254 and NaN 0xFF flow through the GEMV
     as the CPU reference computes them."""
     r = rng(3)
@@ -135,12 +145,43 @@ def test_gemv_edge_scales(ctx):
     scales[3, 3] = 254
     scales[4, 5] = 255
     scales = scales.ravel()
-    x = np.ones(cols, np.float16)
+    x = np.ones(cols, np.float16 if x_dtype == gw.F16 else np.float32)
     ref = oracle.reference_mxfp4(packed, scales, x.astype(np.float32), rows, cols)
-    got = _run_gemv(ctx, packed, scales, x, gw.F16, rows, cols)
+    got = _run_gemv(ctx, packed, scales, x, x_dtype, rows, cols)
     assert np.isnan(got[4]) and np.isnan(ref[4])
     keep = np.arange(rows) != 4
     assert np.allclose(got[keep], ref[keep], rtol=1e-6, atol=0)
+
+
+def test_gemv_f32_large_scales(ctx):
+    """Scale bytes 253 and 254 (2^126, 2^127) with small fp32 x, so the sums stay
+    finite: rows mixing them with ordinary and subnormal scales match the
+    oracle and the float64 sum."""
+    r = rng(11)
+    rows, cols = 40, 512
+    packed, scales = mxfp4_matrix(r, rows, cols)
+    scales = scales.reshape(rows, -1)
+    scales[0, :] = 253
+    scales[1, :] = 254
+    scales[2, ::3] = 253
+    scales[2, 1::3] = 0
+    scales[5, 7] = 254
+    scales[21, 2] = 253          # the second tile
+    scales = scales.ravel()
+    x = (r.standard_normal(cols) * 2.0 ** -20).astype(np.float32)
+    ref = oracle.reference_mxfp4(packed, scales, x, rows, cols)
+    got = _run_gemv(ctx, packed, scales, x, gw.F32, rows, cols)
+    assert np.all(np.isfinite(ref)) and np.all(np.isfinite(got))
+    # fp32 sums in any order stay within a small multiple of 2^-24 of the sum
+    # of |products| from the exact value; rows of large blocks that cancel
+    # are held to that, not to their (smaller) result
+    nb = rows * cols // 32   # weights in float64: 6 * 2^127 overflows fp32
+    codes = oracle.decode(packed, np.full(nb, 127, np.uint8), nb).astype(np.float64)
+    w = (codes.reshape(nb, 32) * 2.0 ** (scales.astype(np.float64) - 127)[:, None]).reshape(rows, cols)
+    exact = w @ x.astype(np.float64)
+    mag = np.abs(w) @ np.abs(x.astype(np.float64))
+    assert np.all(np.abs(ref - exact) <= 1e-5 * mag)   # the oracle itself
+    assert np.all(np.abs(got - exact) <= 1e-5 * mag), np.max(np.abs(got - exact) / mag)
 
 
 def test_gemv_shape_errors(ctx):
