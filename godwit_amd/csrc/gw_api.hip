@@ -65,6 +65,7 @@ struct gw_context {
     hipStream_t stream = nullptr;
     int cus = 0;
     int grid_a = 0, grid_b = 0;
+    int coop = 0;
     bool capturing = false;
     bool profiling = false;
     std::vector<ProfEvent> events;       // recorded pairs, in order
@@ -90,6 +91,7 @@ static gw::Launch launch_of(gw_context *ctx)
     L.cus = ctx->cus;
     L.grid_a = ctx->grid_a;
     L.grid_b = ctx->grid_b;
+    L.coop = ctx->coop;
     return L;
 }
 
@@ -184,6 +186,7 @@ extern "C" int gw_context_create(int device, gw_context **out)
     ctx->cus = prop.multiProcessorCount;
     ctx->grid_a = get_env_int("GODWIT_GRID_A", 0);
     ctx->grid_b = get_env_int("GODWIT_GRID_B", 0);
+    ctx->coop = get_env_int("GODWIT_DECODE_COOP", 0);
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         delete ctx;
@@ -1026,9 +1029,23 @@ static int moe_layer_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int o
     GW_CHECK(a->logits || a->router_weight, GW_ERR_ARG, "need logits or router weights");
     gw_context *ctx = r->ctx;
     const gw::Launch L = launch_of(ctx);
+    if (!a->logits) GW_CHECK(dtype_ok(a->router_weight_dtype), GW_ERR_ARG, "bad router dtype");
+    // One token: the whole layer in one kernel when the shape, the dtype and
+    // the occupancy allow it, which also computes the router logits when the
+    // router rows split evenly over its grid (16-bit x, up to 128 experts).
+    gw::DecodeArgs d = {};
+    size_t dlds = 0;
+    const int dgrid = a->tokens == 1 && r->decode_layer
+                          ? gw::decode_layer_plan(L, (int)r->hidden, (int)r->inter, a->x_dtype,
+                                                  (int)a->top_k, (int)a->expert_count,
+                                                  a->expert_stride, r->bias_dt, &d, &dlds)
+                          : 0;
+    const int rslices = dgrid > 0 && !a->logits && a->expert_count <= 128 &&
+                                aligned16(a->router_weight) && aligned16(a->x)
+                            ? gw::router_slices((int)a->expert_count, (int)r->hidden, dgrid)
+                            : 0;
     const float *logits = a->logits;
-    if (!logits) {
-        GW_CHECK(dtype_ok(a->router_weight_dtype), GW_ERR_ARG, "bad router dtype");
+    if (!logits && rslices == 0) {
         ProfScope ps(ctx, "router");
         GW_HIP(gw::launch_router(ps.launch(L), a->router_weight, a->router_weight_dtype, a->router_bias,
                                  a->router_bias ? (int)a->router_bias_dtype : -1, a->x,
@@ -1049,16 +1066,18 @@ static int moe_layer_impl(gw_expert_runner *r, const gw_moe_layer_args *a, int o
     route.ids_out = a->routing_ids;
     route.w_out = a->routing_weights;
     const gw::Sections sec = sections_of(r->offsets);
-    // One token: the whole layer in one kernel when the shape, the dtype and
-    // the occupancy allow it.
-    if (a->tokens == 1 && r->decode_layer) {
-        gw::DecodeArgs d = {};
-        size_t lds = 0;
-        const int grid = gw::decode_layer_plan(L, (int)r->hidden, (int)r->inter, a->x_dtype,
-                                               (int)a->top_k, (int)a->expert_count,
-                                               a->expert_stride, r->bias_dt, &d, &lds);
+    {
+        const int grid = dgrid;
+        const size_t lds = dlds;
         if (grid > 0) {
             d.logits = logits;
+            if (rslices > 0) {
+                d.rw = a->router_weight;
+                d.rw_dt = (int)a->router_weight_dtype;
+                d.rb = a->router_bias;
+                d.rb_dt = a->router_bias ? (int)a->router_bias_dtype : -1;
+                d.rslices = rslices;
+            }
             d.experts = (int)a->expert_count;
             d.top_k = (int)a->top_k;
             d.base = a->experts_base;

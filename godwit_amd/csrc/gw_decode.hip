@@ -67,6 +67,11 @@ constexpr int kNt = 2;                   // buffer cache policy: non-temporal (s
 constexpr int kSc1 = 16;                 // buffer cache policy: device-coherent (past the L2)
 constexpr uint32_t kOutOfRange = 0x80000000u;   // buffer offset past any layer (reads zero)
 constexpr uint64_t kEmpty = ~0ull;       // an exchange word not written this launch
+// Ticks (10 ns) between publishing the router partial and the first read of
+// the grid's partials (a read before the last publisher costs a round trip;
+// measured on MI355X at the GPT-OSS-20B shape: 0: 22.8, 30: 21.1-21.4, 60:
+// 21.1, 100: 21.3-21.5 us per layer with the layer's router).
+constexpr int kRouterPollDelay = 60;
 // Exchange slots: launches alternate between slots 0 and 1; slot 2 is never
 // written (a host flag points the readers at it to exercise the give-up path).
 constexpr int kXSlotWords = kDecodeXchgSlotBytes / 8;
@@ -224,13 +229,89 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     uint32_t *rkey = reinterpret_cast<uint32_t *>(lds8 + L.dma);   // keys [128]; the down
     float *rlogit = reinterpret_cast<float *>(lds8 + L.dma + 512);  // pieces come later
     unsigned *rcount = reinterpret_cast<unsigned *>(lds8 + L.route + 68);   // [kMaxTopK + 1]
+    bool route_fail = false;   // the router partials' exchange gave up
+    // Router partial slots: every launch clears its word of the next launch's
+    // slot, whether or not it computes the logits itself (that launch's slot
+    // is then empty however the launches before it were made).
+    uint64_t *pslots = a.xchg + 3 * (size_t)kXSlotWords;
+    if (threadIdx.x == 0)
+        __hip_atomic_store(pslots + (size_t)((epoch1 + 1) & 1u) * kDecodeMaxGrid + b, kEmpty,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (wave == 0) {
         if (by_rank) {
             bool nan = false;
+            float lv[2];
+            if (a.rw) {
+                // ---- 0. the router logits in the kernel: this workgroup's
+                // partial out (a 64-bit word, never all ones), the next
+                // launch's word cleared, every partial of the grid read back
+                // (rereads past the L2 while a word is still empty), each
+                // logit its partials in slice order plus the bias.
+                const int S = a.rslices, Lw = H / S;
+                const float p = router_partial_dt<XK>(a.rw, a.rw_dt, a.x, b / S, b % S, Lw, H, lane);
+                float bias_e[2];
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const int i = min(lane + 64 * r, a.experts - 1);
+                    bias_e[r] = a.rb ? load_as_f32(a.rb, a.rb_dt, i) : 0.0f;
+                }
+                if (lane == 0)
+                    __hip_atomic_store(pslots + (size_t)(epoch1 & 1u) * kDecodeMaxGrid + b,
+                                       (uint64_t)__float_as_uint(p), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                if constexpr (kRouterPollDelay > 0) {
+                    const uint32_t t0 = (uint32_t)wall_clock64();
+                    while ((uint32_t)wall_clock64() - t0 < (uint32_t)kRouterPollDelay)
+                        __builtin_amdgcn_s_sleep(2);
+                }
+                const int pslot = a.poll_fault ? 2 : (int)(epoch1 & 1u);
+                const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+                    pslots + (size_t)pslot * kDecodeMaxGrid, (short)0, (int)gridDim.x * 8, kRsrcWord3);
+                constexpr int PW = kDecodeMaxGrid / 64;
+                uint64_t pv[PW];
+#pragma unroll
+                for (int k = 0; k < PW; ++k)
+                    pv[k] = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(
+                                                             pr, (uint32_t)(lane + 64 * k) * 8u, 0, 0));
+                // words past the grid read zero (out of range), never empty
+                unsigned spins = 0;
+                uint32_t pend = 0;
+#pragma unroll
+                for (int k = 0; k < PW; ++k) pend |= (pv[k] == kEmpty ? 1u : 0u) << k;
+                while (__ballot(pend != 0u) != 0ull) {
+                    if (++spins > a.spin_limit) {
+                        route_fail = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+                    for (int k = 0; k < PW; ++k)
+                        if ((pend >> k) & 1u)
+                            pv[k] = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(
+                                                                     pr, (uint32_t)(lane + 64 * k) * 8u, 0, kSc1));
+#pragma unroll
+                    for (int k = 0; k < PW; ++k)
+                        if (pv[k] != kEmpty) pend &= ~(1u << k);
+                }
+                float *rpart = reinterpret_cast<float *>(lds8 + L.dma + 1024);   // [grid]
+#pragma unroll
+                for (int k = 0; k < PW; ++k) rpart[lane + 64 * k] = __uint_as_float((uint32_t)pv[k]);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const int i = min(lane + 64 * r, a.experts - 1);
+                    float v = rpart[i * S];
+                    for (int k = 1; k < S; ++k) v += rpart[i * S + k];
+                    lv[r] = v + bias_e[r];
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 2; ++r) lv[r] = a.logits[min(lane + 64 * r, a.experts - 1)];
+            }
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
                 const int i = lane + 64 * r;
-                const float v = a.logits[min(i, a.experts - 1)];
+                const float v = lv[r];
                 const bool in = i < a.experts, isn = in && __builtin_isnan(v);
                 nan |= isn;
                 rkey[i] = in && !isn ? order_key(v) : 0u;
@@ -285,7 +366,9 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             if (wave == 0) {
                 int sid;
                 float w;
-                select_one<2>(a.logits, a.experts, K, sid, w);
+                // the logits in LDS (rlogit holds all of them): with the
+                // in-kernel router there is no logits array in memory
+                select_one<2>(a.rw ? rlogit : a.logits, a.experts, K, sid, w);
                 if (lane < K) {
                     eid[lane] = sid;
                     ew[lane] = w;
@@ -706,7 +789,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             for (int m = 0; m < 4; ++m)
                 pend |= pair_empty(Bv[j][m]) << (4 * j + m);
         unsigned spins = 0;
-        bool gave_up = local_fail;
+        bool gave_up = local_fail || route_fail;
         while (pend) {
             if (++spins > a.spin_limit) {
                 gave_up = true;
@@ -940,6 +1023,12 @@ hipError_t launch_decode_layer(const Launch &L, int grid, size_t lds, int x_dt, 
     const int shape = shape_of(a.hidden, a.inter);
     if (shape < 0 || grid <= 0) return hipErrorInvalidValue;
     const DecodeKernel kernel = kernel_for(shape, x_dt);
+    if (L.coop && !L.ev_start) {
+        DecodeArgs copy = a;
+        void *args[] = {&copy};
+        return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(kernel), dim3(grid), dim3(kDT),
+                                          args, (unsigned)lds, L.stream);
+    }
     GW_LAUNCH(kernel, dim3(grid), dim3(kDT), lds, L, a);
     return hipGetLastError();
 }

@@ -341,4 +341,74 @@ template <int TPR> __device__ __forceinline__ float seg_sum(float v)
 }
 #undef GW_DPPF
 
+// Eight consecutive elements as fp32 from a 16-byte aligned position (one
+// 16-byte load for 16-bit data, two for fp32).
+template <int DT>
+__device__ __forceinline__ void load8_f32(const void *p, int64_t i, float (&v)[8])
+{
+    if constexpr (DT == DT_F32) {
+        const float4 *q = reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
+        const float4 a = q[0], c = q[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+    } else {
+        const uint4 a = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i);
+        const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint16_t lo = (uint16_t)(w[k] & 0xFFFFu), hi = (uint16_t)(w[k] >> 16);
+            v[2 * k] = DT == DT_BF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+            v[2 * k + 1] = DT == DT_BF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+        }
+    }
+}
+
+// ---- router logits by slices ------------------------------------------------
+// For one token, the E logits (bf16_gemv_bias, router.metal:18-34) can be
+// computed by E * S waves, wave (e, s) dotting weight row e with x over slice
+// s of S (L = H / S elements): the one-token layer kernel does this in its
+// workgroups and the standalone router in the same order, so both give the
+// same logit bits.  Lane l dots the 8-element units l, l + 64, ... of the
+// slice in order (fused multiply-adds into one sum), the wave sum is a fixed
+// xor butterfly, and a logit is its S partials added in slice order plus the
+// bias.
+
+template <int WDT, int XDT>
+__device__ __forceinline__ float router_partial(const void *W, const void *x, int e, int s, int L,
+                                                int H, int lane)
+{
+    const int units = L >> 3;
+    float w[kRouterUnits][8], xv[kRouterUnits][8];
+    bool ok[kRouterUnits];
+#pragma unroll
+    for (int u = 0; u < kRouterUnits; ++u) {
+        const int unit = lane + 64 * u;
+        ok[u] = unit < units;
+        const int at = s * L + 8 * (ok[u] ? unit : 0);
+        load8_f32<WDT>(W, (int64_t)e * H + at, w[u]);
+        load8_f32<XDT>(x, at, xv[u]);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kRouterUnits; ++u)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float nv = acc + w[u][q] * xv[u][q];
+            acc = ok[u] ? nv : acc;
+        }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    return acc;
+}
+
+// router_partial with the weight dtype chosen at run time.
+template <int XDT>
+__device__ __forceinline__ float router_partial_dt(const void *W, int w_dt, const void *x, int e,
+                                                   int s, int L, int H, int lane)
+{
+    if (w_dt == DT_F32) return router_partial<DT_F32, XDT>(W, x, e, s, L, H, lane);
+    if (w_dt == DT_F16) return router_partial<DT_F16, XDT>(W, x, e, s, L, H, lane);
+    return router_partial<DT_BF16, XDT>(W, x, e, s, L, H, lane);
+}
+
 }  // namespace gw

@@ -584,28 +584,6 @@ __global__ __launch_bounds__(256) void router_kernel(const void *__restrict__ W,
     if (lane == 0) logits[(int64_t)t * E + e] = acc + (b ? load_as_f32(b, b_dt, e) : 0.0f);
 }
 
-// Eight consecutive elements as fp32 from a 16-byte aligned position (one
-// 16-byte load for 16-bit data, two for fp32).
-template <int DT>
-__device__ __forceinline__ void load8_f32(const void *p, int64_t i, float (&v)[8])
-{
-    if constexpr (DT == DT_F32) {
-        const float4 *q = reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
-        const float4 a = q[0], c = q[1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
-    } else {
-        const uint4 a = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i);
-        const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint16_t lo = (uint16_t)(w[k] & 0xFFFFu), hi = (uint16_t)(w[k] >> 16);
-            v[2 * k] = DT == DT_BF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
-            v[2 * k + 1] = DT == DT_BF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
-        }
-    }
-}
-
 // Router logits, wide form: workgroup (e, token block) reads expert e's
 // weight row in 8-element units (16-byte loads, all units of a thread in
 // flight together) and dots it with up to 8 token rows; the per-thread sums
@@ -622,10 +600,52 @@ __global__ __launch_bounds__(256) void router_rows_kernel(const void *__restrict
     const int e = blockIdx.x, t0 = blockIdx.y * kMaxRouterTokens;
     const int nt = min(kMaxRouterTokens, T - t0);
     const int H8 = H >> 3;
+    // The bias as the aligned dword holding it, read with the first loads
+    // (a branchy load here would make the compiler drain them at the join).
+    const int bsz = b_dt == DT_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(b ? b : W), (short)0, b ? (E * bsz + 3) & ~3 : 0, 0x00020000);
+    const uint32_t b_at = (uint32_t)(e * bsz);
+    uint32_t bias_word;
     float acc[kMaxRouterTokens];
 #pragma unroll
     for (int t = 0; t < kMaxRouterTokens; ++t) acc[t] = 0.0f;
-    for (int u = (int)threadIdx.x; u < H8; u += 256) {
+    // The first two units of every thread (H up to 4096): every weight and x
+    // load in flight before the first product, out-of-range units clamped
+    // to unit 0 and their products dropped.
+    {
+        float w[2][8];
+        bool has[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int u = (int)threadIdx.x + 256 * k;
+            has[k] = u < H8;
+            load8_f32<WDT>(W, (int64_t)e * H + 8 * (has[k] ? u : 0), w[k]);
+        }
+        const uint32_t bw = __builtin_amdgcn_raw_buffer_load_b32(br, b_at & ~3u, 0, 0);
+        float xv[kMaxRouterTokens][2][8];
+#pragma unroll
+        for (int t = 0; t < kMaxRouterTokens; ++t)
+            if (t < nt)
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int u = (int)threadIdx.x + 256 * k;
+                    load8_f32<XDT>(x, (int64_t)(t0 + t) * H + 8 * (u < H8 ? u : 0), xv[t][k]);
+                }
+        // the same products in the same order as one unit after another
+#pragma unroll
+        for (int t = 0; t < kMaxRouterTokens; ++t)
+            if (t < nt)
+#pragma unroll
+                for (int k = 0; k < 2; ++k)
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) {
+                        const float nv = acc[t] + w[k][q] * xv[t][k][q];
+                        acc[t] = has[k] ? nv : acc[t];
+                    }
+        bias_word = bw;
+    }
+    for (int u = (int)threadIdx.x + 512; u < H8; u += 256) {
         float w[8];
         load8_f32<WDT>(W, (int64_t)e * H + 8 * u, w);
 #pragma unroll
@@ -650,7 +670,26 @@ __global__ __launch_bounds__(256) void router_rows_kernel(const void *__restrict
     if ((int)threadIdx.x < nt) {
         const int t = threadIdx.x;
         const float sum = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
-        logits[(int64_t)(t0 + t) * E + e] = sum + (b ? load_as_f32(b, b_dt, e) : 0.0f);
+        logits[(int64_t)(t0 + t) * E + e] = sum + (b ? decode_bias(bias_word, (int)(b_at & 2u) * 8, b_dt) : 0.0f);
+    }
+}
+
+// Router logits of one token by slices (router_partial, the same order as the
+// one-token layer kernel's in-kernel router): workgroup e, wave s.
+template <int WDT, int XDT>
+__global__ __launch_bounds__(64 * kRouterMaxSlices) void router_split_kernel(
+    const void *__restrict__ W, const void *__restrict__ b, int b_dt, const void *__restrict__ x,
+    float *__restrict__ logits, int H, int S)
+{
+    __shared__ float part[kRouterMaxSlices];
+    const int e = blockIdx.x, s = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+    const float p = router_partial<WDT, XDT>(W, x, e, s, H / S, H, lane);
+    if (lane == 0) part[s] = p;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float v = part[0];
+        for (int k = 1; k < S; ++k) v += part[k];
+        logits[e] = v + (b ? load_as_f32(b, b_dt, e) : 0.0f);
     }
 }
 
@@ -965,6 +1004,24 @@ hipError_t launch_router(const Launch &L, const void *W, int w_dt, const void *b
 {
     const int waves = experts * tokens;
     if (waves == 0) return hipSuccess;
+    const int S = router_slices(experts, hidden, L.cus);
+    if (tokens == 1 && S > 0 && x_dt != DT_F32 && ((uintptr_t)W & 15u) == 0 &&
+        ((uintptr_t)x & 15u) == 0) {
+        // one 16-bit token: the sliced order of the one-token layer's router
+        auto go = [&](auto wdt, auto xdt) {
+            constexpr int WD = decltype(wdt)::value, XD = decltype(xdt)::value;
+            GW_LAUNCH((router_split_kernel<WD, XD>), dim3(experts), dim3(64 * S), 0, L, W, b, b_dt,
+                      x, logits, hidden, S);
+        };
+        auto with_x = [&](auto wdt) {
+            if (x_dt == DT_F16) go(wdt, std::integral_constant<int, DT_F16>{});
+            else go(wdt, std::integral_constant<int, DT_BF16>{});
+        };
+        if (w_dt == DT_F32) with_x(std::integral_constant<int, DT_F32>{});
+        else if (w_dt == DT_F16) with_x(std::integral_constant<int, DT_F16>{});
+        else with_x(std::integral_constant<int, DT_BF16>{});
+        return hipGetLastError();
+    }
     const bool wide = hidden % 8 == 0 && ((uintptr_t)W & 15u) == 0 &&
                       ((uintptr_t)x & 15u) == 0 && div_up(tokens, kMaxRouterTokens) <= 65535;
     if (wide) {

@@ -28,6 +28,7 @@ struct Launch {
     int grid_b;     // workgroups of the down kernel (0 = default)
     hipEvent_t ev_start = nullptr;   // set: recorded by the kernel's dispatch (profiling)
     hipEvent_t ev_stop = nullptr;
+    int coop = 0;   // one-token layer through hipLaunchCooperativeKernel
 };
 
 // Device routing from logits (Router.select + the demand map), done by the
@@ -85,7 +86,8 @@ constexpr int kDecodeMaxGrid = 256;           // workgroups of the one-kernel la
 // The one-kernel layer's exchange: launches alternate between two slots of
 // 8-byte activation words (four fp16 each); a third slot is never written.
 constexpr int kDecodeXchgSlotBytes = 256 * 1024;
-constexpr int kDecodeXchgBytes = 3 * kDecodeXchgSlotBytes;
+// three activation slots, then three slots of router partials (one word a workgroup)
+constexpr int kDecodeXchgBytes = 3 * kDecodeXchgSlotBytes + 3 * kDecodeMaxGrid * 8;
 constexpr uint32_t kDecodeSpinLimit = 1u << 18;   // polls before a wait gives up
 
 struct DecodeArgs {
@@ -110,6 +112,14 @@ struct DecodeArgs {
     int nrmax;                    // most down rows a workgroup owns (ceil(hidden / grid))
     uint32_t spin_limit;          // polls of the exchange before a wait gives up
     int poll_fault;               // 1: read the never-written slot (tests the give-up path)
+    // In-kernel router (rw != null, logits unused): workgroup b computes the
+    // partial (b / rslices, b % rslices) of router_partial, the grid exchanges
+    // them and every workgroup adds each logit's rslices partials in order.
+    const void *rw;               // [experts, hidden] router weights
+    int rw_dt;
+    const void *rb;               // optional [experts] router bias
+    int rb_dt;
+    int rslices;
 };
 struct DecodeLds { int route, xs, actl, dma, scl, part, total; };
 

@@ -36,4 +36,23 @@ struct Sections {
     int64_t gu_blocks, gu_scales, dn_blocks, dn_scales, gu_bias, dn_bias;
 };
 
+// Router logits of one token by slices (router_partial in gw_device.h).
+constexpr int kRouterUnits = 4;        // 8-element units a lane, per slice
+constexpr int kRouterMaxSlices = 16;   // a standalone workgroup's waves
+
+// S for E experts of width H over `waves` waves (waves / E when that divides
+// evenly, into at most 16 slices of whole 8-element units, at most
+// kRouterUnits a lane), else 0.
+#if defined(__HIPCC__)
+__host__ __device__
+#endif
+inline int router_slices(int experts, int hidden, int waves)
+{
+    if (experts <= 0 || waves % experts != 0) return 0;
+    const int S = waves / experts;
+    if (S < 1 || S > kRouterMaxSlices || hidden % S != 0) return 0;
+    const int L = hidden / S;
+    return L % 8 == 0 && L <= 64 * 8 * kRouterUnits ? S : 0;
+}
+
 }  // namespace gw

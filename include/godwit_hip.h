@@ -413,12 +413,23 @@ int gw_moe_block_forward(gw_expert_runner *runner, const gw_moe_block_args *args
  * (hidden and intermediate both 65..96 blocks of 32) with top-k <= 4, or
  * Qwen3-class rows (hidden 25..64 blocks, intermediate 9..24 blocks); other
  * cases, and GODWIT_DECODE_LAYER=0 in the environment when the runner is
- * created, use a gate_up and a down kernel.
+ * created, use a gate_up and a down kernel.  Given router weights instead of
+ * logits (up to 128 experts, 16-byte aligned weights and x, and the CU count
+ * a multiple of expert_count with each logit's hidden / (CUs / experts)
+ * slice whole 8-element units, at most 2048), the kernel computes the
+ * logits too: each workgroup dots one slice of one weight row, the grid
+ * exchanges the partials and every workgroup adds each logit's partials in
+ * slice order plus the bias.  The standalone router adds the same slices in
+ * the same order for one 16-bit token, so both forms route alike.
  *
  * Co-residency contract: the kernel's workgroups wait for each other, so all
  * of them must run at once.  The host checks that one workgroup fits each
  * compute unit of an idle device; nothing else may run on the GPU during a
- * one-token layer (no other stream, runner or process).  The waits are
+ * one-token layer (no other stream, runner or process).  With
+ * GODWIT_DECODE_COOP=1 in the environment when the context is created the
+ * kernel goes through hipLaunchCooperativeKernel, whose runtime refuses a
+ * grid that cannot be resident at once (it captures into graphs, but costs
+ * about 18 us a launch on MI355X with ROCm 7, so it is off by default).  The waits are
  * bounded: a wait that gives up is counted instead of hanging the device,
  * and that launch's outputs are invalid.  gw_context_synchronize then
  * returns GW_ERR_EXCHANGE, and the runner runs later one-token layers with

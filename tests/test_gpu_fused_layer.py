@@ -50,13 +50,93 @@ def _forward(ctx, runner, layout, buf, n_experts, top_k, xb, x_dtype, lb, H):
     return res
 
 
-def _kernel_counts(ctx, fn):
+def _kernel_counts(ctx, fn, names=("moe_layer", "gate_up", "down")):
     ctx.set_profiling(True)
     ctx.profile_reset()
     fn()
-    counts = {k: ctx.profile(k)[1] for k in ("moe_layer", "gate_up", "down")}
+    counts = {k: ctx.profile(k)[1] for k in names}
     ctx.set_profiling(False)
     return counts
+
+
+def _router(r, n_experts, H, w_dt, with_bias):
+    """Router weights N(0, 0.02) in w_dt (and the same values as fp32), and an
+    optional bf16 bias N(0, 0.1)."""
+    W = (r.standard_normal(n_experts * H) * 0.02).astype(np.float32)
+    if w_dt == gw.BF16:
+        dev = oracle.f32_to_bf16_bits(W)
+        W = oracle.bf16_bits_to_f32(dev)
+    elif w_dt == gw.F16:
+        dev = W.astype(np.float16)
+        W = dev.astype(np.float32)
+    else:
+        dev = W
+    bias_bits = bias = None
+    if with_bias:
+        bias_bits = oracle.f32_to_bf16_bits((r.standard_normal(n_experts) * 0.1).astype(np.float32))
+        bias = oracle.bf16_bits_to_f32(bias_bits)
+    return dev, W, bias_bits, bias
+
+
+@pytest.mark.parametrize("shape,n_experts,top_k,w_dt,with_bias",
+                         [(GPTOSS, 32, 4, gw.F32, False), (GPTOSS, 128, 4, gw.BF16, True),
+                          (GPTOSS, 64, 4, gw.F16, True), (QWEN3, 128, 8, gw.BF16, False)],
+                         ids=["gptoss20b-f32", "gptoss120b-bf16-bias", "gptoss-64-f16-bias",
+                              "qwen3-bf16"])
+def test_fused_layer_in_kernel_router(ctx, monkeypatch, shape, n_experts, top_k, w_dt, with_bias):
+    """Router weights and one 16-bit token: the one-kernel layer computes the
+    logits itself (each workgroup one slice of one logit, the partials
+    exchanged across the grid), so the layer is one launch with no router
+    kernel.  The two-kernel form's router adds the same slices in the same
+    order: the routing ids and weights are the same bits and the outputs agree
+    to 1e-5 of the peak.  Against the oracle (router_logits then moe_layer,
+    its own summation order): ids equal, weights to 1e-5, the expert metric."""
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _make_layer(ctx, shape, n_experts, 1900 + n_experts)
+    r = rng(1901 + n_experts)
+    xb, xw = _inputs(ctx, r, H, gw.BF16)
+    wdev, W, bias_bits, bias = _router(r, n_experts, H, w_dt, with_bias)
+    wb = ctx.buffer(wdev)
+    bb = ctx.buffer(bias_bits) if with_bias else None
+    kw = dict(router_weight=wb.ptr, router_weight_dtype=w_dt)
+    if with_bias:
+        kw.update(router_bias=bb.ptr, router_bias_dtype=gw.BF16)
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "1")
+    fused = gw.ExpertRunner(ctx, H, F, shape["act"])
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "0")
+    split = gw.ExpertRunner(ctx, H, F, shape["act"])
+    got, counts = {}, {}
+    for name, runner in (("fused", fused), ("split", split)):
+        out, ids_b, w_b = ctx.empty(H * 4), ctx.empty(top_k * 4), ctx.empty(top_k * 4)
+
+        def run():
+            runner.layer_forward(buf.ptr, layout.stride, n_experts, top_k, xb.ptr, gw.BF16, 1,
+                                 out.ptr, routing_ids=ids_b.ptr, routing_weights=w_b.ptr, **kw)
+            ctx.synchronize()
+
+        counts[name] = _kernel_counts(ctx, run, ("moe_layer", "router", "gate_up", "down"))
+        got[name] = (out.download(np.float32, H), ids_b.download(np.int32, top_k),
+                     w_b.download(np.float32, top_k))
+        for b in (out, ids_b, w_b):
+            b.free()
+    assert counts["fused"] == {"moe_layer": 1, "router": 0, "gate_up": 0, "down": 0}, counts
+    assert counts["split"] == {"moe_layer": 0, "router": 1, "gate_up": 1, "down": 1}, counts
+    f_out, f_ids, f_w = got["fused"]
+    s_out, s_ids, s_w = got["split"]
+    assert np.array_equal(f_ids, s_ids)
+    assert np.array_equal(f_w.view(np.uint32), s_w.view(np.uint32))
+    assert np.max(np.abs(f_out - s_out)) <= 1e-5 * np.max(np.abs(s_out))
+    assert fused.sync_errors() == 0
+    logits = oracle.router_logits(W, bias, xw, n_experts, H)
+    ref, rids, rw = oracle.moe_layer([e.oracle_expert() for e in experts], top_k, logits[None, :],
+                                     xw, H, F, shape["oact"])
+    assert list(f_ids) == list(rids[0])
+    assert np.allclose(f_w, rw[0], rtol=1e-5, atol=1e-6)
+    _close(f_out, ref[0])
+    for b in [xb, wb, buf] + ([bb] if with_bias else []):
+        b.free()
+    fused.close()
+    split.close()
 
 
 @pytest.mark.parametrize("shape,n_experts,top_k", [(GPTOSS, 32, 4), (QWEN3, 128, 8)],
@@ -256,9 +336,73 @@ def test_fused_block_chain_per_layer(ctx, monkeypatch, shape, n_experts, top_k, 
     runner.close()
 
 
-def test_exchange_give_up_is_reported_and_falls_back(ctx, monkeypatch):
+def test_in_kernel_router_interleaved_with_logits(ctx, monkeypatch):
+    """One-token layers that alternate given logits and router weights (each
+    launch clears the next launch's router-partial words whether it routes
+    from weights or not), eagerly and replayed from a graph: every layer's
+    routing and output equal the two-kernel form's."""
+    shape, n_experts, top_k = GPTOSS, 32, 4
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _make_layer(ctx, shape, n_experts, 2000)
+    r = rng(2001)
+    pattern = ["router", "logits", "router", "router", "logits", "logits", "router"]
+    xs, srcs, keep = [], [], []
+    for i, kind in enumerate(pattern):
+        xb, _ = _inputs(ctx, r, H, gw.BF16)
+        xs.append(xb)
+        if kind == "router":
+            wdev, _, _, _ = _router(r, n_experts, H, gw.F32, False)
+            wb = ctx.buffer(wdev)
+            srcs.append(dict(router_weight=wb.ptr, router_weight_dtype=gw.F32))
+            keep.append(wb)
+        else:
+            lb = ctx.buffer(r.standard_normal(n_experts).astype(np.float32))
+            srcs.append(dict(logits=lb.ptr))
+            keep.append(lb)
+    res = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("GODWIT_DECODE_LAYER", mode)
+        runner = gw.ExpertRunner(ctx, H, F, shape["act"])
+        outs = [ctx.empty(H * 4) for _ in pattern]
+        ids = [ctx.empty(top_k * 4) for _ in pattern]
+
+        def seq():
+            for i in range(len(pattern)):
+                runner.layer_forward(buf.ptr, layout.stride, n_experts, top_k, xs[i].ptr, gw.BF16,
+                                     1, outs[i].ptr, routing_ids=ids[i].ptr, **srcs[i])
+
+        seq()
+        ctx.synchronize()
+        eager = [(o.download(np.float32, H), d.download(np.int32, top_k)) for o, d in zip(outs, ids)]
+        if mode == "1":
+            graph = gw.Graph.capture(ctx, seq)
+            for _ in range(3):
+                for o in outs:
+                    o.zero()
+                graph.launch()
+                ctx.synchronize()
+                for i, o in enumerate(outs):
+                    assert np.array_equal(o.download(np.float32, H), eager[i][0]), i
+            graph.destroy()
+            assert runner.sync_errors() == 0
+        res[mode] = eager
+        for b in outs + ids:
+            b.free()
+        runner.close()
+    for i in range(len(pattern)):
+        f_out, f_ids = res["1"][i]
+        s_out, s_ids = res["0"][i]
+        assert np.array_equal(f_ids, s_ids), (i, pattern[i])
+        assert np.max(np.abs(f_out - s_out)) <= 1e-5 * np.max(np.abs(s_out)), (i, pattern[i])
+    for b in xs + keep + [buf]:
+        b.free()
+
+
+@pytest.mark.parametrize("router", [False, True], ids=["logits", "router"])
+def test_exchange_give_up_is_reported_and_falls_back(ctx, monkeypatch, router):
     """The bounded exchange wait made to give up from the host: the one-token
-    layer reads a slot no launch writes, with a 64-poll limit.  Every kernel
+    layer reads a slot no launch writes (the activations', and with router
+    weights the router partials' too), with a 64-poll limit.  Every kernel
     exits, the runner counts the waves that gave up, the next synchronize
     reports GW_ERR_EXCHANGE once, and the runner's later one-token layers run
     as two kernels and match the oracle."""
@@ -270,13 +414,20 @@ def test_exchange_give_up_is_reported_and_falls_back(ctx, monkeypatch):
     runner = gw.ExpertRunner(ctx, H, F, shape["act"])
     r = rng(1501)
     xb, xw = _inputs(ctx, r, H, gw.BF16)
-    logits = r.standard_normal(n_experts).astype(np.float32)
-    lb = ctx.buffer(logits)
+    if router:
+        wdev, W, _, _ = _router(r, n_experts, H, gw.F32, False)
+        lb = ctx.buffer(wdev)
+        src = dict(router_weight=lb.ptr, router_weight_dtype=gw.F32)
+        logits = oracle.router_logits(W, None, xw, n_experts, H)
+    else:
+        logits = r.standard_normal(n_experts).astype(np.float32)
+        lb = ctx.buffer(logits)
+        src = dict(logits=lb.ptr)
     out = ctx.empty(H * 4)
     runner.set_wait_limit(64)
     runner.inject_exchange_fault(True)
     counts = _kernel_counts(ctx, lambda: runner.layer_forward(
-        buf.ptr, layout.stride, n_experts, top_k, xb.ptr, gw.BF16, 1, out.ptr, logits=lb.ptr))
+        buf.ptr, layout.stride, n_experts, top_k, xb.ptr, gw.BF16, 1, out.ptr, **src))
     assert counts == {"moe_layer": 1, "gate_up": 0, "down": 0}, counts
     with pytest.raises(gw.GodwitError) as err:
         ctx.synchronize()
@@ -287,8 +438,16 @@ def test_exchange_give_up_is_reported_and_falls_back(ctx, monkeypatch):
     runner.inject_exchange_fault(False)
     runner.set_wait_limit(0)
     got = {}
-    counts = _kernel_counts(ctx, lambda: got.__setitem__(
-        "x", _forward(ctx, runner, layout, buf, n_experts, top_k, xb, gw.BF16, lb, H)))
+    if router:
+        def fwd():
+            runner.layer_forward(buf.ptr, layout.stride, n_experts, top_k, xb.ptr, gw.BF16, 1,
+                                 out.ptr, **src)
+            ctx.synchronize()
+            got["x"] = (out.download(np.float32, H),)
+    else:
+        def fwd():
+            got["x"] = _forward(ctx, runner, layout, buf, n_experts, top_k, xb, gw.BF16, lb, H)
+    counts = _kernel_counts(ctx, fwd)
     assert counts == {"moe_layer": 0, "gate_up": 1, "down": 1}, counts
     ref, _, _ = oracle.moe_layer([e.oracle_expert() for e in experts], top_k, logits[None, :], xw,
                                  H, F, shape["oact"])
@@ -383,3 +542,45 @@ def test_fused_layer_routing_exact(ctx, monkeypatch, shape, n_experts, top_k, ca
         b.free()
     fused.close()
     split.close()
+
+
+def test_fused_layer_cooperative_launch(monkeypatch):
+    """GODWIT_DECODE_COOP=1 at context creation launches the one-token layer
+    through hipLaunchCooperativeKernel (the runtime then refuses a grid that
+    cannot be resident at once).  Eager and graph-replayed layers equal the
+    ordinary launch's bit for bit."""
+    shape, n_experts, top_k = GPTOSS, 32, 4
+    H, F = shape["hidden"], shape["inter"]
+    outs = {}
+    for coop in ("0", "1"):
+        monkeypatch.setenv("GODWIT_DECODE_COOP", coop)
+        monkeypatch.setenv("GODWIT_DECODE_LAYER", "1")
+        c = gw.Context(0)
+        layout, experts, buf = _make_layer(c, shape, n_experts, 1800)
+        runner = gw.ExpertRunner(c, H, F, shape["act"])
+        r = rng(1801)
+        xb, _ = _inputs(c, r, H, gw.BF16)
+        lb = c.buffer(r.standard_normal(n_experts).astype(np.float32))
+        out = c.empty(H * 4)
+
+        def one():
+            runner.layer_forward(buf.ptr, layout.stride, n_experts, top_k, xb.ptr, gw.BF16, 1,
+                                 out.ptr, logits=lb.ptr)
+
+        one()
+        c.synchronize()
+        eager = out.download(np.float32, H)
+        graph = gw.Graph.capture(c, one)
+        out.zero()
+        for _ in range(3):
+            graph.launch()
+        c.synchronize()
+        assert np.array_equal(out.download(np.float32, H), eager)
+        assert runner.sync_errors() == 0
+        outs[coop] = eager
+        graph.destroy()
+        for b in (xb, lb, out, buf):
+            b.free()
+        runner.close()
+        c.close()
+    assert np.array_equal(outs["0"], outs["1"])
