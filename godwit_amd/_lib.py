@@ -8,7 +8,9 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libgodwit_hip.so")
+# GODWIT_TRACE_LIB=1 loads the phase-stamped build (build.py --trace) instead.
+LIB_PATH = os.path.join(HERE, "libgodwit_hip_trace.so" if os.environ.get("GODWIT_TRACE_LIB") == "1"
+                        else "libgodwit_hip.so")
 
 (GW_OK, GW_ERR_ARG, GW_ERR_SHAPE, GW_ERR_OOM, GW_ERR_HIP, GW_ERR_NO_DEVICE, GW_ERR_UNSUPPORTED,
  GW_ERR_EXCHANGE) = range(8)

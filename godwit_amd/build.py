@@ -27,6 +27,9 @@ import time
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libgodwit_hip.so")
+# The same library with the one-token layer's phase stamps compiled in
+# (-DGW_DECODE_TRACE; loaded when GODWIT_TRACE_LIB=1, see decode_timeline.py).
+TRACE_LIB = os.path.join(HERE, "libgodwit_hip_trace.so")
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -93,17 +96,21 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = True) -> str:
+def build(verbose: bool = True, trace: bool = False) -> str:
     """Compiles the sources in parallel (hipcc per HIP file, the host compiler for
-    the host-only C++), then links."""
-    os.makedirs(OBJDIR, exist_ok=True)
+    the host-only C++), then links.  trace=True builds libgodwit_hip_trace.so
+    (phase stamps in the one-token layer kernel) instead."""
+    objdir = OBJDIR + ("_trace" if trace else "")
+    lib_out = TRACE_LIB if trace else LIB
+    extra = ["-DGW_DECODE_TRACE"] if trace else []
+    os.makedirs(objdir, exist_ok=True)
     inc = ["-I", os.path.join(HERE, "..", "include")]
     t0 = time.time()
     procs = []
     for src in SOURCES + HOST_SOURCES:
-        obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
+        obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
         if src.endswith(".hip"):
-            cmd = [HIPCC, *[f for f in FLAGS if f != "-shared"], *inc, "-c", "-o", obj,
+            cmd = [HIPCC, *[f for f in FLAGS if f != "-shared"], *extra, *inc, "-c", "-o", obj,
                    os.path.join(CSRC, src)]
             if src in NO_SPILL:
                 cmd.append("-Rpass-analysis=kernel-resource-usage")
@@ -127,7 +134,7 @@ def build(verbose: bool = True) -> str:
         objs.append(obj)
     if failed:
         raise RuntimeError("hipcc failed")
-    tmp = LIB + ".tmp"
+    tmp = lib_out + ".tmp"
     link = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs],
                           capture_output=True, text=True)
     if link.returncode != 0:
@@ -135,11 +142,11 @@ def build(verbose: bool = True) -> str:
         raise RuntimeError(f"link failed ({link.returncode})")
     if noise and verbose:
         sys.stderr.write("\n".join(noise) + "\n")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib_out)
     if verbose:
-        print(f"built {LIB} in {time.time() - t0:.1f}s")
-    return LIB
+        print(f"built {lib_out} in {time.time() - t0:.1f}s")
+    return lib_out
 
 
 if __name__ == "__main__":
-    build()
+    build(trace="--trace" in sys.argv[1:])

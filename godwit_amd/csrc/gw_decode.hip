@@ -67,6 +67,31 @@ constexpr int kNt = 2;                   // buffer cache policy: non-temporal (s
 constexpr int kSc1 = 16;                 // buffer cache policy: device-coherent (past the L2)
 constexpr uint32_t kOutOfRange = 0x80000000u;   // buffer offset past any layer (reads zero)
 constexpr uint64_t kEmpty = ~0ull;       // an exchange word not written this launch
+
+// Phase timeline (built only with -DGW_DECODE_TRACE, the library
+// libgodwit_hip_trace.so of `build.py --trace`): lane 0 of every wave stores
+// wall_clock64() (100 MHz) at 11 phase boundaries of the layer, one record
+// per (launch % 4, workgroup, wave); gw_debug_decode_trace copies them out.
+// 0 start, 1 routed, 2 gate_up stream queued (gate_up waves) / the gate_up
+// wave's down pieces flagged (DMA waves), 3 exchange phase entered, 4 own
+// pieces flagged and the workgroup's publication seen, 5 exchange reads
+// issued, 6 down weights widened, 7 exchange complete, 8 products issued,
+// 9 combine start, 10 end.
+#ifdef GW_DECODE_TRACE
+constexpr int kTraceStamps = 16;
+__device__ uint64_t g_decode_trace[4 * kDecodeMaxGrid * 8 * kTraceStamps];
+#define GW_TRACE(P)                                                                                \
+    do {                                                                                           \
+        if ((threadIdx.x & 63) == 0)                                                               \
+            g_decode_trace[(((epoch1 & 3u) * kDecodeMaxGrid + blockIdx.x) * 8 + (threadIdx.x >> 6)) * \
+                               kTraceStamps +                                                      \
+                           (P)] = wall_clock64();                                                  \
+    } while (0)
+#else
+#define GW_TRACE(P) \
+    do {            \
+    } while (0)
+#endif
 // Ticks (10 ns) between publishing the router partial and the first read of
 // the grid's partials (a read before the last publisher costs a round trip;
 // measured on MI355X at the GPT-OSS-20B shape: 0: 22.8, 30: 21.1-21.4, 60:
@@ -214,6 +239,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     float *part = reinterpret_cast<float *>(lds8 + L.part);
     // Launches this workgroup has completed (written back at the end).
     const unsigned epoch1 = a.sync.epochs[b] + 1;
+    GW_TRACE(0);
 
     // ---- 1. route while waves 1.. stage x -----------------------------------
     // Up to 128 experts: wave 0 writes the logits' order keys to LDS (0 for
@@ -390,6 +416,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     }
 
     const int segg = lane / TPG, tlg = lane % TPG;
+    GW_TRACE(1);
     const int nrows = 2 * (p1 - p0);
     const int two_f = 2 * F;
     const float inv_two_f = 1.0f / (float)two_f;
@@ -532,6 +559,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"((SPW - CG) * TPW * 2) : "memory");
         if (lane == 0)
             asm volatile("ds_write_b32 %0, %1" ::"v"((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)(ready + d)), "v"(1u) : "memory");
+        GW_TRACE(2);
     } else {
         // ---- 2b. gate_up (waves 0..kGuWaves-1, one per SIMD): RGW rows a
         // stage, a ring of D stages in flight (stage s + D issued once stage s
@@ -629,6 +657,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             }
         });
 #undef GW_ISSUE_STAGE
+        GW_TRACE(2);
         // ---- 3. the activations out: the gate_up waves count themselves done
         // in LDS (their activations are written first); wave 0 waits for the
         // count and publishes the workgroup's words.
@@ -648,6 +677,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         }
     }
 
+    GW_TRACE(3);
     // ---- 4. the exchange: this wave's activation blocks into operand registers
     // Lane (c, g) = lane c + 16 g holds, for each of the wave's steps s, the
     // block 4s + g of expert rank c (c < K; other lanes hold zeros): the B
@@ -675,6 +705,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         if constexpr (PD > 0)
             while ((uint32_t)wall_clock64() - tp < (uint32_t)PD) __builtin_amdgcn_s_sleep(2);
     }
+    GW_TRACE(4);
     const int slot = a.poll_fault ? 2 : (int)(epoch1 & 1u);
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         a.xchg + (size_t)slot * kXSlotWords, (short)0, kDecodeXchgSlotBytes, kRsrcWord3);
@@ -694,6 +725,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     // and the exchange reads are outstanding); a gate_up wave's are all in.
     // ds_read_b128 written out: the compiler would make each read wait for
     // every load in flight.
+    GW_TRACE(5);
     f16x8 AH[UPW][4];
     uint32_t SC[UPW];                    // the units' scale bytes
     uint32_t oor = 0;                    // units whose block this lane dots on the VALU
@@ -779,6 +811,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     for (int j = 0; j < SPW; ++j)
 #pragma unroll
         for (int m = 0; m < 4; ++m) asm volatile("" : "+v"(Bv[j][m]));
+    GW_TRACE(6);
     {
         // Words still empty are read again past this chip's L2 (the first
         // read may be served by an L2 line fetched before they were written).
@@ -811,6 +844,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         }
         if (__ballot(gave_up) != 0ull && lane == 0) atomicAdd(a.sync.err, 1u);
     }
+    GW_TRACE(7);
     // ---- 6. down products on the matrix cores -------------------------------
     f32x4 acc[TPW][2];
     float vf[TPW];
@@ -828,6 +862,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             for (int m = 0; m < 4; ++m)
                 acc[tt][m & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     AH[j * TPW + tt][m], __builtin_bit_cast(f16x8, Bv[j][m]), acc[tt][m & 1], 0, 0, 0);
+    GW_TRACE(8);
     const bool any_fb = __ballot(oor != 0u) != 0ull;
     if (any_fb) {
         // Scale bytes outside the fp16-exact range (rare): the block dotted on
@@ -888,6 +923,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     }
     __syncthreads();
 
+    GW_TRACE(9);
     // ---- 7. bias and combine in router order: dst += out_k * w_k, the product
     // and the sum rounded separately (expert_accumulate).  accumulate: 0
     // overwrite; 1 add to out (applyAssignments); 2 out += the finished sum
@@ -909,6 +945,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         a.out[o] = dst;
         if (a.out_bf16) a.out_bf16[o] = f32_to_bf16_bits(dst);
     }
+    GW_TRACE(10);
     if (threadIdx.x == 0) a.sync.epochs[b] = epoch1;
 }
 
@@ -1032,5 +1069,12 @@ hipError_t launch_decode_layer(const Launch &L, int grid, size_t lds, int x_dt, 
     GW_LAUNCH(kernel, dim3(grid), dim3(kDT), lds, L, a);
     return hipGetLastError();
 }
+
+#ifdef GW_DECODE_TRACE
+extern "C" __attribute__((visibility("default"))) int gw_debug_decode_trace(uint64_t *dst)
+{
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_decode_trace), sizeof(g_decode_trace));
+}
+#endif
 
 }  // namespace gw
