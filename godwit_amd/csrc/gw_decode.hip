@@ -12,6 +12,12 @@
 // need every activation of their expert.  The down rows' addresses are known
 // as soon as the routing is.
 //
+// * routing: from the given logits, or, given the router weights instead
+//   (bf16_gemv_bias, Metal/MoE/router.metal:18-34), from logits the grid
+//   computes first: each workgroup dots one slice of one router row, the
+//   partials go through their own exchange slot and every workgroup adds a
+//   logit's partials in slice order (the standalone router's order too).
+//
 // * gate_up: waves 0-3 (one per SIMD) stream the workgroup's share of gate_up
 //   rows through a ring of register stages and widen and dot each stage as it
 //   lands; the share is a whole number of 4-feature quads, so the workgroup's

@@ -211,4 +211,21 @@ extension ExpertRunner {
         try check(gw_expert_runner_reserve_prefill(handle.runner, Int32(maxTokens), Int32(topK),
                                                    Int32(reader.manifest.expertCount)))
     }
+
+    /// Waves of the one-token layer kernel whose bounded wait for the other
+    /// workgroups gave up since the runner was created (0 while every result
+    /// is valid).  When one gives up, the next `context.synchronize()` throws
+    /// GodwitHIPError with status GW_ERR_EXCHANGE once, and the runner runs
+    /// later one-token layers as two kernels.  Blocks on the stream.
+    public func syncErrors() throws -> Int {
+        var n: UInt32 = 0
+        try check(gw_expert_runner_sync_errors(handle.runner, &n))
+        return Int(n)
+    }
+
+    /// Polls of the one-token layer's exchange before a wait gives up (0: the
+    /// default, 2^18).
+    public func setWaitLimit(_ polls: UInt32) throws {
+        try check(gw_expert_runner_set_wait_limit(handle.runner, polls))
+    }
 }

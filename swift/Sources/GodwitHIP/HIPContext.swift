@@ -34,6 +34,9 @@ public final class HIPContext {
     deinit { _ = gw_context_destroy(handle) }
 
     /// Waits for everything enqueued on the context (MetalContext.run's wait).
+    /// Throws GW_ERR_EXCHANGE (status 7) once when a one-token layer's bounded
+    /// wait gave up since the last call (that layer's outputs are invalid; see
+    /// ExpertRunner.syncErrors).
     public func synchronize() throws { try check(gw_context_synchronize(handle)) }
 
     /// MetalContext.buffer(_:): a device copy of `values`.
