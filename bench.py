@@ -78,7 +78,7 @@ GATE_UP_TRAFFIC = (35_944_526, "gw_kernels.hip", None)
 PREFILL_GATE_UP_TRAFFIC = (1_238_312_316, "gw_prefill.hip", "76b214d588f4f005")
 #   decode_layer_kernel (the one-kernel layer), GPT-OSS-120B, batch 1, over the
 #   whole 36-layer stack (profiles/decode_layer_traffic.md)
-DECODE_LAYER_TRAFFIC = (54_474_373, "gw_decode.hip", "7724ac124bc59cc6")
+DECODE_LAYER_TRAFFIC = (54_488_336, "gw_decode.hip", "79df0fb2fd2bc41d")
 
 
 def source_sha16(name: str) -> str:

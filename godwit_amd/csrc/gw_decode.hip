@@ -260,7 +260,10 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     const bool by_rank = a.experts <= 128;
     uint32_t *rkey = reinterpret_cast<uint32_t *>(lds8 + L.dma);   // keys [128]; the down
     float *rlogit = reinterpret_cast<float *>(lds8 + L.dma + 512);  // pieces come later
-    unsigned *rcount = reinterpret_cast<unsigned *>(lds8 + L.route + 68);   // [kMaxTopK + 1]
+    // the experts placed at each rank, one byte a rank (at most 128 claims,
+    // no carry), and a NaN flag: two LDS reads check the routing
+    unsigned long long *rcnt = reinterpret_cast<unsigned long long *>(lds8 + L.route + 80);
+    unsigned *rnan = reinterpret_cast<unsigned *>(lds8 + L.route + 88);
     bool route_fail = false;   // the router partials' exchange gave up
     // Router partial slots: every launch clears its word of the next launch's
     // slot, whether or not it computes the logits itself (that launch's slot
@@ -349,10 +352,8 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
                 rkey[i] = in && !isn ? order_key(v) : 0u;
                 rlogit[i] = v;
             }
-            // rcount[0..K) count the experts placed at each rank; rcount[K]
-            // flags a NaN
             const bool any_nan = __ballot(nan) != 0ull;
-            if (lane <= K) rcount[lane] = lane == K && any_nan ? 1u : 0u;
+            if (lane == 0) *rcnt = 0ull, *rnan = any_nan ? 1u : 0u;
             if (lane == 0) *gu_done = 0u, *t_pub = 0u, *scl_in = 0u;
             if (lane < 4) ready[lane] = 0u;
         } else {
@@ -389,11 +390,12 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         if (qe == 0 && mk != 0u && gt < K) {
             eid[gt] = ie;
             ew[gt] = rlogit[ie];                  // the logit until the softmax below
-            atomicAdd(rcount + gt, 1u);
+            atomicAdd(rcnt, 1ull << (8 * gt));
         }
         __syncthreads();
-        bool exact = rcount[K] != 0u;
-        for (int r = 0; r < K; ++r) exact |= rcount[r] != 1u;
+        // exactly one expert at each of the K ranks and no NaN, else the
+        // exact selection
+        const bool exact = *rnan != 0u || *rcnt != (0x0101010101010101ull >> (8 * (kMaxTopK - K)));
         if (exact) {                              // uniform: NaN or a tie
             if (wave == 0) {
                 int sid;
