@@ -31,6 +31,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import sys
@@ -728,6 +729,163 @@ def qwen3_bench(gw, args, batch: int) -> int:
     return 0
 
 
+def sign_test_p(ratios) -> float:
+    """Two-sided sign-test p-value of B beating A (ratio > 1), normal
+    approximation; NaN below 8 pairs (ABResult.signTestP,
+    DequantGEMVBenchmark.swift:237-248)."""
+    n = len(ratios)
+    if n < 8:
+        return float("nan")
+    wins = sum(1 for r in ratios if r > 1)
+    z = abs(wins - n / 2) / (math.sqrt(n) / 2)
+    return math.erfc(z / math.sqrt(2.0))
+
+
+def interleaved_ab(sample_a, sample_b, pairs: int) -> dict:
+    """compareInterleaved (DequantGEMVBenchmark.swift:250-286): `pairs` pairs of
+    one timed sample of each side, the side that runs first alternating, so a
+    pair's two samples are milliseconds apart.  A sample returns seconds per
+    step; a pair's ratio is B's throughput over A's."""
+    ratios, ta_all, tb_all = [], [], []
+    for i in range(pairs):
+        if i % 2 == 0:
+            ta = sample_a(i)
+            tb = sample_b(i)
+        else:
+            tb = sample_b(i)
+            ta = sample_a(i)
+        ratios.append(ta / tb)
+        ta_all.append(ta)
+        tb_all.append(tb)
+    s = sorted(ratios)
+    n = len(s)
+    med = s[n // 2] if n % 2 else (s[n // 2 - 1] + s[n // 2]) / 2
+    return {"pairs": n, "median_ratio": round(med, 4),
+            "b_wins": sum(1 for r in ratios if r > 1), "sign_test_p": sign_test_p(ratios),
+            "a_median_us": round(sorted(ta_all)[n // 2] * 1e6, 2),
+            "b_median_us": round(sorted(tb_all)[n // 2] * 1e6, 2),
+            "ratios": [round(r, 4) for r in ratios]}
+
+
+def stack_sampler(gw, ctx, runner, layers, lay, n_layers: int, n_experts: int, top_k: int,
+                  batch: int, logits_all, n_tokens: int, iters: int, seed: int):
+    """One side of an A/B over a decode stack: its own activations, outputs and
+    logits slot on `ctx`, the shared resident layers, the token captured as one
+    graph.  Returns sample(i): `iters` tokens (logits i*iters.. of the shared
+    pool, so both sides route alike), timed between two synchronisations,
+    seconds per token."""
+    H_, step_logits = lay.hidden_size, n_layers * batch * n_experts * 4
+    cur = ctx.empty(step_logits)
+    xs = [ctx.empty(batch * H_ * 2) for _ in range(n_layers + 1)]
+    ctx.fill_normal(xs[0], gw.BF16, batch * H_, 0.0, 1.0, seed * 31 + 9)
+    outs = [ctx.empty(batch * H_ * 4) for _ in range(n_layers)]
+    ctx.synchronize()
+
+    def token():
+        for l in range(n_layers):
+            runner.layer_forward(layers[l].ptr, lay.stride, n_experts, top_k, xs[l].ptr, gw.BF16,
+                                 batch, outs[l].ptr, logits=cur.address(l * batch * n_experts * 4),
+                                 out_bf16=xs[l + 1].ptr)
+
+    graph = gw.Graph.capture(ctx, token)
+
+    def step(t: int):
+        ctx.copy_async(cur.ptr, logits_all.address((t % n_tokens) * step_logits), step_logits)
+        graph.launch()
+
+    for t in range(iters):   # warm-up
+        step(t)
+    ctx.synchronize()
+
+    def sample(i: int) -> float:
+        ctx.synchronize()
+        t0 = time.perf_counter()
+        for t in range(i * iters, (i + 1) * iters):
+            step(t)
+        ctx.synchronize()
+        return (time.perf_counter() - t0) / iters / batch
+
+    return sample
+
+
+def parse_ab(spec: str) -> dict:
+    env = {}
+    for item in spec.split(","):
+        name, sep, val = item.strip().partition("=")
+        if not sep or not name.startswith("GODWIT_"):
+            raise SystemExit(f"--ab takes GODWIT_NAME=VALUE[,GODWIT_NAME=VALUE...], got {item!r}")
+        env[name] = val
+    return env
+
+
+def ab_bench(gw, args) -> int:
+    """The reference's interleaved A/B (DequantGEMVBenchmark.swift:220-286) over
+    the library's runtime switches: A is a context and runner made with the
+    environment as it is, B one made with the `--ab` variables set (they are
+    read at context and runner creation), both in this process over the same
+    resident layers.  Workloads: decode (config 2's 36-layer GPT-OSS-120B
+    stack) and qwen3 / qwen3-b8 (config 3).  Prints one JSON line with the
+    pairs' B/A throughput ratios, their median, B's wins and the sign test."""
+    b_env = parse_ab(args.ab)
+    if args.workload == "decode":
+        Hs, Fs, Es, Ks, Ls, act, batch, biases = H, F, E, K, L, ("gptOssClampedGLU", 7.0, 1.702), 1, True
+    elif args.workload in ("qwen3", "qwen3-b8"):
+        q = QWEN3
+        Hs, Fs, Es, Ks, Ls = q["H"], q["F"], q["E"], q["K"], q["L"]
+        act, biases = ("silu",), False
+        batch = args.batch or (8 if args.workload == "qwen3-b8" else 1)
+    else:
+        raise SystemExit("--ab runs the decode, qwen3 and qwen3-b8 workloads")
+    lay = gw.ExpertLayout(Hs, Fs, Es)
+
+    def side(env: dict):
+        saved = {k: os.environ.get(k) for k in env}
+        os.environ.update(env)
+        try:
+            ctx = gw.Context(0)
+            runner = gw.ExpertRunner(ctx, Hs, Fs, *act)
+            runner.reserve_prefill(batch, Ks, Es)
+        finally:
+            for k, v in saved.items():
+                if v is None:
+                    os.environ.pop(k, None)
+                else:
+                    os.environ[k] = v
+        return ctx, runner
+
+    ctx_a, run_a = side({})
+    ctx_b, run_b = side(b_env)
+    layers = []
+    for l in range(Ls):
+        buf = ctx_a.empty(lay.layer_file_size)
+        fill_layer(ctx_a, gw, buf, lay, Es, args.seed * 1000003 + l * 7919, biases=biases)
+        layers.append(buf)
+    n_tokens = 64
+    logits_all = ctx_a.empty(n_tokens * Ls * batch * Es * 4)
+    ctx_a.fill_normal(logits_all, gw.F32, n_tokens * Ls * batch * Es, 0.0, 1.0, args.seed * 31 + 7)
+    ctx_a.synchronize()
+    log(f"A/B on {args.workload} (batch {batch}): A = the environment as given, "
+        f"B = {', '.join(f'{k}={v}' for k, v in b_env.items())}; {args.ab_pairs} pairs of "
+        f"{args.ab_iters} tokens")
+    sample_a = stack_sampler(gw, ctx_a, run_a, layers, lay, Ls, Es, Ks, batch, logits_all,
+                             n_tokens, args.ab_iters, args.seed)
+    sample_b = stack_sampler(gw, ctx_b, run_b, layers, lay, Ls, Es, Ks, batch, logits_all,
+                             n_tokens, args.ab_iters, args.seed)
+    res = interleaved_ab(sample_a, sample_b, args.ab_pairs)
+    errs = run_a.sync_errors() + run_b.sync_errors()
+    log(f"median B/A {res['median_ratio']:.4f}, B wins {res['b_wins']} of {res['pairs']}, "
+        f"sign test p = {res['sign_test_p']:.3g}; A {res['a_median_us']} us/token, "
+        f"B {res['b_median_us']} us/token; exchange waits that gave up: {errs}")
+    print(json.dumps({"ab": {"workload": args.workload, "batch": batch, "a": "environment as given",
+                             "b": b_env, "iterations_per_sample": args.ab_iters, **res,
+                             "unit": "us/token", "sync_errors": errs}}), flush=True)
+    for r in (run_a, run_b):
+        r.close()
+    for c in (ctx_a, ctx_b):
+        c.close()
+    return 1 if errs else 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -753,6 +911,13 @@ def main() -> int:
                          "qwen3-b8: config 3, the Qwen3 stack at batch 1 / 8; gemv: config 0, "
                          "one gate_up-shaped GEMV; gptoss20b: config 1, a 20B layer with its "
                          "router")
+    ap.add_argument("--ab", default=None, metavar="GODWIT_NAME=VALUE[,...]",
+                    help="interleaved A/B instead of the benchmark line: A = a context and runner "
+                         "made with the environment as given, B = made with these variables set; "
+                         "decode / qwen3 / qwen3-b8 workloads; prints the B/A ratios, their "
+                         "median and a sign test")
+    ap.add_argument("--ab-pairs", type=int, default=40)
+    ap.add_argument("--ab-iters", type=int, default=12, help="tokens per A/B sample")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -763,6 +928,8 @@ def main() -> int:
 
     import godwit_amd as gw
 
+    if args.ab:
+        return ab_bench(gw, args)
     if args.counter_pass:
         return counter_pass(gw, args)
     if args.workload == "prefill":
