@@ -188,6 +188,55 @@ def test_fused_layer_equals_two_kernel_form(ctx, monkeypatch, shape, n_experts, 
     split.close()
 
 
+@pytest.mark.parametrize("shape,n_experts,top_k", [(GPTOSS, 16, 1), (GPTOSS, 16, 2), (GPTOSS, 16, 3),
+                                                   (QWEN3, 32, 1), (QWEN3, 32, 3), (QWEN3, 32, 6)],
+                         ids=["gptoss-k1", "gptoss-k2", "gptoss-k3", "qwen3-k1", "qwen3-k3",
+                              "qwen3-k6"])
+def test_fused_layer_smaller_top_k(ctx, monkeypatch, shape, n_experts, top_k):
+    """Every top-k the one-kernel layer accepts below the models' own (GPT-OSS
+    1-3 of its 4, Qwen3 below 8): fewer down rows per workgroup, so whole
+    tiles, down pieces and exchange reads fall past the rows and read zeros.
+    One launch per layer; the two-kernel form to 1e-5 of the peak, the oracle
+    to the expert metric, routing exact; and three graph replays equal to
+    the eager launch."""
+    H, F = shape["hidden"], shape["inter"]
+    layout, experts, buf = _make_layer(ctx, shape, n_experts, 2100 + 10 * top_k)
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "1")
+    fused = gw.ExpertRunner(ctx, H, F, shape["act"])
+    monkeypatch.setenv("GODWIT_DECODE_LAYER", "0")
+    split = gw.ExpertRunner(ctx, H, F, shape["act"])
+    r = rng(2200 + top_k)
+    xb, xw = _inputs(ctx, r, H, gw.BF16)
+    logits = r.standard_normal(n_experts).astype(np.float32)
+    lb = ctx.buffer(logits)
+    got = {}
+    counts = _kernel_counts(ctx, lambda: got.__setitem__(
+        "fused", _forward(ctx, fused, layout, buf, n_experts, top_k, xb, gw.BF16, lb, H)))
+    assert counts == {"moe_layer": 1, "gate_up": 0, "down": 0}, counts
+    got["split"] = _forward(ctx, split, layout, buf, n_experts, top_k, xb, gw.BF16, lb, H)
+    f_out, f16, f_ids, f_w = got["fused"]
+    s_out, _, s_ids, s_w = got["split"]
+    assert np.array_equal(f_ids, s_ids) and np.array_equal(f_w, s_w)
+    assert np.max(np.abs(f_out - s_out)) <= 1e-5 * np.max(np.abs(s_out))
+    assert np.array_equal(f16, oracle.f32_to_bf16_bits(f_out))
+    rid, rw = oracle.router_select(logits, top_k)
+    assert list(f_ids) == list(rid)
+    assert np.allclose(f_w, rw, rtol=1e-6, atol=1e-7)
+    ref, _, _ = oracle.moe_layer([e.oracle_expert() for e in experts], top_k, logits[None, :],
+                                 xw, H, F, shape["oact"])
+    _close(f_out, ref[0])
+    out = ctx.empty(H * 4)
+    _replay_equals_eager(
+        ctx, lambda: fused.layer_forward(buf.ptr, layout.stride, n_experts, top_k, xb.ptr,
+                                         gw.BF16, 1, out.ptr, logits=lb.ptr),
+        lambda: None, [out], [f_out], replays=3)
+    assert fused.sync_errors() == 0
+    for b in (xb, lb, buf, out):
+        b.free()
+    fused.close()
+    split.close()
+
+
 def _oracle_token(buf, layout, n_experts, top_k, logits, xw, shape):
     """oracle.moe_layer for one token, downloading only the experts the router
     selects (the other entries of the list repeat one of them; the oracle's
