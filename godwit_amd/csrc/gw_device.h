@@ -218,6 +218,23 @@ __device__ __forceinline__ void stage_vector(uint32_t *dst, const void *src, int
     }
 }
 
+// Whether stage_vector's aligned form covers the vector with one batch of 4
+// loads per thread (n4 <= 4 * nthr): a kernel can then issue those loads, queue
+// other loads behind them and store the values to LDS afterwards (the compiler
+// waits for these loads only, the older ones).
+template <int XK> __device__ __forceinline__ bool vector_batch_fits(const void *src, int n, int nthr)
+{
+    const int n4 = XK == DT_F32 ? n / 4 : n / 8;
+    return (reinterpret_cast<uintptr_t>(src) & 15u) == 0 && n4 <= 4 * nthr;
+}
+
+// The 16-byte piece `i` of such a vector into its place in the LDS layout.
+template <int XK> __device__ __forceinline__ void vector_store(uint32_t *dst, int i, const uint4 &v)
+{
+    constexpr int Q = XK == DT_F32 ? 8 : 4, BQ = XL<XK>::kBlockDw / 4;
+    reinterpret_cast<uint4 *>(dst)[(i / Q) * BQ + (i % Q)] = v;
+}
+
 template <int XK>
 __device__ __forceinline__ void stage_vector(uint32_t *dst, const void *src, int n)
 {

@@ -308,8 +308,6 @@ __global__ __launch_bounds__(kNT) void gemv_kernel(const uint8_t *__restrict__ p
     constexpr int TPR = SH::TPR;
     extern __shared__ __align__(16) uint32_t lds[];
     uint32_t *xs = lds;
-    stage_vector<XK>(xs, x, bpr * 32);
-    __syncthreads();
     int r0, r1;
     slice_of(rows, r0, r1);
     const int64_t row_bytes = (int64_t)bpr * 16;
@@ -327,7 +325,32 @@ __global__ __launch_bounds__(kNT) void gemv_kernel(const uint8_t *__restrict__ p
     auto epi = [&](int item, bool valid, int, float (&acc)[1], uint32_t bw, int bsh) {
         if (valid && (threadIdx.x % TPR) == 0) y[r0 + item] = acc[0] + decode_bias(bw, bsh, bias_dt);
     };
-    row_engine<kGemvDepth, XK, 1, SH, true>(r1 - r0, chunks, bpr, xs, rowfn, epi);
+    if (vector_batch_fits<XK>(x, bpr * 32, kNT)) {
+        // x's loads first, the weight stages queued right behind them, then x
+        // into LDS: loads complete in issue order, so x lands first and its
+        // round trip overlaps the weights'.  A bare barrier (a fenced one
+        // would also wait for the weights in flight).
+        const int n4 = (XK == DT_F32 ? 8 : 4) * bpr, last = n4 - 1;
+        const int t = (int)threadIdx.x;
+        const uint4 *xg = static_cast<const uint4 *>(x);
+        const uint4 x0 = xg[min(t, last)], x1 = xg[min(t + kNT, last)];
+        const uint4 x2 = xg[min(t + 2 * kNT, last)], x3 = xg[min(t + 3 * kNT, last)];
+        __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of every weight load
+        EngineRing<kGemvDepth, 1, SH> E;
+        engine_prime<kGemvDepth, 1, SH>(E, r1 - r0, chunks, bpr, rowfn);
+        vector_store<XK>(xs, min(t, last), x0);
+        vector_store<XK>(xs, min(t + kNT, last), x1);
+        vector_store<XK>(xs, min(t + 2 * kNT, last), x2);
+        vector_store<XK>(xs, min(t + 3 * kNT, last), x3);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        engine_run<kGemvDepth, XK, 1, SH, true>(E, r1 - r0, chunks, bpr, xs, rowfn, epi);
+    } else {
+        stage_vector<XK>(xs, x, bpr * 32);
+        __syncthreads();
+        row_engine<kGemvDepth, XK, 1, SH, true>(r1 - r0, chunks, bpr, xs, rowfn, epi);
+    }
 }
 
 // ---------------------------------------------------------------------------
