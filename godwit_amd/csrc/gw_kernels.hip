@@ -325,19 +325,16 @@ __global__ __launch_bounds__(kNT) void gemv_kernel(const uint8_t *__restrict__ p
     auto epi = [&](int item, bool valid, int, float (&acc)[1], uint32_t bw, int bsh) {
         if (valid && (threadIdx.x % TPR) == 0) y[r0 + item] = acc[0] + decode_bias(bw, bsh, bias_dt);
     };
-    if (vector_batch_fits<XK>(x, bpr * 32, kNT)) {
-        // x's loads first, the weight stages queued right behind them, then x
-        // into LDS: loads complete in issue order, so x lands first and its
-        // round trip overlaps the weights'.  A bare barrier (a fenced one
-        // would also wait for the weights in flight).
-        const int n4 = (XK == DT_F32 ? 8 : 4) * bpr, last = n4 - 1;
-        const int t = (int)threadIdx.x;
-        const uint4 *xg = static_cast<const uint4 *>(x);
-        const uint4 x0 = xg[min(t, last)], x1 = xg[min(t + kNT, last)];
-        const uint4 x2 = xg[min(t + 2 * kNT, last)], x3 = xg[min(t + 3 * kNT, last)];
-        __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of every weight load
-        EngineRing<kGemvDepth, 1, SH> E;
-        engine_prime<kGemvDepth, 1, SH>(E, r1 - r0, chunks, bpr, rowfn);
+    const bool fits = vector_batch_fits<XK>(x, bpr * 32, kNT);
+    const int n4 = (XK == DT_F32 ? 8 : 4) * bpr, last = n4 - 1;
+    const int t = (int)threadIdx.x;
+    const uint4 *xg = static_cast<const uint4 *>(x);
+    // x's loads first, the weight loads queued right behind them, then x into
+    // LDS: loads complete in issue order, so x lands first and its round trip
+    // overlaps the weights'.  A bare barrier (a fenced one would also wait for
+    // the weights in flight).  Each form issues its own x loads, so the
+    // compiler's waits see one straight path from them to the weight loads.
+    auto store_x = [&](const uint4 &x0, const uint4 &x1, const uint4 &x2, const uint4 &x3) {
         vector_store<XK>(xs, min(t, last), x0);
         vector_store<XK>(xs, min(t + kNT, last), x1);
         vector_store<XK>(xs, min(t + 2 * kNT, last), x2);
@@ -345,6 +342,44 @@ __global__ __launch_bounds__(kNT) void gemv_kernel(const uint8_t *__restrict__ p
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
+    };
+    if (fits && chunks == 1 && r1 - r0 <= kNT / TPR) {
+        // The workgroup's rows are one stage (the launch shapes of the
+        // standalone GEMV): that stage's loads only, then each block dotted
+        // as it lands (its loads complete in issue order: a block, its scale
+        // byte, the next block ...), in order.
+        const uint4 x0 = xg[min(t, last)], x1 = xg[min(t + kNT, last)];
+        const uint4 x2 = xg[min(t + 2 * kNT, last)], x3 = xg[min(t + 3 * kNT, last)];
+        __builtin_amdgcn_sched_barrier(0);
+        Stage<1, SH::M> S;
+        issue<1, SH>(S, 0, 1, bpr, r1 - r0, rowfn);
+        __builtin_amdgcn_sched_barrier(0);
+        store_x(x0, x1, x2, x3);
+        constexpr int BD = XL<XK>::kBlockDw;
+        const int lane = threadIdx.x % TPR;
+        float acc[1] = {0.0f};
+        Unroll<0, SH::M>::run([&](auto mc) {
+            constexpr int m = decltype(mc)::value;
+            __builtin_amdgcn_sched_barrier(0);
+            u32x4 w = S.w[m];
+            uint32_t sb = S.s[m];
+            asm volatile("" : "+v"(w), "+v"(sb));   // block m's wait here, not hoisted
+            const int cb = lane + m * TPR;
+            const bool use = S.valid && cb < bpr;
+            WBlock<XK> wb;
+            widen_u(w, wb);
+            const float d = block_dot<XK>(wb, xs + (use ? cb : 0) * BD) * decode_scale(sb);
+            acc[0] += use ? d : 0.0f;
+        });
+        acc[0] = seg_sum<TPR>(acc[0]);
+        epi(S.item, S.valid, S.ntok, acc, S.bw, S.bshift);
+    } else if (fits) {
+        const uint4 x0 = xg[min(t, last)], x1 = xg[min(t + kNT, last)];
+        const uint4 x2 = xg[min(t + 2 * kNT, last)], x3 = xg[min(t + 3 * kNT, last)];
+        __builtin_amdgcn_sched_barrier(0);
+        EngineRing<kGemvDepth, 1, SH> E;
+        engine_prime<kGemvDepth, 1, SH>(E, r1 - r0, chunks, bpr, rowfn);
+        store_x(x0, x1, x2, x3);
         engine_run<kGemvDepth, XK, 1, SH, true>(E, r1 - r0, chunks, bpr, xs, rowfn, epi);
     } else {
         stage_vector<XK>(xs, x, bpr * 32);
