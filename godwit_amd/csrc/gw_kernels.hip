@@ -388,6 +388,73 @@ __global__ __launch_bounds__(kNT) void gemv_kernel(const uint8_t *__restrict__ p
     }
 }
 
+// One workgroup of NT threads (384 or 512) per CU, each holding its rows (at
+// most NT / 16: 16 lanes a row, 6 blocks a lane, rows of 65..96 blocks) in
+// one stage, for 17..32 rows per CU: every CU then streams the same share,
+// where 256-thread workgroups of 16 rows would leave some CUs two of them.
+// The order of gemv_kernel's one-stage form: x's loads, the stage's loads, x
+// into LDS, a bare barrier, each block dotted as it lands.  The same blocks,
+// lanes and sums as gemv_kernel, so the same bits.
+template <int XK, int NT>
+__global__ __launch_bounds__(NT) void gemv_wide_kernel(const uint8_t *__restrict__ packed,
+                                                                const uint8_t *__restrict__ scales,
+                                                                const void *__restrict__ bias,
+                                                                int bias_dt,
+                                                                const void *__restrict__ x,
+                                                                float *__restrict__ y, int rows, int bpr)
+{
+    constexpr int TPR = 16, M = 6, BD = XL<XK>::kBlockDw;
+    extern __shared__ __align__(16) uint32_t lds[];
+    uint32_t *xs = lds;
+    int r0, r1;
+    slice_of(rows, r0, r1);
+    const int t = (int)threadIdx.x, lane = t % TPR;
+    const int item = t / TPR, row = r0 + min(item, r1 - r0 - 1);
+    const bool valid = r0 + item < r1;
+    // x: two 16-byte loads per thread cover up to NT * 32 bytes (the host checks)
+    const int n4 = (XK == DT_F32 ? 8 : 4) * bpr, last = n4 - 1;
+    const uint4 xv0 = static_cast<const uint4 *>(x)[min(t, last)];
+    const uint4 xv1 = static_cast<const uint4 *>(x)[min(t + NT, last)];
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t *prow = packed + (int64_t)row * bpr * 16;
+    const uint8_t *srow = scales + (int64_t)row * bpr;
+    u32x4 w[M];
+    uint32_t sb[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const int cb = valid ? min(lane + m * TPR, bpr - 1) : 0;
+        w[m] = load_block(prow, cb);
+        sb[m] = load_scale(srow, cb);
+    }
+    const int bsz = bias_dt == DT_F32 ? 4 : 2;
+    const uintptr_t ba = reinterpret_cast<uintptr_t>(bias_dt >= 0 ? static_cast<const uint8_t *>(bias) +
+                                                                         (int64_t)row * bsz
+                                                                   : srow);
+    const uint32_t bw = *(const __attribute__((address_space(1))) uint32_t *)(ba & ~(uintptr_t)3);
+    __builtin_amdgcn_sched_barrier(0);
+    vector_store<XK>(xs, min(t, last), xv0);   // spares store the last piece again
+    vector_store<XK>(xs, min(t + NT, last), xv1);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    float acc = 0.0f;
+    Unroll<0, M>::run([&](auto mc) {
+        constexpr int m = decltype(mc)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        u32x4 wm = w[m];
+        uint32_t sm = sb[m];
+        asm volatile("" : "+v"(wm), "+v"(sm));   // block m's wait here, not hoisted
+        const int cb = lane + m * TPR;
+        const bool use = valid && cb < bpr;
+        WBlock<XK> wb;
+        widen_u(wm, wb);
+        const float d = block_dot<XK>(wb, xs + (use ? cb : 0) * BD) * decode_scale(sm);
+        acc += use ? d : 0.0f;
+    });
+    acc = seg_sum<TPR>(acc);
+    if (valid && lane == 0) y[row] = acc + decode_bias(bw, (int)(ba & 2u) * 8, bias_dt);
+}
+
 // ---------------------------------------------------------------------------
 // Fused gate_up GEMV + bias + activation (expert.metal:311-368 then :82-102 or
 // :380-393), all groups of a plan.  Rows 2i and 2i+1 of an expert are gate i
@@ -922,6 +989,31 @@ hipError_t launch_gemv(const Launch &L, const uint8_t *packed, const uint8_t *sc
     const int bpr = cols / 32;
     const RowShape s = row_shape(bpr);
     const int rg = kNT / s.tpr;
+    const size_t x_bytes = (size_t)cols * (x_dt == DT_F32 ? 4 : 2);
+    const int per_cu = div_up(rows, L.cus);
+    if (L.grid_a <= 0 && s.tpr == 16 && s.m == 6 && s.chunks == 1 && per_cu > rg && per_cu <= 32 &&
+        (reinterpret_cast<uintptr_t>(x) & 15u) == 0) {
+        // 17..32 rows a CU: one workgroup per CU, all its rows in one stage
+        const int nt = per_cu <= 24 ? 384 : 512;
+        if (x_bytes <= (size_t)nt * 32) {
+            const size_t lds = (size_t)bpr * x_block_dw(x_dt) * 4;
+            auto go = [&](auto ntc) {
+                constexpr int NT = decltype(ntc)::value;
+                if (x_dt == DT_F32)
+                    GW_LAUNCH((gemv_wide_kernel<DT_F32, NT>), dim3(L.cus), dim3(NT), lds, L, packed,
+                              scales, bias, bias_dt, x, y, rows, bpr);
+                else if (x_dt == DT_F16)
+                    GW_LAUNCH((gemv_wide_kernel<DT_F16, NT>), dim3(L.cus), dim3(NT), lds, L, packed,
+                              scales, bias, bias_dt, x, y, rows, bpr);
+                else
+                    GW_LAUNCH((gemv_wide_kernel<DT_BF16, NT>), dim3(L.cus), dim3(NT), lds, L, packed,
+                              scales, bias, bias_dt, x, y, rows, bpr);
+            };
+            if (nt == 384) go(std::integral_constant<int, 384>{});
+            else go(std::integral_constant<int, 512>{});
+            return hipGetLastError();
+        }
+    }
     int grid = L.grid_a > 0 ? L.grid_a : 2 * L.cus;
     grid = grid < div_up(rows, rg) ? grid : div_up(rows, rg);
     const size_t lds = (size_t)bpr * x_block_dw(x_dt) * 4;

@@ -113,16 +113,19 @@ def test_gemv_config0_shape(ctx, x_dtype):
 
 @pytest.mark.parametrize("rows,cols", [(1, 32), (3, 64), (17, 768), (5, 4096), (33, 2048),
                                        (7, 32 * 600), (8196, 2880), (5000, 32 * 100),
-                                       (9, 6144)])
+                                       (9, 6144), (6000, 2176), (7000, 2304)])
 @pytest.mark.parametrize("x_dtype", [gw.BF16, gw.F32], ids=["bf16", "f32"])
 def test_gemv_ragged_shapes(ctx, rows, cols, x_dtype):
     """Ragged row counts and widths, bf16 and fp32 x, against the oracle and
     the float64 sum (rows past 512 workgroups' worth, rows wider than the
     register stages).  Between them they take every staging order of the
-    kernel: a workgroup whose rows are one stage (dotted block by block as
+    kernels: a workgroup whose rows are one stage (dotted block by block as
     they land), several stages or chunks with x's loads issued first (8196
-    rows; 6144 columns in bf16), and x staged before any weight load (x wider
-    than one batch of loads: 19200 columns, 6144 in fp32)."""
+    rows; 6144 columns in bf16), x staged before any weight load (x wider
+    than one batch of loads: 19200 columns, 6144 in fp32), and the
+    one-workgroup-per-CU form for 17..32 rows a CU of 65..96 blocks, 384
+    threads up to 24 rows (6000 x 2176; the config-0 shape too) and 512
+    beyond (7000 x 2304, on 256 CUs)."""
     r = rng(rows * 1000 + cols)
     packed, scales = mxfp4_matrix(r, rows, cols)
     bits, bias = bias_bf16(r, rows)
