@@ -709,10 +709,11 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
     // waves (after which every row of chunk q+1 is in LDS and nobody reads
     // chunk q's buffer any more).
     const int nq = (nb + kKC - 1) / kKC;
-    auto step = [&](int q, auto s_const, auto fb_const) {
+    auto step = [&](int q, auto s_const, auto fb_const, auto guard_const) {
         constexpr int s = decltype(s_const)::value;
         constexpr int sn = (s + D - 1) % D;
-        if (q >= nq) return;                          // uniform: past the last chunk
+        if constexpr (decltype(guard_const)::value)
+            if (q >= nq) return;                      // uniform: past the last chunk
         if constexpr (decltype(fb_const)::value) {
             // The split body: the same staging and barrier as the other
             // waves, but this chunk's weights loaded here and every load
@@ -823,10 +824,35 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
     // fp16 range, the split one: two copies of the loop rather than a branch
     // per chunk, so neither body's registers are held across the other.
     // Barriers match between the copies (one per step).
+    // The common K sizes (12, 8 and 4 chunks, padded to the ring depth: hidden
+    // or intermediate 2880, 2048, 768 ...) have their steps written out, the
+    // guard only in the last ring-depth group: where a loop's back edge, or a
+    // guard's skip path, meets the next step, the compiler's wait bookkeeping
+    // no longer knows that a ring slot's last load was used a step ago, and
+    // waits for nearly every load in flight before reusing the slot's
+    // registers (the ring drains each step).  Other sizes take the loop.
+    // (Written out only where it costs no register spill or stack: the
+    // 4-wave 2-deep and 8-wave 4-deep shapes with one or two input planes,
+    // and in the down GEMM only the fp16 body; the shapes held to fewer
+    // registers and the rare split body keep the loop.)
+    constexpr bool kWriteOutShape = PL <= 2 && ((W == 4 && D == 2) || (W == 8 && D == 4));
     auto kloop = [&](auto fb_const) {
-        for (int q = 0; q < nq_pad; q += D)
-            Unroll<0, D>::run(
-                [&](auto s_const) { step(q + decltype(s_const)::value, s_const, fb_const); });
+        constexpr bool kWriteOut = kWriteOutShape && !decltype(fb_const)::value;
+        auto written_out = [&](auto nc) {
+            constexpr int N = decltype(nc)::value;
+            Unroll<0, N>::run([&](auto qc) {
+                constexpr int q = decltype(qc)::value;
+                step(q, std::integral_constant<int, q % D>{}, fb_const,
+                     std::integral_constant<bool, (q >= N - D)>{});
+            });
+        };
+        if (kWriteOut && nq_pad == 12) written_out(std::integral_constant<int, 12>{});
+        else if (kWriteOut && nq_pad == 8) written_out(std::integral_constant<int, 8>{});
+        else if (kWriteOut && nq_pad == 4) written_out(std::integral_constant<int, 4>{});
+        else
+            for (int q = 0; q < nq_pad; q += D)
+                Unroll<0, D>::run(
+                    [&](auto s_const) { step(q + decltype(s_const)::value, s_const, fb_const, std::true_type{}); });
     };
     if constexpr (F16IN) {
         if (f16ok) kloop(std::false_type{});
