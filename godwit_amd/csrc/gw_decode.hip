@@ -82,7 +82,8 @@ constexpr uint64_t kEmpty = ~0ull;       // an exchange word not written this la
 // wave's down pieces flagged (DMA waves), 3 exchange phase entered, 4 own
 // pieces flagged and the workgroup's publication seen, 5 exchange reads
 // issued, 6 down weights widened, 7 exchange complete, 8 products issued,
-// 9 combine start, 10 end.
+// 9 combine start, 10 end; 11 the exchange words' first check, 12 partial
+// sums written.
 #ifdef GW_DECODE_TRACE
 constexpr int kTraceStamps = 16;
 __device__ uint64_t g_decode_trace[4 * kDecodeMaxGrid * 8 * kTraceStamps];
@@ -124,9 +125,10 @@ template <int TPR_, int M_> struct DShape {
 // pieces: 1 KiB pieces of the down rows (one per unit); scale_pieces: 1 KiB
 // pieces of their scale bytes; parts: fp32 partial sums of the down rows
 // (step groups x rows); rows_per_wg: gate_up rows a workgroup can hold (its
-// fp16 activations take that many bytes at most).
+// fp16 activations take that many bytes at most); bx_pieces: 1 KiB pieces of
+// the DMA waves' exchange words, read for them by the gate_up waves.
 __host__ __device__ inline DecodeLds decode_lds(int hidden, int pieces, int scale_pieces, int parts,
-                                               int rows_per_wg)
+                                               int rows_per_wg, int bx_pieces)
 {
     DecodeLds l;
     const int hb = hidden / 32;
@@ -136,7 +138,8 @@ __host__ __device__ inline DecodeLds decode_lds(int hidden, int pieces, int scal
     l.dma = (l.actl + rows_per_wg + 255) & ~255;   // down pieces (routing keys before them)
     l.scl = l.dma + (pieces > 1 ? pieces : 1) * kChunk;
     l.part = l.scl + scale_pieces * kChunk;
-    l.total = l.part + parts * 4;
+    l.bx = (l.part + parts * 4 + 15) & ~15;
+    l.total = l.bx + bx_pieces * kChunk;
     return l;
 }
 
@@ -211,7 +214,9 @@ __device__ __forceinline__ uint32_t pair_empty(const u32x4 &v)
 // wave takes TD / WT tiles); the kDW / WT step groups take SPW steps of four
 // blocks each.  NSP: 1 KiB pieces of down scale bytes each DMA wave copies.  PD: ticks of the 100 MHz real-time counter between the
 // workgroup publishing its activations and its first read of the exchange.
-template <int XK, class GS, int NSG, int GD, int TD, int WT, int SPW, int NSP, int PD>
+// PX: a gate_up wave reads its DMA partner's exchange words into LDS (else
+// every wave reads its own).
+template <int XK, class GS, int NSG, int GD, int TD, int WT, int SPW, int NSP, int PD, bool PX>
 __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
 {
     constexpr int TPG = GS::TPR, MG = GS::M, SEGG = 64 / TPG, RGW = kGuWaves * SEGG;
@@ -233,13 +238,15 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     slice_of(H, r0, r1);
     const int nr = r1 - r0;
     const int nrows_dn = K * nr;         // down rows, expert-major: row k * nr + q
-    const DecodeLds L = decode_lds(H, kDW * UPW, (kDW - kGuWaves) * NSP, WS * 16 * TD, RGW * NSG);
+    const DecodeLds L = decode_lds(H, kDW * UPW, (kDW - kGuWaves) * NSP, WS * 16 * TD, RGW * NSG,
+                                   PX ? (kDW - kGuWaves) * SPW * 4 : 0);
     int32_t *eid = reinterpret_cast<int32_t *>(lds8 + L.route);
     float *ew = reinterpret_cast<float *>(lds8 + L.route + 32);
     unsigned *gu_done = reinterpret_cast<unsigned *>(lds8 + L.route + 64);   // gate_up waves done
     unsigned *ready = reinterpret_cast<unsigned *>(lds8 + L.route + 112);    // [4] gate_up waves' units landed
     unsigned *t_pub = reinterpret_cast<unsigned *>(lds8 + L.route + 128);    // publish time (0: not yet)
     unsigned *scl_in = reinterpret_cast<unsigned *>(lds8 + L.route + 132);   // DMA waves' scale pieces landed
+    unsigned *bx_in = reinterpret_cast<unsigned *>(lds8 + L.route + 144);    // [4] DMA waves' exchange words landed
     uint32_t *xs = reinterpret_cast<uint32_t *>(lds8 + L.xs);
     uint16_t *actl = reinterpret_cast<uint16_t *>(lds8 + L.actl);
     float *part = reinterpret_cast<float *>(lds8 + L.part);
@@ -355,10 +362,10 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             const bool any_nan = __ballot(nan) != 0ull;
             if (lane == 0) *rcnt = 0ull, *rnan = any_nan ? 1u : 0u;
             if (lane == 0) *gu_done = 0u, *t_pub = 0u, *scl_in = 0u;
-            if (lane < 4) ready[lane] = 0u;
+            if (lane < 4) ready[lane] = 0u, bx_in[lane] = 0u;
         } else {
             if (lane == 0) *gu_done = 0u, *t_pub = 0u, *scl_in = 0u;
-            if (lane < 4) ready[lane] = 0u;
+            if (lane < 4) ready[lane] = 0u, bx_in[lane] = 0u;
             int sid;
             float w;
             select_one<4>(a.logits, a.experts, K, sid, w);
@@ -690,21 +697,26 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     // Lane (c, g) = lane c + 16 g holds, for each of the wave's steps s, the
     // block 4s + g of expert rank c (c < K; other lanes hold zeros): the B
     // operand of the unit's four MFMAs, one fp16 octet each.  A gate_up wave
-    // reads once its units' pieces are flagged, a DMA wave once it has flagged
-    // its gate_up wave's, both at least PD ticks after this workgroup
-    // published; the reads queue behind the down pieces still in flight.
-    // Waits on this workgroup's own waves (all resident with it) are bounded by
-    // the fixed kDecodeSpinLimit, not the caller's exchange limit, and a wait
-    // that ran out is counted like a failed exchange wait.
+    // reads its own once its units' pieces are flagged and PD ticks after this
+    // workgroup published.  With PX, after widening its units, it reads its
+    // DMA partner's into LDS (past this chip's L2, by LDS-DMA) and flags them
+    // once they are in, so a DMA wave's words do not queue behind its own
+    // down pieces (a wave's loads complete in order); else a DMA wave reads
+    // its own at the same point as the gate_up wave, behind its pieces.
+    // Waits on this workgroup's own waves (all resident with it) are bounded
+    // by the fixed kDecodeSpinLimit, not the caller's exchange limit, and a
+    // wait that ran out is counted like a failed exchange wait.
     bool local_fail = false;
-    if (wave < kGuWaves) {
+    const bool dma_wave = wave >= kGuWaves;
+    const bool own_reads = !PX || !dma_wave;
+    if (!dma_wave) {
         unsigned spins = 0;
         while (lds_peek(ready + wave) == 0u) {
             if (++spins > kDecodeSpinLimit) { local_fail = true; break; }   // the DMA wave flags them
             __builtin_amdgcn_s_sleep(1);
         }
     }
-    {
+    if (own_reads) {
         unsigned spins = 0, tp;
         while ((tp = lds_peek(t_pub)) == 0u) {
             if (++spins > kDecodeSpinLimit) { local_fail = true; break; }   // wave 0 publishes
@@ -717,20 +729,28 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     const int slot = a.poll_fault ? 2 : (int)(epoch1 & 1u);
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         a.xchg + (size_t)slot * kXSlotWords, (short)0, kDecodeXchgSlotBytes, kRsrcWord3);
+    // the words of step group kind k's j-th step for this lane
+    auto word_off = [&](int k, int j) -> uint32_t {
+        const int blk = 4 * (sbase + k * SPW + j) + gr;
+        const bool ok = (rr < K) & (blk < fb);   // a select, not a branch
+        return ok ? (uint32_t)((rr * F + 32 * blk) * 2) : kOutOfRange;
+    };
     uint32_t boff[SPW];
     u32x4 Bv[SPW][4];
 #pragma unroll
-    for (int j = 0; j < SPW; ++j) {
-        const int blk = 4 * (sbase + kind * SPW + j) + gr;
-        boff[j] = rr < K && blk < fb ? (uint32_t)((rr * F + 32 * blk) * 2) : kOutOfRange;
+    for (int j = 0; j < SPW; ++j) boff[j] = word_off(kind, j);
+    if (own_reads) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-            Bv[j][m] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, boff[j] + 16u * m, 0, 0));
+        for (int j = 0; j < SPW; ++j)
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                Bv[j][m] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, boff[j] + 16u * m, 0, 0));
     }
     // ---- 5. this wave's units widened to fp16 while the exchange is in flight
     // A DMA wave takes each of its own pieces as it lands (the vector-memory
-    // counter completes in order: piece i is in once only the later pieces
-    // and the exchange reads are outstanding); a gate_up wave's are all in.
+    // counter completes in order: piece i is in once only the later pieces,
+    // and its own exchange reads when it makes them, are outstanding); a
+    // gate_up wave's are all in.
     // ds_read_b128 written out: the compiler would make each read wait for
     // every load in flight.
     GW_TRACE(5);
@@ -742,7 +762,6 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
         // block gr of the step's four (slot (4 (step & 1) + gr) ^ (rr & 7))
         const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)(lds8 + L.dma) +
                               (uint32_t)(simd * PPS * kChunk + (rr >> 3) * kChunk + (rr & 7) * 128);
-        const bool dma_wave = wave >= kGuWaves;
         {
             unsigned spins = 0;
             while (lds_peek(scl_in) < (unsigned)(kDW - kGuWaves)) {
@@ -774,10 +793,10 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             Unroll<0, UPW>::run([&](auto ic) {
                 constexpr int i = decltype(ic)::value, j = i / TPW, tt = i % TPW;
                 // a DMA wave's unit has landed once only later chunks' pieces
-                // and the exchange reads are in flight
+                // are in flight
                 if constexpr (j == 0 || ((SPW + j) >> 1) != ((SPW + j - 1) >> 1)) {
                     constexpr int later = SPW - 1 - ((SPW + j) >> 1);
-                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(later * TPW * 2 + 4 * SPW) : "memory");
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(later * TPW * 2 + (PX ? 0 : 4 * SPW)) : "memory");
                 }
                 uint32_t wa, sa;
                 bool live;
@@ -813,22 +832,60 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             }
         }
     }
-    // the exchange reads are looked at only now, after the widening (the
-    // compiler would hoist the check, and its wait for them, above it)
+    GW_TRACE(6);
+    if (PX && !dma_wave) {
+        // the DMA partner's words into LDS past this chip's L2 (each lane's
+        // 16-byte reads as in its own registers), flagged once all of this
+        // wave's loads are in; its own words were read before the widening
+        uint8_t *bxw = lds8 + L.bx + simd * SPW * 4 * kChunk;
+#pragma unroll
+        for (int j = 0; j < SPW; ++j) {
+            const uint32_t po = word_off(1, j);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const uint32_t voff = po + 16u * (uint32_t)m;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (l_void *)(bxw + (j * 4 + m) * kChunk), 16, voff, 0, 0,
+                                                         kSc1);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (lane == 0)
+            asm volatile("ds_write_b32 %0, %1"
+                         ::"v"((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)(bx_in + simd)), "v"(1u)
+                         : "memory");
+    }
+    uint32_t pend = 0;
+    if (PX && dma_wave) {
+        // this wave's words, read for it by its gate_up wave
+        unsigned spins = 0;
+        while (lds_peek(bx_in + simd) == 0u) {
+            if (++spins > 4u * kDecodeSpinLimit) { local_fail = true; break; }   // the gate_up wave flags them
+            __builtin_amdgcn_s_sleep(1);
+        }
+        const uint32_t bxa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)(lds8 + L.bx) +
+                             (uint32_t)(simd * SPW * 4 * kChunk + lane * 16);
+#pragma unroll
+        for (int j = 0; j < SPW; ++j)
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(Bv[j][m]) : "v"(bxa), "i"((j * 4 + m) * kChunk));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    // the reads are looked at only now, after the widening (the compiler
+    // would hoist the check, and its wait for them, above it)
 #pragma unroll
     for (int j = 0; j < SPW; ++j)
 #pragma unroll
         for (int m = 0; m < 4; ++m) asm volatile("" : "+v"(Bv[j][m]));
-    GW_TRACE(6);
     {
         // Words still empty are read again past this chip's L2 (the first
         // read may be served by an L2 line fetched before they were written).
-        uint32_t pend = 0;
 #pragma unroll
         for (int j = 0; j < SPW; ++j)
 #pragma unroll
             for (int m = 0; m < 4; ++m)
                 pend |= pair_empty(Bv[j][m]) << (4 * j + m);
+        GW_TRACE(11);
         unsigned spins = 0;
         bool gave_up = local_fail || route_fail;
         while (pend) {
@@ -904,7 +961,9 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             }
     }
     // Partial sum of row rho = 16 t + r from its expert's column: lane l holds
-    // D[4 (l >> 4) + v][l & 15].
+    // D[4 (l >> 4) + v][l & 15], and column c is expert rank c, whose rows are
+    // [c * nr, c * nr + nr) (two compares, no division).
+    const int rlo = rr < K ? rr * nr : 0, rhi = rr < K ? rlo + nr : 0;
 #pragma unroll
     for (int tt = 0; tt < TPW; ++tt) {
         const int t = tg * TPW + tt;
@@ -912,9 +971,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int rho = 16 * t + 4 * gr + v;
-            int k, q;
-            divmod_small(rho < nrows_dn ? rho : 0, nr, inv_nr, k, q);
-            if (rho < nrows_dn && k == rr) part[sg * 16 * TD + rho] = dsum[v];
+            if (rho >= rlo && rho < rhi) part[sg * 16 * TD + rho] = dsum[v];
         }
     }
     if (any_fb) {
@@ -929,6 +986,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
             if (gr == 0 && rho < nrows_dn) part[sg * 16 * TD + rho] += v;
         }
     }
+    GW_TRACE(12);
     __syncthreads();
 
     GW_TRACE(9);
@@ -939,15 +997,23 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     if (wave == kGuWaves && lane < nr) {
         const int64_t o = r0 + lane;
         float dst = a.accumulate == 1 ? a.out[o] : 0.0f;
+        // every partial and weight read at once (rank K - 1's again past K),
+        // then summed in step-group and router order
+        float pv[kMaxTopK][WS], wk[kMaxTopK];
 #pragma unroll
         for (int k = 0; k < kMaxTopK; ++k) {
-            if (k < K) {
-                const int rho = k * nr + lane;
-                float v = part[rho];
+            const int kk = k < K ? k : K - 1, rho = kk * nr + lane;
 #pragma unroll
-                for (int g = 1; g < WS; ++g) v += part[g * 16 * TD + rho];
-                dst = add_scaled_rn(dst, v + bias_of(BW[k], BSHF[k], a.bias_dt), ew[k]);
-            }
+            for (int g = 0; g < WS; ++g) pv[k][g] = part[g * 16 * TD + rho];
+            wk[k] = ew[kk];
+        }
+#pragma unroll
+        for (int k = 0; k < kMaxTopK; ++k) {
+            float v = pv[k][0];
+#pragma unroll
+            for (int g = 1; g < WS; ++g) v += pv[k][g];
+            const float nd = add_scaled_rn(dst, v + bias_of(BW[k], BSHF[k], a.bias_dt), wk[k]);
+            dst = k < K ? nd : dst;
         }
         if (a.accumulate == 2) dst = a.out[o] + dst;
         a.out[o] = dst;
@@ -983,6 +1049,9 @@ constexpr int kScalePieces[2] = {2, 1};   // per DMA wave
 // the same from 0 to 1 us (the reads queue behind the down pieces anyway);
 // Qwen3 0.3 us is best.
 constexpr int kPollDelay[2] = {60, 30};
+// The gate_up waves read their DMA partners' exchange words (GPT-OSS: the
+// DMA waves' reads would complete only behind their down pieces).
+constexpr bool kPartnerReads[2] = {true, false};
 
 int shape_of(int hidden, int inter)
 {
@@ -995,7 +1064,7 @@ int shape_of(int hidden, int inter)
 
 #define GW_DECODE_KERNEL(S, XD)                                                                 \
     decode_layer_kernel<XD, DShape<16, (S) == kShapeGptOss ? 6 : 4>, kStagesG[S], kRingG[S], kTiles[S], \
-                        kTileGroups[S], kStepsPerWave[S], kScalePieces[S], kPollDelay[S]>
+                        kTileGroups[S], kStepsPerWave[S], kScalePieces[S], kPollDelay[S], kPartnerReads[S]>
 
 typedef void (*DecodeKernel)(DecodeArgs);
 
@@ -1036,7 +1105,8 @@ int decode_layer_plan(const Launch &L, int hidden, int inter, int x_dt, int top_
     // every expert's scale window (from a 16-byte aligned start) fits the pieces
     if (top_k * ((nrmax * fb + 15 + 15) & ~15) > (8 - kGuWaves) * kScalePieces[shape] * kChunk) return 0;
     const DecodeLds l = decode_lds(hidden, 8 * (kTiles[shape] / wt) * spw, (8 - kGuWaves) * kScalePieces[shape],
-                                   (8 / wt) * 16 * kTiles[shape], kStagesG[shape] * kRowsPerStage[shape]);
+                                   (8 / wt) * 16 * kTiles[shape], kStagesG[shape] * kRowsPerStage[shape],
+                                   kPartnerReads[shape] ? (8 - kGuWaves) * spw * 4 : 0);
     if (l.total > kDecodeLdsMax) return 0;
     // The exchange needs the whole grid resident: one workgroup per CU.
     const void *fn = reinterpret_cast<const void *>(kernel_for(shape, x_dt));

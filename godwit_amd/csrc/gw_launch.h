@@ -121,7 +121,7 @@ struct DecodeArgs {
     int rb_dt;
     int rslices;
 };
-struct DecodeLds { int route, xs, actl, dma, scl, part, total; };
+struct DecodeLds { int route, xs, actl, dma, scl, part, bx, total; };
 
 // Grid (one workgroup per CU) of the one-kernel layer for this shape, or 0
 // when it is not available (shape, dtype or top-k not built, LDS, or the grid

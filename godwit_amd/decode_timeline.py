@@ -6,7 +6,7 @@
 
 Loads libgodwit_hip_trace.so (the library built with -DGW_DECODE_TRACE),
 whose layer kernel stores wall_clock64() (100 MHz) from lane 0 of every wave
-at 11 phase boundaries.  A stack of `layers` layers (default 12) with fresh
+at 13 phase boundaries.  A stack of `layers` layers (default 12) with fresh
 synthetic experts (nibbles U{0..15}, scales U{119..127}, GPT-OSS biases
 N(0, 0.02)) and logits N(0, 1) is captured as one graph of one-token layers,
 each layer's bf16 output the next one's input, as in bench.py's decode
@@ -31,7 +31,7 @@ from godwit_amd._lib import lib  # noqa: E402
 
 PHASES = ["start", "routed", "stream queued/flagged", "exchange phase", "own pieces + publish",
           "exchange reads out", "down widened", "exchange complete", "products issued",
-          "combine start", "end"]
+          "combine start", "end", "first word check", "partials written"]
 SHAPES = {"gptoss": (2880, 2880, 128, 4, "gptOssClampedGLU", True),
           "qwen3": (2048, 768, 128, 8, "silu", False)}
 LAUNCH_SLOTS, MAX_GRID, WAVES, STAMPS = 4, 256, 8, 16
@@ -112,6 +112,18 @@ def main():
                 med.append(np.median(v))
                 mx.append(v.max())
             print(f"  {p:2d} {label:22s} median {np.median(med):6.2f}  max {np.median(mx):6.2f}")
+    print("== per wave: median over samples of the median over workgroups (us)")
+    print("  " + " " * 25 + " ".join(f"  w{w}  " for w in range(WAVES)))
+    for p, label in enumerate(PHASES):
+        row = []
+        for w in range(WAVES):
+            row.append(np.median([np.median((t[:, w, p] - t[:, :, 0].min()) * 0.01) for t in samples]))
+        print(f"  {p:2d} {label:22s}" + " ".join(f"{v:6.2f}" for v in row))
+    print("== within a workgroup: median over samples and workgroups of the latest wave minus the "
+          "workgroup's median wave (us)")
+    for p in (6, 11, 7, 8, 12):
+        d = [np.median((t[:, :, p].max(axis=1) - np.median(t[:, :, p], axis=1)) * 0.01) for t in samples]
+        print(f"  {p:2d} {PHASES[p]:22s} {np.median(d):5.2f}")
     spans = [(t[:, :, 10].max() - t[:, :, 0].min()) * 0.01 for t in samples]
     print("span, first start to last end, per sample (us):", " ".join(f"{v:.2f}" for v in spans))
     graph.destroy()
