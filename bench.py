@@ -79,7 +79,7 @@ GATE_UP_TRAFFIC = (35_944_526, "gw_kernels.hip", None)
 PREFILL_GATE_UP_TRAFFIC = (1_251_374_667, "gw_prefill.hip", "009cf73ce30a432c")
 #   decode_layer_kernel (the one-kernel layer), GPT-OSS-120B, batch 1, over the
 #   whole 36-layer stack (profiles/decode_layer_traffic.md)
-DECODE_LAYER_TRAFFIC = (54_488_336, "gw_decode.hip", "79df0fb2fd2bc41d")
+DECODE_LAYER_TRAFFIC = (54_469_014, "gw_decode.hip", "723e1fa7217756e3")
 
 
 def source_sha16(name: str) -> str:

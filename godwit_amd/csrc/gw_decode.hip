@@ -87,14 +87,19 @@ constexpr uint64_t kEmpty = ~0ull;       // an exchange word not written this la
 #ifdef GW_DECODE_TRACE
 constexpr int kTraceStamps = 16;
 __device__ uint64_t g_decode_trace[4 * kDecodeMaxGrid * 8 * kTraceStamps];
+// The wave's stamp row is addressed once (a scalar load of the array's
+// address before every stamp would delay the code after it).
+#define GW_TRACE_ROW()                                                                             \
+    uint64_t *const gw_trace_row =                                                                 \
+        g_decode_trace + (((epoch1 & 3u) * kDecodeMaxGrid + blockIdx.x) * 8 + (threadIdx.x >> 6)) * kTraceStamps
 #define GW_TRACE(P)                                                                                \
     do {                                                                                           \
-        if ((threadIdx.x & 63) == 0)                                                               \
-            g_decode_trace[(((epoch1 & 3u) * kDecodeMaxGrid + blockIdx.x) * 8 + (threadIdx.x >> 6)) * \
-                               kTraceStamps +                                                      \
-                           (P)] = wall_clock64();                                                  \
+        if ((threadIdx.x & 63) == 0) gw_trace_row[(P)] = wall_clock64();                           \
     } while (0)
 #else
+#define GW_TRACE_ROW() \
+    do {               \
+    } while (0)
 #define GW_TRACE(P) \
     do {            \
     } while (0)
@@ -252,6 +257,7 @@ __global__ __launch_bounds__(kDT) void decode_layer_kernel(DecodeArgs a)
     float *part = reinterpret_cast<float *>(lds8 + L.part);
     // Launches this workgroup has completed (written back at the end).
     const unsigned epoch1 = a.sync.epochs[b] + 1;
+    GW_TRACE_ROW();
     GW_TRACE(0);
 
     // ---- 1. route while waves 1.. stage x -----------------------------------
