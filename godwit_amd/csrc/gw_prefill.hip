@@ -179,11 +179,12 @@ __global__ __launch_bounds__(kGroupThreads) void prefill_group_kernel(
 // (bf16 x: the input itself; fp16 or fp32 x: split beforehand); the down
 // input is one plane of fp16 activations, written by the gate_up epilogue.  Per
 // chunk a lane (row r = lane & 31, half h = lane >> 5) holds its row's blocks
-// 4h .. 4h+3 (64 contiguous bytes), widened to bf16 with the block scale
-// folded in; MFMA 4i+d takes dword d of block 4h+i, i.e. chunk elements
-// 128h + 32i + 8d .. +7, from A (weights) and from B (the staged activation
-// row of entry r), so A and B share one K order.  C element v of a lane is
-// feature row 8(v/4) + 4h + (v%4), entry column lane & 31.
+// 2i + h, i = 0..3 (so the two lanes of a row read 32 contiguous bytes per
+// load instruction), widened to bf16 with the block scale folded in; MFMA
+// 4i+d takes dword d of block 2i+h, i.e. chunk elements 64i + 32h + 8d .. +7,
+// from A (weights) and from B (the staged activation row of entry r), so A
+// and B share one K order.  C element v of a lane is feature row 8(v/4) +
+// 4h + (v%4), entry column lane & 31.
 //
 // Pipeline.  A chunk's activations are staged by LDS-DMA (16 bytes per lane
 // straight into LDS, no registers) and its weights are loaded into a
@@ -534,16 +535,18 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
         }
     };
 
-    // Weight ring: per chunk a lane's four 16-byte blocks 4h .. 4h+3 (64
-    // contiguous bytes of its row).  Block indices past nb clamp to the row's
-    // last block.  The loaded words are used only when their chunk is
-    // multiplied (arithmetic on them here would wait for the load just issued).
+    // Weight ring: per chunk a lane's four 16-byte blocks 2i + h (load i
+    // reads 32 contiguous bytes of each of the wave's 32 rows; the fewer lines
+    // a load instruction touches, the fewer requests the texture path makes:
+    // blocks 4h + i, two pieces 64 bytes apart, took 11% longer at 512
+    // tokens).  Block indices past nb clamp to the row's last block.  The
+    // loaded words are used only when their chunk is multiplied (arithmetic
+    // on them here would wait for the load just issued).
     u32x4v wq[D][4];
     auto wload = [&](int slot, int q) {
-        const int base = q * kKC + 4 * h;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int bb = min(base + i, nb - 1);
+            const int bb = min(q * kKC + 2 * i + h, nb - 1);
             wq[slot][i] = *(g_u32x4v *)(wrow + (int64_t)bb * 16);
         }
     };
@@ -555,12 +558,16 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
         acc1[i] = 0.0f;
     }
 
-    // B read address of piece 16h + j for entry c: row c, slot (j ^ (c & 15)).
-    const uint32_t rb = (uint32_t)(c * kRowBytes + 256 * h + ((c & 15) << 4));
+    // B read address of piece p for entry c: row c, slot p ^ (c & 15).  MFMA
+    // m = 4i + d reads piece 4 (2i + h) + d = (8i + d) ^ 4h (bits apart), so
+    // its offset is this lane's base XOR a constant of m.
+    const uint32_t rb = (uint32_t)(c * kRowBytes + (((4 * h) ^ (c & 15)) << 4));
+
     const uint32_t xbase = lds_address(xring);
-    // The lane's scale bytes for chunk q start at byte srel + 8q of the copy.
+    // The scale bytes of chunk q of the lane's row start at byte srel + 8q of
+    // the copy; the lane's are those of blocks h, h+2, h+4, h+6.
     const uint32_t sbase = lds_address(lds8 + lay.scales);
-    const int srel = sshift + (row - f0) * nb + 4 * h;
+    const int srel = sshift + (row - f0) * nb + h;
 
     // Chunk q from ring slot / staging buffer s.  A block past nb is widened
     // from a zero word with scale 1: exact zeros.  The 16 MFMAs (m = 4i + d)
@@ -579,26 +586,33 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
         auto read_group = [&](int g, bf16x8 (&dst)[G][PL]) {
 #pragma unroll
             for (int j = 0; j < G; ++j) {
-                const uint32_t off = rbs ^ (uint32_t)((g * G + j) << 4);
+                const int mm = g * G + j;
+                const uint32_t off = rbs ^ (uint32_t)((((mm >> 2) << 3) | (mm & 3)) << 4);
 #pragma unroll
                 for (int p = 0; p < PL; ++p)
                     dst[j][p] = lds_read16(xbase + (uint32_t)((s * PL + p) * kPlaneBytes) + off);
             }
         };
-        // The four scale bytes (blocks 4h .. 4h+3): two aligned dwords and a
-        // byte shift, read ahead of the first B group.
+        // The lane's four scale bytes, every other byte of the seven from
+        // its first: three aligned dwords and a byte shift, read ahead of the
+        // first B group.  (Byte reads into 16-bit halves would save a
+        // register, but with SRAM ECC on, as on this part, a 16-bit load
+        // clears the other half.)
         const uint32_t sb0 = sbase + (uint32_t)(srel + 8 * q);
-        uint32_t slo = lds_read4(sb0 & ~3u), shi = lds_read4((sb0 & ~3u) + 4);
+        uint32_t slo = lds_read4(sb0 & ~3u), smid = lds_read4((sb0 & ~3u) + 4),
+                 shi = lds_read4((sb0 & ~3u) + 8);
         // Bit masks rather than selects, so no branch separates a load from
         // its use.
         uint32_t keep[4];
         float sc[4];
         auto scales = [&]() {
-            asm volatile("" : "+v"(slo), "+v"(shi));
-            const uint32_t sword = __builtin_amdgcn_alignbyte(shi, slo, sb0 & 3u);
+            asm volatile("" : "+v"(slo), "+v"(smid), "+v"(shi));
+            const uint32_t b03 = __builtin_amdgcn_alignbyte(smid, slo, sb0 & 3u);
+            const uint32_t b47 = __builtin_amdgcn_alignbyte(shi, smid, sb0 & 3u);
+            const uint32_t sword = __builtin_amdgcn_perm(b47, b03, 0x06040200u);   // bytes 0, 2, 4, 6
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                keep[i] = q * kKC + 4 * h + i < nb ? 0xFFFFFFFFu : 0u;
+                keep[i] = q * kKC + 2 * i + h < nb ? 0xFFFFFFFFu : 0u;
                 const uint32_t sb = (sword >> (8 * i)) & 0xFFu;
                 sc[i] = decode_scale(sb ^ ((sb ^ 127u) & ~keep[i]));
             }
@@ -621,7 +635,8 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
             scales();
 #pragma unroll
             for (int mm = 0; mm < 16; ++mm) {
-                bf16x8 raw = lds_read16(xbase + (uint32_t)(s * kPlaneBytes) + (rbs ^ (uint32_t)(mm << 4)));
+                bf16x8 raw = lds_read16(xbase + (uint32_t)(s * kPlaneBytes) +
+                                        (rbs ^ (uint32_t)((((mm >> 2) << 3) | (mm & 3)) << 4)));
                 lds_wait<0>();
                 asm volatile("" : "+v"(raw));
                 const uint4 rw = __builtin_bit_cast(uint4, raw);
@@ -721,10 +736,9 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
             xload(sn, q + D - 1);
             __builtin_amdgcn_sched_barrier(0);
             u32x4v w1[4];
-            const int base = q * kKC + 4 * h;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                w1[i] = *(g_u32x4v *)(wrow + (int64_t)min(base + i, nb - 1) * 16);
+                w1[i] = *(g_u32x4v *)(wrow + (int64_t)min(q * kKC + 2 * i + h, nb - 1) * 16);
             wait_vmcnt<0>();
             multiply(q, s_const, fb_const, w1);
             __builtin_amdgcn_sched_barrier(0);
