@@ -17,7 +17,11 @@ biases, plus the logits, activations and outputs, per token, divided by the
 wall time per token of the median timing round.  The timed steps run as the
 reference's protocol does (DequantGEMVBenchmark.swift:290-322): 7 rounds of
 --steps tokens each, every round bracketed by a device synchronisation, the
-median round reported beside the min and max.  The `roofline` object covers
+median round reported beside the min and max.  Each round's tokens are one
+captured graph (36 layer launches a token, each layer reading its token's
+logits where they lie in HBM), replayed once; `us_per_token_graph_per_token`
+is the same tokens run as one graph per token behind a copy of its logits.
+The `roofline` object covers
 the dominant kernel (decode_layer_kernel, the one-kernel MoE layer) timed
 with hipEvents on the library's stream; `sync_errors` counts the layer
 kernel's failed exchange waits (the run fails if there is any);
@@ -455,6 +459,39 @@ def timed_rounds(steps: int, run_step, sync, rounds: int = TIMING_ROUNDS):
     return per_step, time.perf_counter() - t0
 
 
+def round_graphs(gw, ctx, args, run_tokens, rounds: int = TIMING_ROUNDS):
+    """timed_rounds with each round's `args.steps` tokens captured as one graph
+    (run_tokens(first, n) enqueues tokens first .. first+n-1) and replayed
+    once, so the per-token cost holds no graph launch or input copy: warm-up
+    tokens 0 .. warmup-1 first (one graph) and one untimed replay of every
+    round's graph, then `rounds` timed rounds of args.steps tokens, each
+    bracketed by a device synchronisation.  Returns (per-token seconds of each
+    round, total seconds)."""
+    if args.warmup:
+        warm = gw.Graph.capture(ctx, run_tokens(0, args.warmup))
+        warm.launch()
+        ctx.synchronize()
+        warm.destroy()
+    graphs = [gw.Graph.capture(ctx, run_tokens(args.warmup + r * args.steps, args.steps))
+              for r in range(rounds)]
+    # every graph replayed once before timing (its first launch also moves it
+    # to the device); the replay recomputes everything, weights included
+    for g in graphs:
+        g.launch()
+    per_step = []
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for g in graphs:
+        tr = time.perf_counter()
+        g.launch()
+        ctx.synchronize()
+        per_step.append((time.perf_counter() - tr) / args.steps)
+    total = time.perf_counter() - t0
+    for g in graphs:
+        g.destroy()
+    return per_step, total
+
+
 def round_stats(per_step, scale: float) -> dict:
     """rounds / median / min / max of the per-step times, times `scale`."""
     v = sorted(x * scale for x in per_step)
@@ -661,6 +698,25 @@ def qwen3_bench(gw, args, batch: int) -> int:
                                  out_bf16=xs[l + 1].ptr,
                                  routing_ids=ids.address(l * batch * Kq * 4))
 
+    def run_tokens(first: int, n: int):
+        # steps first .. first+n-1, each layer reading its own logits in place
+        def run():
+            for i in range(first, first + n):
+                for l in range(Lq):
+                    runner.layer_forward(layers[l].ptr, lay.stride, Eq, Kq, xs[l].ptr, gw.BF16,
+                                         batch, outs[l].ptr,
+                                         logits=logits_all.address(i * step_logits +
+                                                                   l * batch * Eq * 4),
+                                         out_bf16=xs[l + 1].ptr,
+                                         routing_ids=ids.address(l * batch * Kq * 4))
+        return run
+
+    uniq = []
+    # one graph a round (as the GPT-OSS stack); then one graph a step behind a
+    # logits copy, reported beside it
+    per_step, elapsed = round_graphs(gw, ctx, args, run_tokens)
+    stats = round_stats(per_step, 1e6 / batch)
+    dt = stats["median"] * 1e-6 * batch
     graph = gw.Graph.capture(ctx, token)
 
     def step(i):
@@ -669,11 +725,8 @@ def qwen3_bench(gw, args, batch: int) -> int:
 
     for i in range(args.warmup):
         step(i)
-    uniq = []
-    per_step, elapsed = timed_rounds(args.steps, lambda j: step(args.warmup + j),
-                                     ctx.synchronize)
-    stats = round_stats(per_step, 1e6 / batch)
-    dt = stats["median"] * 1e-6 * batch
+    per_step_tok, _ = timed_rounds(args.steps, lambda j: step(args.warmup + j), ctx.synchronize)
+    stats_tok = round_stats(per_step_tok, 1e6 / batch)
     # distinct experts per layer, from the routing of the steps just timed
     lg = logits_all.download(np.float32, total * Lq * batch * Eq).reshape(total, Lq, batch, Eq)
     for i in range(args.warmup, total):
@@ -730,6 +783,7 @@ def qwen3_bench(gw, args, batch: int) -> int:
         "steps_per_round": args.steps,
         "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
         "us_per_token": round(dt * 1e6 / batch, 2), "hbm_frac_of_peak": round(value / PEAK_HBM_GBS, 4),
+        "us_per_token_graph_per_token": stats_tok["median"],
         "us_per_token_mean": round(elapsed / timed * 1e6 / batch, 2), "sync_errors": sync_err,
         **stats, "rounds_unit": "us/token",
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
@@ -986,6 +1040,27 @@ def main() -> int:
                                  out_bf16=xs[l + 1].ptr, routing_ids=ids.address(l * K * 4))
 
     step_logits = L * E * 4
+
+    def run_tokens(first: int, n: int):
+        # tokens first .. first+n-1, each layer reading its own logits in place
+        def run():
+            for i in range(first, first + n):
+                for l in range(L):
+                    runner.layer_forward(layers[l].ptr, lay.stride, E, K, xs[l].ptr, gw.BF16, 1,
+                                         outs[l].ptr,
+                                         logits=logits_all.address(i * step_logits + l * E * 4),
+                                         out_bf16=xs[l + 1].ptr,
+                                         routing_ids=ids.address(l * K * 4))
+        return run
+
+    # The timed rounds: each round's tokens captured as one graph (36 layer
+    # launches a token), replayed once per round.
+    per_step, elapsed = round_graphs(gw, ctx, args, run_tokens)
+    stats = round_stats(per_step, 1e6)
+    s_per_token = stats["median"] * 1e-6
+    # The same tokens as one graph per token, each behind a copy of its
+    # logits into a fixed buffer (how a serving loop without per-round
+    # capture would run them): reported beside the main figure.
     graph = gw.Graph.capture(ctx, token)
 
     def step(i: int):
@@ -994,10 +1069,8 @@ def main() -> int:
 
     for i in range(args.warmup):
         step(i)
-    per_step, elapsed = timed_rounds(args.steps, lambda j: step(args.warmup + j),
-                                     ctx.synchronize)
-    stats = round_stats(per_step, 1e6)
-    s_per_token = stats["median"] * 1e-6
+    per_step_tok, _ = timed_rounds(args.steps, lambda j: step(args.warmup + j), ctx.synchronize)
+    stats_tok = round_stats(per_step_tok, 1e6)
 
     # routing sanity: the last token's experts are distinct and in range
     last = ids.download(np.int32, L * K).reshape(L, K)
@@ -1005,9 +1078,11 @@ def main() -> int:
 
     bytes_token = L * (K * expert_bytes(lay) + E * 4 + H * 2 + H * 4 + H * 2)
     value = bytes_token / s_per_token / 1e9
-    log(f"{timed} tokens in {elapsed * 1e3:.2f} ms ({stats['rounds']} rounds): median "
-        f"{stats['median']:.1f} us/token (min {stats['min']:.1f}, max {stats['max']:.1f}), "
-        f"{value:.0f} GB/s ({value / PEAK_HBM_GBS * 100:.1f}% of {PEAK_HBM_GBS:.0f})")
+    log(f"{timed} tokens in {elapsed * 1e3:.2f} ms ({stats['rounds']} rounds, one graph a "
+        f"round): median {stats['median']:.1f} us/token (min {stats['min']:.1f}, max "
+        f"{stats['max']:.1f}), {value:.0f} GB/s ({value / PEAK_HBM_GBS * 100:.1f}% of "
+        f"{PEAK_HBM_GBS:.0f}); one graph a token behind a logits copy: "
+        f"{stats_tok['median']:.1f} us/token")
 
     roofline = None
     kernels = {}
@@ -1085,6 +1160,7 @@ def main() -> int:
         "ms_per_step": round(s_per_token * 1e3, 4),
         "us_per_token": round(s_per_token * 1e6, 2),
         "us_per_token_mean": round(elapsed / timed * 1e6, 2),
+        "us_per_token_graph_per_token": stats_tok["median"],
         "sync_errors": sync_err,
         **stats, "rounds_unit": "us/token",
         "hbm_frac_of_peak": round(value / PEAK_HBM_GBS, 4),
