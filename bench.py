@@ -724,19 +724,26 @@ def qwen3_bench(gw, args, batch: int) -> int:
     uniq = []
     # one graph a round (as the GPT-OSS stack); then one graph a step behind a
     # logits copy, reported beside it
-    per_step, elapsed = round_graphs(gw, ctx, args, run_tokens)
-    stats = round_stats(per_step, 1e6 / batch)
-    dt = stats["median"] * 1e-6 * batch
-    graph = gw.Graph.capture(ctx, token)
+    if not (args.token_graphs or args.eager):
+        per_step, elapsed = round_graphs(gw, ctx, args, run_tokens)
+    graph = None if args.eager else gw.Graph.capture(ctx, token)
 
     def step(i):
         ctx.copy_async(cur.ptr, logits_all.address(i * step_logits), step_logits)
-        graph.launch()
+        if args.eager:
+            token()
+        else:
+            graph.launch()
 
     for i in range(args.warmup):
         step(i)
-    per_step_tok, _ = timed_rounds(args.steps, lambda j: step(args.warmup + j), ctx.synchronize)
+    per_step_tok, elapsed_tok = timed_rounds(args.steps, lambda j: step(args.warmup + j),
+                                             ctx.synchronize)
     stats_tok = round_stats(per_step_tok, 1e6 / batch)
+    if args.token_graphs or args.eager:
+        per_step, elapsed = per_step_tok, elapsed_tok
+    stats = round_stats(per_step, 1e6 / batch)
+    dt = stats["median"] * 1e-6 * batch
     # distinct experts per layer, from the routing of the steps just timed
     lg = logits_all.download(np.float32, total * Lq * batch * Eq).reshape(total, Lq, batch, Eq)
     for i in range(args.warmup, total):
@@ -794,6 +801,8 @@ def qwen3_bench(gw, args, batch: int) -> int:
         "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
         "us_per_token": round(dt * 1e6 / batch, 2), "hbm_frac_of_peak": round(value / PEAK_HBM_GBS, 4),
         "us_per_token_graph_per_token": stats_tok["median"],
+        "timing": ("eager launches" if args.eager else "one graph per step" if args.token_graphs
+                   else "one graph per round"),
         "us_per_token_mean": round(elapsed / timed * 1e6 / batch, 2), "sync_errors": sync_err,
         **stats, "rounds_unit": "us/token",
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
@@ -978,6 +987,13 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bounded CPU-baseline sample (0 disables it)")
     ap.add_argument("--no-profile-pass", action="store_true")
+    ap.add_argument("--token-graphs", action="store_true",
+                    help="decode stacks: time one captured graph per token (behind a copy of "
+                         "its logits) instead of one graph per timing round")
+    ap.add_argument("--eager", action="store_true",
+                    help="decode stacks: as --token-graphs but each token's launches enqueued "
+                         "directly, no graph (for profiler runs: rocprofv3's kernel trace has "
+                         "crashed on the host inside graph launches of the batch-8 stack)")
     ap.add_argument("--counter-pass", type=int, default=0, metavar="MIB",
                     help="decode only: run --steps tokens eagerly (no graph, no events), then a "
                          "device-to-device copy of MIB MiB three times, and exit; the run "
@@ -1064,23 +1080,31 @@ def main() -> int:
         return run
 
     # The timed rounds: each round's tokens captured as one graph (36 layer
-    # launches a token), replayed once per round.
-    per_step, elapsed = round_graphs(gw, ctx, args, run_tokens)
-    stats = round_stats(per_step, 1e6)
-    s_per_token = stats["median"] * 1e-6
+    # launches a token), replayed once per round (--token-graphs: one graph
+    # per token, below, is the timing).
+    if not (args.token_graphs or args.eager):
+        per_step, elapsed = round_graphs(gw, ctx, args, run_tokens)
     # The same tokens as one graph per token, each behind a copy of its
     # logits into a fixed buffer (how a serving loop without per-round
     # capture would run them): reported beside the main figure.
-    graph = gw.Graph.capture(ctx, token)
+    graph = None if args.eager else gw.Graph.capture(ctx, token)
 
     def step(i: int):
         ctx.copy_async(cur_logits.ptr, logits_all.address(i * step_logits), step_logits)
-        graph.launch()
+        if args.eager:
+            token()
+        else:
+            graph.launch()
 
     for i in range(args.warmup):
         step(i)
-    per_step_tok, _ = timed_rounds(args.steps, lambda j: step(args.warmup + j), ctx.synchronize)
+    per_step_tok, elapsed_tok = timed_rounds(args.steps, lambda j: step(args.warmup + j),
+                                             ctx.synchronize)
     stats_tok = round_stats(per_step_tok, 1e6)
+    if args.token_graphs or args.eager:
+        per_step, elapsed = per_step_tok, elapsed_tok
+    stats = round_stats(per_step, 1e6)
+    s_per_token = stats["median"] * 1e-6
 
     # routing sanity: the last token's experts are distinct and in range
     last = ids.download(np.int32, L * K).reshape(L, K)
@@ -1089,7 +1113,8 @@ def main() -> int:
     bytes_token = L * (K * expert_bytes(lay) + E * 4 + H * 2 + H * 4 + H * 2)
     value = bytes_token / s_per_token / 1e9
     log(f"{timed} tokens in {elapsed * 1e3:.2f} ms ({stats['rounds']} rounds, one graph a "
-        f"round): median {stats['median']:.1f} us/token (min {stats['min']:.1f}, max "
+        f"{'token' if args.token_graphs or args.eager else 'round'}): median {stats['median']:.1f} us/token "
+        f"(min {stats['min']:.1f}, max "
         f"{stats['max']:.1f}), {value:.0f} GB/s ({value / PEAK_HBM_GBS * 100:.1f}% of "
         f"{PEAK_HBM_GBS:.0f}); one graph a token behind a logits copy: "
         f"{stats_tok['median']:.1f} us/token")
@@ -1171,6 +1196,8 @@ def main() -> int:
         "us_per_token": round(s_per_token * 1e6, 2),
         "us_per_token_mean": round(elapsed / timed * 1e6, 2),
         "us_per_token_graph_per_token": stats_tok["median"],
+        "timing": ("eager launches" if args.eager else "one graph per token" if args.token_graphs
+                   else "one graph per round"),
         "sync_errors": sync_err,
         **stats, "rounds_unit": "us/token",
         "hbm_frac_of_peak": round(value / PEAK_HBM_GBS, 4),
@@ -1190,7 +1217,8 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
-    graph.destroy()
+    if graph is not None:
+        graph.destroy()
     runner.close()
     ctx.close()
     if sync_err:
