@@ -80,7 +80,7 @@ COUNTER_LAYERS = L
 #   gate_up_kernel, GPT-OSS-120B layer, batch 1 (profiles/decode_gate_up_down_traffic.md)
 GATE_UP_TRAFFIC = (35_944_526, "gw_kernels.hip", None)
 #   prefill gate_up GEMM, 512 tokens, seed 1 (profiles/prefill_gemm_gptoss_512.md)
-PREFILL_GATE_UP_TRAFFIC = (1_246_497_507, "gw_prefill.hip", "7732687cd11af9af")
+PREFILL_GATE_UP_TRAFFIC = (1_248_605_362, "gw_prefill.hip", "38f5ec0c68d728b2")
 #   decode_layer_kernel (the one-kernel layer), GPT-OSS-120B, batch 1, over the
 #   whole 36-layer stack (profiles/decode_layer_traffic.md)
 DECODE_LAYER_TRAFFIC = (54_469_014, "gw_decode.hip", "723e1fa7217756e3")

@@ -38,7 +38,12 @@ SOURCES = ["gw_kernels.hip", "gw_decode.hip", "gw_prefill.hip", "gw_model.hip", 
 HOST_SOURCES = ["gw_host.cpp"]
 # Sources whose kernels must not spill vector registers (counted waits).
 NO_SPILL = {"gw_decode.hip", "gw_prefill.hip"}
-_REMARK = re.compile(r"remark: +(Function Name|VGPRs Spill|AGPRs Spill): (\S+)")
+_REMARK = re.compile(r"remark: +(Function Name|VGPRs Spill|AGPRs Spill|ScratchSize \[bytes/lane\]): (\S+)")
+# Stack bytes a NO_SPILL kernel may keep: a few bytes of an unused private
+# segment appear in some kernels; an array placed on the stack or a call to an
+# outlined function (whose frame holds its arguments) takes far more, and its
+# scratch loads and stores would sit among the counted waits.
+SCRATCH_LIMIT = 32
 
 
 def _without_remarks(out: str) -> str:
@@ -57,14 +62,17 @@ def _without_remarks(out: str) -> str:
 
 
 def spilled_kernels(report: str) -> list[str]:
-    """Kernels with a vector-register spill in a -Rpass-analysis=
-    kernel-resource-usage report (remarks in order: the kernel name, then its
-    figures)."""
+    """Kernels with a vector-register spill, or a stack frame above
+    SCRATCH_LIMIT bytes a lane, in a -Rpass-analysis=kernel-resource-usage
+    report (remarks in order: the kernel name, then its figures)."""
     bad, name = [], None
     for m in _REMARK.finditer(report):
         key, val = m.group(1), m.group(2)
         if key == "Function Name":
             name = val
+        elif key.startswith("ScratchSize"):
+            if int(val) > SCRATCH_LIMIT and name:
+                bad.append(f"{name} (stack {val} bytes a lane)")
         elif int(val) > 0 and name:
             bad.append(f"{name} ({key} {val})")
     return bad

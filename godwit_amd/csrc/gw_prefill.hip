@@ -335,6 +335,11 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
     constexpr bool F16IN = PL == 1 && !GATE_UP;
     // Loads a wave issues after a chunk's DMA until it waits for that DMA.
     constexpr int kYounger = kNW + (D - 2) * (kNX + kNW);
+    // Weight loads four lanes to a row with a pair swap (kSwap), or, in the
+    // 8-wave 2-deep shape held to 128 registers, two lanes to a row reading
+    // their own blocks (the swap's extra registers would spill there); the
+    // lane's blocks, and so every product and sum, are the same either way.
+    constexpr bool kSwap = !(W == 8 && D == 2);
     static_assert(D * PL * kPlaneBytes >= 2048, "the self-grouping lists must fit in the ring");
     // Dynamic LDS only (a static __shared__ variable would shift the dynamic
     // area off its alignment); layout in prefill_lds.
@@ -468,6 +473,13 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
     const int row = min(fbase + c, a.fdim - 1);       // clamped: rows past fdim are never stored
     const uint8_t *ex = a.experts_base + (int64_t)e * a.stride;
     const uint8_t *wrow = ex + a.blocks_off + (int64_t)row * nb * 16;
+    // The weight loads read the lane's row pair (rows c & ~1 and c | 1 of the
+    // tile, clamped like row): four lanes to a row per load; byte offsets of
+    // the two rows from the expert's blocks (an expert's section is far below
+    // 4 GiB).
+    const uint8_t *wbase = ex + a.blocks_off;
+    const uint32_t wrow0 = (uint32_t)min(fbase + (c & ~1), a.fdim - 1) * (uint32_t)(nb * 16);
+    const uint32_t wrow1 = (uint32_t)min(fbase + (c | 1), a.fdim - 1) * (uint32_t)(nb * 16);
 
     __syncthreads();                                  // ent[] is written
 
@@ -535,20 +547,42 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
         }
     };
 
-    // Weight ring: per chunk a lane's four 16-byte blocks 2i + h (load i
-    // reads 32 contiguous bytes of each of the wave's 32 rows; the fewer lines
-    // a load instruction touches, the fewer requests the texture path makes:
-    // blocks 4h + i, two pieces 64 bytes apart, took 11% longer at 512
-    // tokens).  Block indices past nb clamp to the row's last block.  The
-    // loaded words are used only when their chunk is multiplied (arithmetic
-    // on them here would wait for the load just issued).
+    // Weight ring: load 2j + t of a chunk reads, for row 2p + t of each of the
+    // tile's 16 row pairs (p = c >> 1), the 64 contiguous bytes of blocks 4j ..
+    // 4j+3: lane (h, c) block 4j + 2 (c & 1) + h.  The fewer lines a load
+    // instruction touches, the fewer requests the texture path makes.  A lane
+    // and its pair partner (lane ^ 1) then swap the blocks each read of the
+    // other's row (take_blocks), so that the lane holds blocks 2i + h of its
+    // own row.  Block indices past nb clamp to the row's last block.  The
+    // loaded words are used only when their chunk is multiplied (arithmetic on
+    // them here would wait for the load just issued).
     u32x4v wq[D][4];
     auto wload = [&](int slot, int q) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int bb = min(q * kKC + 2 * i + h, nb - 1);
-            wq[slot][i] = *(g_u32x4v *)(wrow + (int64_t)bb * 16);
+            if constexpr (kSwap) {
+                const int bb = min(q * kKC + 4 * (i >> 1) + 2 * (c & 1) + h, nb - 1);
+                wq[slot][i] = *(g_u32x4v *)(wbase + ((i & 1) ? wrow1 : wrow0) + (uint32_t)bb * 16u);
+            } else {
+                wq[slot][i] = *(g_u32x4v *)(wrow + (int64_t)min(q * kKC + 2 * i + h, nb - 1) * 16);
+            }
         }
+    };
+    // Dword d of block 2i + h of the lane's own row, from the chunk's loads
+    // as loaded: of the row pair's two loads of blocks 4j .. 4j+3 (j = i >> 1),
+    // the one of the lane's own row holds it for one parity of i, and for the
+    // other the partner (lane ^ 1) read it: a lane swap by DPP.  Taken where
+    // it is used, so no second copy of the chunk's words is held.
+    const bool odd_row = (c & 1) != 0;
+    auto wdw = [&](const u32x4v (&ld)[4], int i, int d) __attribute__((always_inline)) -> uint32_t {
+        if constexpr (!kSwap) return (uint32_t)ld[i][d];
+        const int jj = i >> 1;
+        if (i & 1) {
+            const uint32_t x0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)ld[2 * jj][d], 0xB1, 0xF, 0xF, true);
+            return odd_row ? (uint32_t)ld[2 * jj + 1][d] : x0;
+        }
+        const uint32_t x1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)ld[2 * jj + 1][d], 0xB1, 0xF, 0xF, true);
+        return odd_row ? x1 : (uint32_t)ld[2 * jj][d];
     };
 
     f32x16 acc, acc1;
@@ -577,7 +611,7 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
     constexpr int NG = 16 / G;
     // FB: the wave's scale bytes leave the fp16 range (F16IN only).  wsrc:
     // the chunk's weight words.
-    auto multiply = [&](int q, auto s_const, auto fb_const, const u32x4v (&wsrc)[4]) {
+    auto multiply = [&](int q, auto s_const, auto fb_const, const u32x4v (&wsrc)[4]) __attribute__((always_inline)) {
         constexpr int s = decltype(s_const)::value;
         constexpr bool FB = decltype(fb_const)::value;
         // Recomputed per chunk rather than kept in 16 registers per plane.
@@ -619,7 +653,7 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
         };
         auto widen_bf16 = [&](int mm) {
             const int i = mm >> 2, d = mm & 3;
-            const uint32_t w = wsrc[i][d] & keep[i];
+            const uint32_t w = wdw(wsrc, i, d) & keep[i];
             return __builtin_bit_cast(bf16x8, make_uint4(
                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 0)),
                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[i], 1)),
@@ -676,7 +710,7 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
 #pragma unroll
                 for (int j = 0; j < G; ++j) {
                     const int mm = g * G + j, i = mm >> 2, d = mm & 3;
-                    const uint32_t w = wsrc[i][d] & keep[i];
+                    const uint32_t w = wdw(wsrc, i, d) & keep[i];
                     A16[j] = __builtin_bit_cast(f16x8, make_uint4(
                         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc[i], 0)),
                         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc[i], 1)),
@@ -724,7 +758,7 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
     // waves (after which every row of chunk q+1 is in LDS and nobody reads
     // chunk q's buffer any more).
     const int nq = (nb + kKC - 1) / kKC;
-    auto step = [&](int q, auto s_const, auto fb_const, auto guard_const) {
+    auto step = [&](int q, auto s_const, auto fb_const, auto guard_const) __attribute__((always_inline)) {
         constexpr int s = decltype(s_const)::value;
         constexpr int sn = (s + D - 1) % D;
         if constexpr (decltype(guard_const)::value)
@@ -738,7 +772,9 @@ __global__ __launch_bounds__(64 * W, W == 8 && D == 2 ? 4 : W == 4 ? 3 : 1) void
             u32x4v w1[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                w1[i] = *(g_u32x4v *)(wrow + (int64_t)min(q * kKC + 2 * i + h, nb - 1) * 16);
+                w1[i] = kSwap ? *(g_u32x4v *)(wbase + ((i & 1) ? wrow1 : wrow0) +
+                                              (uint32_t)min(q * kKC + 4 * (i >> 1) + 2 * (c & 1) + h, nb - 1) * 16u)
+                              : *(g_u32x4v *)(wrow + (int64_t)min(q * kKC + 2 * i + h, nb - 1) * 16);
             wait_vmcnt<0>();
             multiply(q, s_const, fb_const, w1);
             __builtin_amdgcn_sched_barrier(0);

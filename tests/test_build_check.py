@@ -65,3 +65,16 @@ def test_spill_check_fails_without_kernel_records():
     for text in ("", "gw_prefill.hip:40:9: warning: unused variable 'x' [-Wunused-variable]\n"):
         problems = gwbuild.spill_check(text)
         assert len(problems) == 1 and "no kernel-resource-usage records" in problems[0]
+
+
+def test_spilled_kernels_flags_stack_frames():
+    """A kernel whose stack frame is larger than a few bytes (an array the
+    compiler could not keep in registers, or a call to an outlined function)
+    is flagged like a spill; a small unused private segment is not."""
+    report = REPORT.replace("VGPRs Spill: 56", "VGPRs Spill: 0").replace("AGPRs Spill: 3", "AGPRs Spill: 0")
+    big = report.replace("ScratchSize [bytes/lane]: 0", "ScratchSize [bytes/lane]: 1152")
+    assert gwbuild.spilled_kernels(big) == [
+        "_ZN2gw19prefill_gemm_kernelILi1ELb1ELi8ELi2ELb0EEEvNS_8GemmArgsE (stack 1152 bytes a lane)"]
+    small = report.replace("ScratchSize [bytes/lane]: 0", "ScratchSize [bytes/lane]: 20")
+    assert gwbuild.spilled_kernels(small) == []
+
