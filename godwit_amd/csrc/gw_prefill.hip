@@ -86,12 +86,14 @@ __global__ __launch_bounds__(256) void prefill_route_kernel(const float *__restr
 // from LDS atomics: each entry's results depend only on its own token row, so
 // the order inside a group never changes a value.  The expert offsets and the
 // tile list come from one exclusive scan over the experts (waves 0..3 hold
-// one expert per lane).  Small batches (T <= kRouteGroupTokens) are routed in
-// the same workgroup first, one wave per token, and skip the route kernel.
+// one expert per lane).  Batches of at most kRouteGroupTokens tokens (one
+// per wave) are routed in the same workgroup first and skip the route kernel
+// (batches above the GEMMs' own grouping reach this only when that grouping
+// is lowered); with two tokens a wave the route kernel in front was faster.
 // ---------------------------------------------------------------------------
 
 constexpr int kGroupThreads = 1024;
-constexpr int kRouteGroupTokens = 32;
+constexpr int kRouteGroupTokens = 16;
 constexpr int kRouteGroupEntries = kRouteGroupTokens * kMaxTopK;
 
 __global__ __launch_bounds__(kGroupThreads) void prefill_group_kernel(
