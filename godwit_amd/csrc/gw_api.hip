@@ -704,10 +704,12 @@ extern "C" int gw_expert_runner_create(gw_context *ctx, int64_t hidden_size,
     ctx->runners.push_back(r);
     const int pa = get_env_int("GODWIT_PREFILL_ABOVE", 1);
     r->prefill_above = pa < 1 ? 1 : pa > gw::kMaxTokens ? gw::kMaxTokens : pa;
-    // 16: at 32 tokens the selection in every gate_up workgroup (three rounds
-    // of workgroups per CU) costs more than the group kernel (Qwen3: 5478
-    // against 5006 us per step); at 16 the two tie, at 8 self-grouping wins.
-    const int sg = get_env_int("GODWIT_SELF_GROUP_TOKENS", 16);
+    // 12: Qwen3 per token, self-grouped against the route and group kernels
+    // in front: 296.1 / 305.3 us at 10 tokens, 273.7 / 277.1 at 12, 283.0 /
+    // 237.7 at 14, 255.1 / 214.3 at 16, 257.2 / 208.8 at 17 (the selection
+    // in every gate_up workgroup grows with the batch; the kernels in front
+    // cost a fixed ~9 us a layer).
+    const int sg = get_env_int("GODWIT_SELF_GROUP_TOKENS", 12);
     r->self_group_max = sg < 0 ? 0 : sg > 32 ? 32 : sg;
     const int fc = get_env_int("GODWIT_FUSED_COMBINE_TOKENS", 32);
     r->fused_combine_max = fc < 0 ? 0 : fc;

@@ -261,10 +261,10 @@ int gw_expert_apply_assignments_async(gw_expert_runner *runner, const void *inpu
  * 2..8 tokens (more than GODWIT_PREFILL_ABOVE at runner creation, default 1)
  * when hidden and intermediate sizes are multiples of 32 and >= 128, x is
  * 16-byte aligned, there are at most 256 experts and, during graph capture,
- * the prefill scratch is already reserved.  Batches of up to 16 tokens are
+ * the prefill scratch is already reserved.  Batches of up to 12 tokens are
  * routed and grouped inside the grouped GEMMs themselves (every expert then
  * holds at most one 32-entry tile); GODWIT_SELF_GROUP_TOKENS at runner
- * creation (0..32, default 16) sets that bound, larger batches use the
+ * creation (0..32, default 12) sets that bound, larger batches use the
  * group kernel's tile list.  Up to GODWIT_FUSED_COMBINE_TOKENS tokens (default
  * 32, 0 disables) the weighted combine runs inside the down GEMM instead of
  * a kernel of its own; results are the same bytes either way.  Enqueue only. */

@@ -193,7 +193,7 @@ def test_prefill_router_and_graph_replay(ctx):
     (GPTOSS, 12, 4, 20, gw.F32, 4),      # three planes, 2880-wide K
     (SMALL, 64, 4, 2, gw.BF16, 5),       # the smallest grouped batch
     (SMALL, 1, 1, 5, gw.BF16, 6),        # one expert: a one-bit mask, every entry in one tile
-    (SMALL, 256, 8, 16, gw.F16, 7),      # the default bound: 16 tokens over 256 experts
+    (SMALL, 256, 8, 16, gw.F16, 7),      # 16 tokens over 256 experts
 ], ids=["qwen3-t8", "small-e8-t32", "small-e256-t32", "gptoss-f32-t20", "small-t2",
         "small-e1-t5", "small-e256-t16"])
 def test_self_grouped_equals_tile_list(ctx, monkeypatch, shape, E, K, T, x_dtype, seed):
